@@ -1,0 +1,134 @@
+/*
+ * qe.h -- C ABI of the MI355X-native Qwen3 batch-1 decode engine (libqe.so).
+ *
+ * The engine API of the reference's Rust crate, flattened to plain C so that a Rust `-sys`
+ * crate (or ctypes, or C++) can bind it without any GPU types in the signatures. Every entry
+ * point returns an int status (QE_OK == 0) and never aborts; qe_last_error() gives the message
+ * of the last failure on the calling thread. A model handle and the caches made from it are
+ * single-threaded: calls on one model must not overlap (the reference's MetalModel shares its
+ * scratch buffers the same way, metal_inference.rs:85-98).
+ *
+ * Reference interfaces replaced (paths relative to the reference root):
+ *   metal_infrence_engine/src/cpu_inference.rs, metal_infrence_engine/src/metal_inference.rs,
+ *   metal_infrence_engine/src/bin/bench.rs, metal_infrence_engine/tests/read_bandwidth.rs.
+ */
+#ifndef QE_H
+#define QE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* status codes */
+#define QE_OK 0
+#define QE_ERR_IO 1          /* file missing or unreadable (io::Error in the reference) */
+#define QE_ERR_FORMAT 2      /* bad safetensors header / config.json / alignment */
+#define QE_ERR_TENSOR 3      /* missing tensor, non-BF16 dtype, or shape mismatch */
+#define QE_ERR_POS 4         /* pos >= max_seq, or pos beyond the cached length */
+#define QE_ERR_ARG 5         /* invalid argument (null pointer, token >= vocab, ...) */
+#define QE_ERR_UNSUPPORTED 6 /* a shape the kernels do not handle (head_dim != 128, ...) */
+#define QE_ERR_HIP 7         /* a HIP runtime call failed */
+#define QE_ERR_NO_DEVICE 8   /* no usable gfx950 device */
+#define QE_ERR_KERNEL 9      /* a kernel reported a failure through its error word */
+
+/* KV cache element types */
+#define QE_KV_F32 0
+#define QE_KV_BF16 1
+
+/* Subset of config.json the forward pass reads. Replaces `Config`, cpu_inference.rs:20-33. */
+typedef struct qe_config {
+  uint64_t hidden_size;
+  uint64_t intermediate_size;
+  uint64_t num_hidden_layers;
+  uint64_t num_attention_heads;
+  uint64_t num_key_value_heads;
+  uint64_t head_dim;
+  uint64_t vocab_size;
+  float rms_norm_eps;
+  float rope_theta;
+  uint32_t eos_token_id;
+} qe_config;
+
+typedef struct qe_model qe_model;
+typedef struct qe_kv qe_kv;
+
+/* Called once per finished decode step with that step's greedy token, in order. */
+typedef void (*qe_on_token)(void* user, uint32_t token);
+
+/* Message of the last failed call on this thread ("" if none). Valid until the next call. */
+const char* qe_last_error(void);
+
+/* ---- model: MetalModel::load_model (metal_inference.rs:157-168), which reads the file with
+ *      Model::load_model (cpu_inference.rs:58-84) and the sibling config.json. Weights are
+ *      copied once into a device arena on the current HIP device. ---- */
+int qe_model_load(const char* safetensors_path, qe_model** out);
+void qe_model_free(qe_model* model);
+/* MetalModel::config (metal_inference.rs:170) */
+int qe_model_config(const qe_model* model, qe_config* out);
+/* bench.rs:106-116 (tests/mbu.rs:19-30): every tensor's bytes except the embedding table,
+ * plus one embedding row */
+uint64_t qe_weight_bytes_per_token(const qe_model* model);
+/* bench.rs:118-119: K and V bytes read at position pos (f32 as in the reference; bf16 halves) */
+uint64_t qe_kv_bytes_at(const qe_model* model, uint64_t pos, int kv_dtype);
+
+/* ---- KV cache: MetalKVCache::new (metal_inference.rs:129-137). One cache per sequence,
+ *      tied to the model it was made from; holds the RoPE table for max_seq positions. ---- */
+int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out);
+void qe_kv_free(qe_kv* kv);
+uint64_t qe_kv_max_seq(const qe_kv* kv);
+/* positions cached so far (the next forward must use pos <= this) */
+uint64_t qe_kv_len(const qe_kv* kv);
+
+/* ---- one token: MetalModel::forward (metal_inference.rs:284-291) == Model::forward
+ *      (cpu_inference.rs:98-179). Runs `token` at `pos`, writes its K/V into the cache and
+ *      returns the vocab_size logits in logits_out (host memory). Requires pos < max_seq and
+ *      pos <= qe_kv_len(kv); afterwards qe_kv_len(kv) == pos + 1. ---- */
+int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* logits_out);
+
+/* ---- prefill: the prompt loop of bench.rs:174-176 (one forward per token). Writes the last
+ *      position's logits to last_logits (nullable). ---- */
+int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv,
+               float* last_logits);
+
+/* ---- greedy decode: MetalModel::decode (metal_inference.rs:293-316). `first` goes in at
+ *      start_pos; each step's GPU argmax (lowest index on ties, main.rs:37-42) feeds the next
+ *      step on the device. on_token (nullable) is called with each step's token as the step
+ *      finishes. If logits_per_step is not NULL it receives steps*vocab_size floats (slower:
+ *      one device-to-host copy per step; meant for parity tests). ---- */
+int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv,
+              qe_on_token on_token, void* user, float* logits_per_step);
+
+/* ---- synthetic inputs (the reference loads a real checkpoint; this build writes a seeded
+ *      random-init one with the same tensor names, shapes and file format) ---- */
+/* Writes <dir>/model.safetensors and <dir>/config.json: every matrix bf16 ~ N(0, 0.02) from
+ * `seed`, norm gains 1.0, lm_head.weight a byte copy of model.embed_tokens.weight. */
+int qe_write_random_checkpoint(const char* dir, uint64_t seed, const qe_config* cfg);
+/* n token ids uniform in [0, vocab) from `seed` */
+void qe_random_prompt(uint64_t seed, uint64_t n, uint32_t vocab, uint32_t* out);
+
+/* ---- isolated device ops on caller-owned device memory (HIP device pointers; stream may be
+ *      NULL for the default stream). For the isolated benchmarks and kernel parity tests. ---- */
+/* out[r] = sum_c bf16(w[r*cols + c]) * x[c], f32 accumulate; matvec_bf16,
+ * inference.metal:143-186 / cpu_inference.rs:225-257. cols % 8 == 0, w 16-byte aligned. */
+int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, uint64_t cols,
+                      void* stream);
+/* One decode step of GQA attention (cpu_inference.rs:144-162, inference.metal:234-296) for
+ * head_dim 128: q [n_heads*128] (post q-norm and RoPE), k/v caches laid out
+ * [n_kv_heads][kv_stride][128] f32, attending positions 0..n_pos-1; out [n_heads*128].
+ * n_splits == 0 picks the split-K count from n_pos; 1 forces the single-pass kernel. `work`
+ * must hold qe_op_attention_work_bytes(...) bytes of device memory. */
+uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint64_t n_pos);
+int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
+                    uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,
+                    void* work, void* stream);
+/* Streaming read of n floats (n % 4 == 0): the read_sum kernel of tests/read_bandwidth.rs:16-54,
+ * writing one partial sum per block to partial[grid]. grid == 0 picks a default. */
+int qe_op_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,620 @@
+// Host engine behind the C ABI of include/qe.h: device weight arena, per-sequence KV cache with
+// its RoPE table and step state, one decode step captured as a hipGraph per cache and replayed.
+//
+// Reference: metal_infrence_engine/src/metal_inference.rs (MetalModel, MetalKVCache, forward,
+// decode, commit_step) and cpu_inference.rs (the loader contract and the byte formula).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/qe.h"
+#include "checkpoint.h"
+#include "kernels.h"
+
+using qe::ArgCand;
+using qe::AttnParams;
+using qe::MatvecParams;
+using qe::StepState;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[1024];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                       \
+  do {                                                                                      \
+    hipError_t e_ = (expr);                                                                 \
+    if (e_ != hipSuccess) return fail(QE_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(e_)); \
+  } while (0)
+
+struct Layer {
+  const uint16_t* w_in;    // input_layernorm [H]
+  const uint16_t* w_qkv;   // q_proj | k_proj | v_proj rows, [QD + 2 KD][H]
+  const uint16_t* q_norm;  // [D]
+  const uint16_t* k_norm;  // [D]
+  const uint16_t* w_o;     // [H][QD]
+  const uint16_t* w_post;  // post_attention_layernorm [H]
+  const uint16_t* w_gu;    // gate/up rows interleaved: row 2i = gate_i, row 2i+1 = up_i, [2I][H]
+  const uint16_t* w_down;  // [H][I]
+};
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+}  // namespace
+
+struct qe_model {
+  qe::Checkpoint ckpt;
+  qe_config cfg{};
+  int device = 0;
+  hipStream_t stream = nullptr;
+  uint8_t* arena = nullptr;
+  size_t arena_bytes = 0;
+  const uint16_t* embed = nullptr;
+  const uint16_t* lm_head = nullptr;
+  const uint16_t* final_norm = nullptr;
+  std::vector<Layer> layers;
+  // activations
+  float* x = nullptr;
+  float* qkv = nullptr;
+  float* att = nullptr;
+  float* h = nullptr;
+  float* logits = nullptr;
+  ArgCand* cand = nullptr;
+  uint32_t n_cand = 0;
+  float* attn_part = nullptr;
+  uint32_t* attn_cnt = nullptr;
+  uint32_t* err = nullptr;  // device error word
+  uint8_t* scratch = nullptr;
+  // pinned host staging
+  float* h_logits = nullptr;
+  uint32_t* h_small = nullptr;  // [0..3] state staging, [4] error word
+  uint64_t weight_bytes = 0;
+
+  ~qe_model() {  // teardown errors have nowhere to go; the handle is gone either way
+    if (stream) (void)hipStreamSynchronize(stream);
+    if (arena) (void)hipFree(arena);
+    if (scratch) (void)hipFree(scratch);
+    if (h_logits) (void)hipHostFree(h_logits);
+    if (h_small) (void)hipHostFree(h_small);
+    if (stream) (void)hipStreamDestroy(stream);
+  }
+};
+
+struct qe_kv {
+  qe_model* model = nullptr;
+  uint64_t max_seq = 0;
+  int dtype = QE_KV_F32;
+  uint8_t* mem = nullptr;  // K, V, rope table, state, token ring
+  void* k = nullptr;       // [L][n_kv][max_seq][D]
+  void* v = nullptr;
+  float* rope = nullptr;   // [max_seq][D/2][2]
+  StepState* state = nullptr;
+  uint32_t* tokens = nullptr;       // device token ring [tok_cap]
+  uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
+  uint32_t tok_cap = 0;
+  uint32_t attn_splits = 1;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<hipEvent_t> events;
+  uint64_t len = 0;
+
+  ~qe_kv() {
+    if (model && model->stream) (void)hipStreamSynchronize(model->stream);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (auto e : events) (void)hipEventDestroy(e);
+    if (mem) (void)hipFree(mem);
+    if (host_tokens) (void)hipHostFree(host_tokens);
+  }
+};
+
+namespace {
+
+int check_device(int& dev) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(QE_ERR_NO_DEVICE, "no HIP device is visible");
+  HIP_TRY(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  HIP_TRY(hipGetDeviceProperties(&prop, dev));
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+    return fail(QE_ERR_NO_DEVICE, "device %d is %s; this build targets gfx950 (MI355X)", dev, prop.gcnArchName);
+  return QE_OK;
+}
+
+int validate_config(const qe_config& c) {
+  if (c.head_dim != qe::kHeadDim) return fail(QE_ERR_UNSUPPORTED, "head_dim %llu: the kernels need 128", (unsigned long long)c.head_dim);
+  if (!c.num_key_value_heads || c.num_attention_heads % c.num_key_value_heads)
+    return fail(QE_ERR_UNSUPPORTED, "num_attention_heads must be a multiple of num_key_value_heads");
+  uint64_t g = c.num_attention_heads / c.num_key_value_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 8) return fail(QE_ERR_UNSUPPORTED, "q heads per KV head must be 1, 2, 4 or 8");
+  const uint64_t H = c.hidden_size, I = c.intermediate_size, QD = c.num_attention_heads * c.head_dim;
+  if (!H || !I || !c.num_hidden_layers || !c.vocab_size) return fail(QE_ERR_UNSUPPORTED, "zero dimension in config");
+  if (H % 8 || I % 8 || QD % 8) return fail(QE_ERR_UNSUPPORTED, "hidden/intermediate/q sizes must be multiples of 8");
+  if (H > 4096 || I > 4096 || QD > 4096) return fail(QE_ERR_UNSUPPORTED, "matvec input widths above 4096 are not supported");
+  if (c.vocab_size >= 0xFFFFFFFFull) return fail(QE_ERR_UNSUPPORTED, "vocab too large");
+  return QE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qe_last_error(void) { return g_err.c_str(); }
+
+int qe_model_load(const char* path, qe_model** out) {
+  if (!path || !out) return fail(QE_ERR_ARG, "null argument");
+  *out = nullptr;
+  std::unique_ptr<qe_model> m(new qe_model());
+  std::string err;
+  int rc = m->ckpt.open(path, err);
+  if (rc != QE_OK) return fail(rc, "%s", err.c_str());
+  m->cfg = m->ckpt.config();
+  const qe_config& c = m->cfg;
+  const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
+  const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
+
+  // resolve every tensor on the host first, so a bad file fails before any device work
+  struct Src { const uint16_t* p; uint64_t n; };
+  auto get = [&](const std::string& name, uint64_t numel, Src& s) -> bool {
+    s.p = m->ckpt.bf16(name, numel, err);
+    s.n = numel;
+    return s.p != nullptr;
+  };
+  Src embed, lm, fnorm;
+  if (!get("model.embed_tokens.weight", V * H, embed) || !get("lm_head.weight", V * H, lm) ||
+      !get("model.norm.weight", H, fnorm))
+    return fail(QE_ERR_TENSOR, "%s", err.c_str());
+  struct LSrc { Src in, q, k, v, qn, kn, o, post, g, u, d; };
+  std::vector<LSrc> ls(L);
+  for (uint64_t l = 0; l < L; l++) {
+    LSrc& s = ls[l];
+    if (!get(qe::layer_tensor(l, "input_layernorm.weight"), H, s.in) ||
+        !get(qe::layer_tensor(l, "self_attn.q_proj.weight"), QD * H, s.q) ||
+        !get(qe::layer_tensor(l, "self_attn.k_proj.weight"), KD * H, s.k) ||
+        !get(qe::layer_tensor(l, "self_attn.v_proj.weight"), KD * H, s.v) ||
+        !get(qe::layer_tensor(l, "self_attn.q_norm.weight"), D, s.qn) ||
+        !get(qe::layer_tensor(l, "self_attn.k_norm.weight"), D, s.kn) ||
+        !get(qe::layer_tensor(l, "self_attn.o_proj.weight"), H * QD, s.o) ||
+        !get(qe::layer_tensor(l, "post_attention_layernorm.weight"), H, s.post) ||
+        !get(qe::layer_tensor(l, "mlp.gate_proj.weight"), I * H, s.g) ||
+        !get(qe::layer_tensor(l, "mlp.up_proj.weight"), I * H, s.u) ||
+        !get(qe::layer_tensor(l, "mlp.down_proj.weight"), H * I, s.d))
+      return fail(QE_ERR_TENSOR, "%s", err.c_str());
+  }
+  if ((rc = validate_config(c)) != QE_OK) return rc;
+  if ((rc = check_device(m->device)) != QE_OK) return rc;
+  m->weight_bytes = m->ckpt.weight_bytes_per_token();
+
+  // arena layout (256-byte aligned tensors)
+  size_t off = 0;
+  auto take = [&](uint64_t elems) { size_t o = off; off = align_up(off + elems * 2, 256); return o; };
+  const size_t o_embed = take(V * H), o_lm = take(V * H), o_fnorm = take(H);
+  struct LOff { size_t in, qkv, qn, kn, o, post, gu, d; };
+  std::vector<LOff> lo(L);
+  for (uint64_t l = 0; l < L; l++) {
+    lo[l].in = take(H);
+    lo[l].qkv = take((QD + 2 * KD) * H);
+    lo[l].qn = take(D);
+    lo[l].kn = take(D);
+    lo[l].o = take(H * QD);
+    lo[l].post = take(H);
+    lo[l].gu = take(2 * I * H);
+    lo[l].d = take(H * I);
+  }
+  m->arena_bytes = off;
+  HIP_TRY(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  HIP_TRY(hipMalloc(&m->arena, m->arena_bytes));
+
+  // upload through a pinned staging buffer; relayout q|k|v and gate/up on the host
+  const size_t stage_bytes = size_t(64) << 20;
+  uint8_t* stage = nullptr;
+  HIP_TRY(hipHostMalloc(&stage, stage_bytes, hipHostMallocDefault));
+  auto upload = [&](size_t dst_off, const void* src, size_t bytes) -> int {
+    const uint8_t* s = static_cast<const uint8_t*>(src);
+    for (size_t done = 0; done < bytes; done += stage_bytes) {
+      size_t n = std::min(stage_bytes, bytes - done);
+      memcpy(stage, s + done, n);
+      hipError_t e = hipMemcpyAsync(m->arena + dst_off + done, stage, n, hipMemcpyHostToDevice, m->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+      if (e != hipSuccess) return fail(QE_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    return QE_OK;
+  };
+  auto upload_rows_interleaved = [&](size_t dst_off, const uint16_t* a, const uint16_t* b, uint64_t rows, uint64_t cols) -> int {
+    // row 2i <- a[i], row 2i+1 <- b[i]
+    const uint64_t row_bytes = cols * 2;
+    const uint64_t rows_per = std::max<uint64_t>(1, stage_bytes / (2 * row_bytes));
+    for (uint64_t r0 = 0; r0 < rows; r0 += rows_per) {
+      uint64_t nr = std::min(rows_per, rows - r0);
+      for (uint64_t i = 0; i < nr; i++) {
+        memcpy(stage + (2 * i) * row_bytes, a + (r0 + i) * cols, row_bytes);
+        memcpy(stage + (2 * i + 1) * row_bytes, b + (r0 + i) * cols, row_bytes);
+      }
+      hipError_t e = hipMemcpyAsync(m->arena + dst_off + 2 * r0 * row_bytes, stage, 2 * nr * row_bytes, hipMemcpyHostToDevice, m->stream);
+      if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+      if (e != hipSuccess) return fail(QE_ERR_HIP, "weight upload failed: %s", hipGetErrorString(e));
+    }
+    return QE_OK;
+  };
+  rc = upload(o_embed, embed.p, V * H * 2);
+  if (rc == QE_OK) rc = upload(o_lm, lm.p, V * H * 2);
+  if (rc == QE_OK) rc = upload(o_fnorm, fnorm.p, H * 2);
+  for (uint64_t l = 0; l < L && rc == QE_OK; l++) {
+    const LSrc& s = ls[l];
+    rc = upload(lo[l].in, s.in.p, H * 2);
+    if (rc == QE_OK) rc = upload(lo[l].qkv, s.q.p, QD * H * 2);
+    if (rc == QE_OK) rc = upload(lo[l].qkv + QD * H * 2, s.k.p, KD * H * 2);
+    if (rc == QE_OK) rc = upload(lo[l].qkv + (QD + KD) * H * 2, s.v.p, KD * H * 2);
+    if (rc == QE_OK) rc = upload(lo[l].qn, s.qn.p, D * 2);
+    if (rc == QE_OK) rc = upload(lo[l].kn, s.kn.p, D * 2);
+    if (rc == QE_OK) rc = upload(lo[l].o, s.o.p, H * QD * 2);
+    if (rc == QE_OK) rc = upload(lo[l].post, s.post.p, H * 2);
+    if (rc == QE_OK) rc = upload_rows_interleaved(lo[l].gu, s.g.p, s.u.p, I, H);
+    if (rc == QE_OK) rc = upload(lo[l].d, s.d.p, H * I * 2);
+  }
+  (void)hipHostFree(stage);
+  if (rc != QE_OK) return rc;
+
+  auto at = [&](size_t o) { return reinterpret_cast<const uint16_t*>(m->arena + o); };
+  m->embed = at(o_embed);
+  m->lm_head = at(o_lm);
+  m->final_norm = at(o_fnorm);
+  m->layers.resize(L);
+  for (uint64_t l = 0; l < L; l++)
+    m->layers[l] = Layer{at(lo[l].in), at(lo[l].qkv), at(lo[l].qn), at(lo[l].kn),
+                         at(lo[l].o), at(lo[l].post), at(lo[l].gu), at(lo[l].d)};
+
+  // activations and reduction scratch
+  const uint32_t G = uint32_t(c.num_attention_heads / c.num_key_value_heads);
+  m->n_cand = qe::matvec_num_blocks(uint32_t(V), uint32_t(H), qe::kLogits);
+  size_t so = 0;
+  auto stake = [&](size_t bytes) { size_t o = so; so = align_up(so + bytes, 256); return o; };
+  const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
+               s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
+               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxSplits * G * (2 + D) * 4),
+               s_cnt = stake(c.num_key_value_heads * 4), s_err = stake(4);
+  HIP_TRY(hipMalloc(&m->scratch, so));
+  HIP_TRY(hipMemset(m->scratch, 0, so));
+  m->x = reinterpret_cast<float*>(m->scratch + s_x);
+  m->qkv = reinterpret_cast<float*>(m->scratch + s_qkv);
+  m->att = reinterpret_cast<float*>(m->scratch + s_att);
+  m->h = reinterpret_cast<float*>(m->scratch + s_h);
+  m->logits = reinterpret_cast<float*>(m->scratch + s_logits);
+  m->cand = reinterpret_cast<ArgCand*>(m->scratch + s_cand);
+  m->attn_part = reinterpret_cast<float*>(m->scratch + s_part);
+  m->attn_cnt = reinterpret_cast<uint32_t*>(m->scratch + s_cnt);
+  m->err = reinterpret_cast<uint32_t*>(m->scratch + s_err);
+  HIP_TRY(hipHostMalloc(&m->h_logits, V * 4, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(&m->h_small, 64, hipHostMallocDefault));
+  *out = m.release();
+  return QE_OK;
+}
+
+void qe_model_free(qe_model* model) { delete model; }
+
+int qe_model_config(const qe_model* model, qe_config* out) {
+  if (!model || !out) return fail(QE_ERR_ARG, "null argument");
+  *out = model->cfg;
+  return QE_OK;
+}
+
+uint64_t qe_weight_bytes_per_token(const qe_model* model) { return model ? model->weight_bytes : 0; }
+
+uint64_t qe_kv_bytes_at(const qe_model* model, uint64_t pos, int kv_dtype) {
+  if (!model) return 0;
+  const qe_config& c = model->cfg;
+  const uint64_t el = kv_dtype == QE_KV_BF16 ? 2 : 4;
+  return 2 * c.num_hidden_layers * (pos + 1) * c.num_key_value_heads * c.head_dim * el;
+}
+
+}  // extern "C"
+
+namespace {
+
+// Enqueue one decode step (reads tokens[tok_idx] at state.pos) on the model stream.
+int enqueue_step(qe_model* m, qe_kv* kv) {
+  const qe_config& c = m->cfg;
+  const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
+  const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
+  const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
+  const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
+  hipStream_t s = m->stream;
+  HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
+  for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
+    const Layer& w = m->layers[l];
+    MatvecParams p{};
+    p.eps = c.rms_norm_eps;
+    // input_layernorm + q|k|v projections (cpu_inference.rs:129-132)
+    p.w = w.w_qkv; p.x = m->x; p.nw = w.w_in; p.rows = QD + 2 * KD; p.cols = H; p.out = m->qkv;
+    HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kStore, s));
+    // q/k norm + RoPE, K/V append, attention (cpu_inference.rs:134-162)
+    AttnParams a{};
+    a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
+    a.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
+    a.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
+    a.partial = m->attn_part; a.counter = m->attn_cnt; a.att = m->att; a.state = kv->state; a.err = m->err;
+    a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
+    a.max_seq = uint32_t(kv->max_seq); a.eps = c.rms_norm_eps; a.scale = 1.0f / sqrtf(float(D));
+    a.kv_bf16 = kv->dtype == QE_KV_BF16; a.norm_rope = 1;
+    HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
+    // o_proj + residual (cpu_inference.rs:163-164)
+    p = MatvecParams{};
+    p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
+    HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+    // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
+    p = MatvecParams{};
+    p.eps = c.rms_norm_eps;
+    p.w = w.w_gu; p.x = m->x; p.nw = w.w_post; p.rows = 2 * I; p.cols = H; p.out = m->h;
+    HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kSiluPair, s));
+    // down_proj + residual (cpu_inference.rs:171-172)
+    p = MatvecParams{};
+    p.w = w.w_down; p.x = m->h; p.rows = H; p.cols = I; p.out = m->x;
+    HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+  }
+  // final norm + lm_head + greedy candidates (cpu_inference.rs:175-178), then argmax
+  MatvecParams p{};
+  p.eps = c.rms_norm_eps;
+  p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
+  HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err, s));
+  return QE_OK;
+}
+
+// host -> device: state {pos, tok_idx = 0} and tokens[0] = token, through pinned staging
+int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  StepState st{uint32_t(pos), 0u, uint32_t(kv->max_seq), kv->tok_cap};
+  memcpy(m->h_small, &st, sizeof(st));
+  m->h_small[8] = token;
+  HIP_TRY(hipMemcpyAsync(kv->state, m->h_small, sizeof(st), hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipMemcpyAsync(kv->tokens, m->h_small + 8, 4, hipMemcpyHostToDevice, m->stream));
+  return QE_OK;
+}
+
+// read and clear the device error word
+int check_err(qe_model* m) {
+  HIP_TRY(hipMemcpyAsync(m->h_small + 12, m->err, 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  uint32_t e = m->h_small[12];
+  if (e) {
+    HIP_TRY(hipMemsetAsync(m->err, 0, 4, m->stream));
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    return fail(QE_ERR_KERNEL, "kernel error bits 0x%x (1: pos >= max_seq, 2: token >= vocab, 4: token ring full)", e);
+  }
+  return QE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
+  if (!model || !out) return fail(QE_ERR_ARG, "null argument");
+  *out = nullptr;
+  if (max_seq == 0 || max_seq > (1u << 24)) return fail(QE_ERR_ARG, "max_seq must be in 1..2^24");
+  if (kv_dtype != QE_KV_F32 && kv_dtype != QE_KV_BF16) return fail(QE_ERR_ARG, "kv_dtype must be QE_KV_F32 or QE_KV_BF16");
+  const qe_config& c = model->cfg;
+  std::unique_ptr<qe_kv> kv(new qe_kv());
+  kv->model = model;
+  kv->max_seq = max_seq;
+  kv->dtype = kv_dtype;
+  kv->tok_cap = uint32_t(max_seq + 2);
+  const size_t el = kv_dtype == QE_KV_BF16 ? 2 : 4;
+  const size_t D = c.head_dim;
+  const size_t kv_bytes = c.num_hidden_layers * c.num_key_value_heads * max_seq * D * el;
+  const size_t rope_bytes = max_seq * D * 4;
+  size_t off = 0;
+  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
+  const size_t ok_ = take(kv_bytes), ov = take(kv_bytes), orope = take(rope_bytes), ost = take(sizeof(StepState)),
+               otok = take(size_t(kv->tok_cap) * 4);
+  HIP_TRY(hipSetDevice(model->device));
+  HIP_TRY(hipMalloc(&kv->mem, off));
+  HIP_TRY(hipMemsetAsync(kv->mem, 0, off, model->stream));
+  kv->k = kv->mem + ok_;
+  kv->v = kv->mem + ov;
+  kv->rope = reinterpret_cast<float*>(kv->mem + orope);
+  kv->state = reinterpret_cast<StepState*>(kv->mem + ost);
+  kv->tokens = reinterpret_cast<uint32_t*>(kv->mem + otok);
+  HIP_TRY(hipHostMalloc(&kv->host_tokens, size_t(kv->tok_cap) * 4, hipHostMallocDefault));
+  memset(kv->host_tokens, 0, size_t(kv->tok_cap) * 4);
+
+  // RoPE table, same expressions as rope_table (metal_inference.rs:140-154) and rope
+  // (cpu_inference.rs:203-215): freq_i = theta^(-2i/D) via powf, then sin/cos of pos*freq
+  std::vector<float> table(max_seq * D);
+  const size_t half = D / 2;
+  std::vector<float> freqs(half);
+  for (size_t i = 0; i < half; i++) freqs[i] = powf(c.rope_theta, -2.0f * float(i) / float(D));
+  for (size_t pos = 0; pos < max_seq; pos++)
+    for (size_t i = 0; i < half; i++) {
+      const float ang = float(pos) * freqs[i];
+      table[(pos * half + i) * 2] = cosf(ang);
+      table[(pos * half + i) * 2 + 1] = sinf(ang);
+    }
+  HIP_TRY(hipMemcpyAsync(kv->rope, table.data(), rope_bytes, hipMemcpyHostToDevice, model->stream));
+  HIP_TRY(hipStreamSynchronize(model->stream));
+
+  uint64_t splits = (max_seq + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk;
+  kv->attn_splits = uint32_t(std::min<uint64_t>(splits, qe::kAttnMaxSplits));
+
+  // capture one decode step
+  HIP_TRY(hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_step(model, kv.get());
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(model->stream, &g);
+  if (rc != QE_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return fail(QE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+  kv->graph = g;
+  HIP_TRY(hipGraphInstantiate(&kv->exec, g, nullptr, nullptr, 0));
+  kv->events.resize(4);
+  for (auto& ev : kv->events) HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  *out = kv.release();
+  return QE_OK;
+}
+
+void qe_kv_free(qe_kv* kv) { delete kv; }
+uint64_t qe_kv_max_seq(const qe_kv* kv) { return kv ? kv->max_seq : 0; }
+uint64_t qe_kv_len(const qe_kv* kv) { return kv ? kv->len : 0; }
+
+int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* logits_out) {
+  if (!model || !kv || !logits_out) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (pos >= kv->max_seq) return fail(QE_ERR_POS, "pos %llu exceeds KV cache size %llu", (unsigned long long)pos, (unsigned long long)kv->max_seq);
+  if (pos > kv->len) return fail(QE_ERR_POS, "pos %llu is past the %llu cached positions", (unsigned long long)pos, (unsigned long long)kv->len);
+  if (token >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab %llu", token, (unsigned long long)model->cfg.vocab_size);
+  int rc = set_state(model, kv, token, pos);
+  if (rc) return rc;
+  HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+  const size_t V = model->cfg.vocab_size;
+  HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
+  if ((rc = check_err(model))) return rc;
+  memcpy(logits_out, model->h_logits, V * 4);
+  kv->len = pos + 1;
+  return QE_OK;
+}
+
+int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv, float* last_logits) {
+  if (!model || !kv || (!ids && n)) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (n == 0) return QE_OK;
+  if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
+  if (start_pos + n > kv->max_seq) return fail(QE_ERR_POS, "prompt end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + n), (unsigned long long)kv->max_seq);
+  for (uint64_t i = 0; i < n; i++)
+    if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
+  // each step reads tokens[tok_idx]; stage the whole prompt into the ring in one copy, then
+  // replay the step n times (the argmax write to tokens[k+1] is overwritten by the next id)
+  int rc = set_state(model, kv, ids[0], start_pos);
+  if (rc) return rc;
+  for (uint64_t i = 0; i < n; i++) {
+    if (i > 0) {
+      // overwrite the slot the previous step's argmax wrote with the next prompt id
+      HIP_TRY(hipMemcpyAsync(kv->tokens + i, ids + i, 4, hipMemcpyHostToDevice, model->stream));
+    }
+    HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+  }
+  if (last_logits) {
+    HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost, model->stream));
+  }
+  if ((rc = check_err(model))) return rc;
+  if (last_logits) memcpy(last_logits, model->h_logits, model->cfg.vocab_size * 4);
+  kv->len = start_pos + n;
+  return QE_OK;
+}
+
+int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv, qe_on_token on_token,
+              void* user, float* logits_per_step) {
+  if (!model || !kv) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (steps == 0) return QE_OK;
+  if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
+  if (start_pos + steps > kv->max_seq) return fail(QE_ERR_POS, "decode end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + steps), (unsigned long long)kv->max_seq);
+  if (first >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab", first);
+  int rc = set_state(model, kv, first, start_pos);
+  if (rc) return rc;
+  const size_t V = model->cfg.vocab_size;
+  const size_t nev = kv->events.size();
+  // step i runs while the host waits for step i-1 (metal_inference.rs:297-316)
+  for (uint64_t i = 0; i <= steps; i++) {
+    if (i < steps) {
+      if (i >= nev) HIP_TRY(hipEventSynchronize(kv->events[i % nev]));  // ring slot free
+      HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+      if (logits_per_step) {
+        HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
+      }
+      HIP_TRY(hipEventRecord(kv->events[i % nev], model->stream));
+      if (logits_per_step) {
+        HIP_TRY(hipEventSynchronize(kv->events[i % nev]));
+        memcpy(logits_per_step + i * V, model->h_logits, V * 4);
+      }
+    }
+    if (i >= 1) {
+      HIP_TRY(hipEventSynchronize(kv->events[(i - 1) % nev]));
+      if (on_token) on_token(user, __atomic_load_n(&kv->host_tokens[i], __ATOMIC_ACQUIRE));
+    }
+  }
+  if ((rc = check_err(model))) return rc;
+  kv->len = start_pos + steps;
+  return QE_OK;
+}
+
+// ---- synthetic inputs ----
+int qe_write_random_checkpoint(const char* dir, uint64_t seed, const qe_config* cfg) {
+  if (!dir || !cfg) return fail(QE_ERR_ARG, "null argument");
+  std::string err;
+  int rc = qe::write_random_checkpoint(dir, seed, *cfg, err);
+  if (rc) return fail(rc, "%s", err.c_str());
+  return QE_OK;
+}
+
+void qe_random_prompt(uint64_t seed, uint64_t n, uint32_t vocab, uint32_t* out) {
+  if (out && vocab) qe::random_prompt(seed, n, vocab, out);
+}
+
+// ---- isolated ops ----
+int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, uint64_t cols, void* stream) {
+  if (!w || !x || !out) return fail(QE_ERR_ARG, "null argument");
+  if (cols % 8 || rows == 0 || cols == 0 || rows > 0xFFFFFFFFull || cols > 0xFFFFFFFFull)
+    return fail(QE_ERR_ARG, "rows must be > 0 and cols a positive multiple of 8");
+  if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(x) % 16)
+    return fail(QE_ERR_ARG, "w and x must be 16-byte aligned");
+  MatvecParams p{};
+  p.w = static_cast<const uint16_t*>(w); p.x = x; p.rows = uint32_t(rows); p.cols = uint32_t(cols); p.out = out;
+  HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint64_t n_pos) {
+  if (!n_kv_heads) return 0;
+  const uint64_t G = n_heads / n_kv_heads;
+  return align_up(n_kv_heads * qe::kAttnMaxSplits * G * (2 + qe::kHeadDim) * 4, 256) + align_up(n_kv_heads * 4, 256) + 256;
+}
+
+int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos, uint64_t kv_stride,
+                    uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits, void* work, void* stream) {
+  if (!q || !k || !v || !out || !work) return fail(QE_ERR_ARG, "null argument");
+  if (n_pos == 0 || n_pos > kv_stride || kv_stride > 0xFFFFFFFFull) return fail(QE_ERR_ARG, "need 0 < n_pos <= kv_stride");
+  if (!n_kv_heads || n_heads % n_kv_heads) return fail(QE_ERR_ARG, "n_heads must be a multiple of n_kv_heads");
+  const uint64_t G = n_heads / n_kv_heads;
+  if (G != 1 && G != 2 && G != 4 && G != 8) return fail(QE_ERR_UNSUPPORTED, "q heads per KV head must be 1, 2, 4 or 8");
+  if (n_splits > qe::kAttnMaxSplits) return fail(QE_ERR_ARG, "n_splits above %d", qe::kAttnMaxSplits);
+  uint8_t* w8 = static_cast<uint8_t*>(work);
+  const size_t part_bytes = align_up(n_kv_heads * qe::kAttnMaxSplits * G * (2 + qe::kHeadDim) * 4, 256);
+  AttnParams a{};
+  a.qkv = q; a.k_cache = const_cast<float*>(k); a.v_cache = const_cast<float*>(v);
+  a.partial = reinterpret_cast<float*>(w8);
+  a.counter = reinterpret_cast<uint32_t*>(w8 + part_bytes);
+  a.err = reinterpret_cast<uint32_t*>(w8 + part_bytes + align_up(n_kv_heads * 4, 256));
+  a.att = out; a.n_heads = uint32_t(n_heads); a.n_kv = uint32_t(n_kv_heads); a.max_seq = uint32_t(kv_stride);
+  a.scale = 1.0f / sqrtf(float(qe::kHeadDim)); a.norm_rope = 0; a.n_pos_fixed = uint32_t(n_pos);
+  a.force_splits = n_splits;
+  uint64_t splits = n_splits ? n_splits : (n_pos + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk;
+  splits = std::min<uint64_t>(std::max<uint64_t>(splits, 1), qe::kAttnMaxSplits);
+  HIP_TRY(qe::launch_attention(a, uint32_t(splits), static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+int qe_op_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream) {
+  if (!src || !partial) return fail(QE_ERR_ARG, "null argument");
+  if (n % 4) return fail(QE_ERR_ARG, "n must be a multiple of 4");
+  HIP_TRY(qe::launch_read_sum(src, n, partial, grid ? grid : 2048, static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,82 @@
+// Device-side data structures and launch wrappers of the decode step (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qe {
+
+constexpr int kHeadDim = 128;        // the attention kernels' lane layout: 64 lanes x float2
+constexpr int kMaxGroup = 8;         // q heads per KV head handled by one attention workgroup
+constexpr int kAttnMinChunk = 16;    // fewest positions per split-K workgroup
+constexpr int kAttnMaxSplits = 128;  // most split-K workgroups per KV head
+
+// Per-sequence device state, advanced by the last kernel of each step so a captured step can
+// be replayed without host writes: step i reads tokens[tok_idx] at position pos and writes its
+// greedy token to tokens[tok_idx + 1].
+struct StepState {
+  uint32_t pos;
+  uint32_t tok_idx;
+  uint32_t max_seq;
+  uint32_t tok_cap;  // entries in the token ring
+};
+
+// Error bits a kernel sets in the model's error word instead of faulting.
+enum : uint32_t {
+  kErrPos = 1u,       // pos >= max_seq seen on the device
+  kErrToken = 2u,     // input token >= vocab
+  kErrRing = 4u,      // token ring full
+};
+
+// Per-workgroup greedy candidate (value, index); NaN is never a candidate.
+struct ArgCand {
+  float v;
+  uint32_t i;
+};
+
+struct MatvecParams {
+  const uint16_t* w;     // bf16 [rows][cols] row-major
+  const float* x;        // [cols] input
+  const uint16_t* nw;    // bf16 [cols] RMSNorm gain (prologue kNorm)
+  float eps;
+  uint32_t rows, cols;
+  float* out;            // [rows] (store / residual add), [rows/2] (silu pairs)
+  ArgCand* cand;         // per-workgroup argmax candidates (epilogue kLogits)
+};
+
+enum Prologue { kCopy = 0, kNorm = 1 };
+enum Epilogue { kStore = 0, kResAdd = 1, kSiluPair = 2, kLogits = 3 };
+
+struct AttnParams {
+  const float* qkv;        // raw projections [n_heads*D | n_kv*D | n_kv*D]
+  const uint16_t* q_norm;  // bf16 [D]
+  const uint16_t* k_norm;  // bf16 [D]
+  const float* rope;       // [max_seq][D/2][2] (cos, sin)
+  void* k_cache;           // layer base, [n_kv][max_seq][D], f32 or bf16
+  void* v_cache;
+  float* partial;          // [n_kv][kAttnMaxSplits][group][2 + D]
+  uint32_t* counter;       // [n_kv] split arrival counters (zero between launches)
+  float* att;              // [n_heads*D]
+  const StepState* state;
+  uint32_t* err;
+  uint32_t n_heads, n_kv, max_seq;
+  float eps, scale;
+  int kv_bf16;
+  int norm_rope;           // 1: q/k are raw and this kernel applies q/k-norm + RoPE and writes
+                           //    the new K/V slot; 0: q is final and the cache is complete
+  uint32_t n_pos_fixed;    // norm_rope == 0: attend 0..n_pos_fixed-1
+  uint32_t force_splits;   // 0: choose from n_pos
+};
+
+// --- launch wrappers (kernels.hip) ---
+hipError_t launch_embed(const uint16_t* table, uint32_t hidden, uint32_t vocab, const uint32_t* tokens,
+                        const StepState* st, float* x, uint32_t* err, hipStream_t s);
+hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
+uint32_t matvec_num_blocks(uint32_t rows, uint32_t cols, int epilogue);
+hipError_t launch_attention(const AttnParams& p, uint32_t grid_splits, hipStream_t s);
+hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,
+                         uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, hipStream_t s);
+hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, hipStream_t s);
+
+}  // namespace qe

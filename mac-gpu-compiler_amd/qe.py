@@ -1,0 +1,288 @@
+"""Python mirror of the reference engine API over the C ABI of libqe.so (include/qe.h).
+
+The reference crate exposes (metal_infrence_engine/src/metal_inference.rs):
+    MetalModel::load_model(path)            -> Model.load_model(path)
+    MetalModel::config()                    -> Model.config()
+    MetalKVCache::new(&model, max_seq)      -> KVCache(model, max_seq)
+    MetalModel::forward(token, pos, cache)  -> Model.forward(token, pos, cache) -> np.ndarray[V]
+    MetalModel::decode(first, start_pos, steps, cache, on_token)
+                                            -> Model.decode(first, start_pos, steps, cache, on_token)
+Where the reference panics on a contract violation, this raises QeError with the C status.
+
+libqe.so must be built (mac-gpu-compiler_amd/build.py); there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from dataclasses import dataclass
+from typing import Callable, Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libqe.so")
+
+QE_OK = 0
+QE_ERR_IO = 1
+QE_ERR_FORMAT = 2
+QE_ERR_TENSOR = 3
+QE_ERR_POS = 4
+QE_ERR_ARG = 5
+QE_ERR_UNSUPPORTED = 6
+QE_ERR_HIP = 7
+QE_ERR_NO_DEVICE = 8
+QE_ERR_KERNEL = 9
+
+QE_KV_F32 = 0
+QE_KV_BF16 = 1
+
+ERROR_NAMES = {
+    QE_ERR_IO: "io", QE_ERR_FORMAT: "format", QE_ERR_TENSOR: "tensor", QE_ERR_POS: "pos",
+    QE_ERR_ARG: "arg", QE_ERR_UNSUPPORTED: "unsupported", QE_ERR_HIP: "hip",
+    QE_ERR_NO_DEVICE: "no_device", QE_ERR_KERNEL: "kernel",
+}
+
+
+class QeError(RuntimeError):
+    def __init__(self, code: int, message: str):
+        super().__init__(f"[{ERROR_NAMES.get(code, code)}] {message}")
+        self.code = code
+
+
+class _CConfig(ctypes.Structure):
+    _fields_ = [
+        ("hidden_size", ctypes.c_uint64),
+        ("intermediate_size", ctypes.c_uint64),
+        ("num_hidden_layers", ctypes.c_uint64),
+        ("num_attention_heads", ctypes.c_uint64),
+        ("num_key_value_heads", ctypes.c_uint64),
+        ("head_dim", ctypes.c_uint64),
+        ("vocab_size", ctypes.c_uint64),
+        ("rms_norm_eps", ctypes.c_float),
+        ("rope_theta", ctypes.c_float),
+        ("eos_token_id", ctypes.c_uint32),
+    ]
+
+
+@dataclass(frozen=True)
+class Config:
+    """config.json subset (cpu_inference.rs:20-33)."""
+    hidden_size: int
+    intermediate_size: int
+    num_hidden_layers: int
+    num_attention_heads: int
+    num_key_value_heads: int
+    head_dim: int
+    vocab_size: int
+    rms_norm_eps: float
+    rope_theta: float
+    eos_token_id: int
+
+    def to_c(self) -> _CConfig:
+        return _CConfig(*[getattr(self, f) for f, _ in _CConfig._fields_])
+
+    @staticmethod
+    def from_c(c: _CConfig) -> "Config":
+        return Config(*[getattr(c, f) for f, _ in _CConfig._fields_])
+
+
+# The Qwen3-0.6B architecture (28 layers, hidden 1024, 16/8 heads, head_dim 128, SwiGLU 3072,
+# vocab 151936, RMSNorm eps 1e-6, RoPE theta 1e6).
+QWEN3_0_6B = Config(1024, 3072, 28, 16, 8, 128, 151936, 1e-6, 1e6, 151645)
+
+ON_TOKEN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32)
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libqe.so (raises if it has not been built)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with mac-gpu-compiler_amd/build.py")
+    # One HIP runtime per process: PyTorch links its bundled libamdhip64.so by the unversioned
+    # name, libqe.so by the soname libamdhip64.so.7. Loading torch first makes libqe.so bind to
+    # the copy torch already mapped (same soname) instead of mapping /opt/rocm's beside it.
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+    L = ctypes.CDLL(LIB_PATH)
+    vp, u64, u32, i32, f32p = ctypes.c_void_p, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_int, ctypes.POINTER(ctypes.c_float)
+    sig = {
+        "qe_last_error": (ctypes.c_char_p, []),
+        "qe_model_load": (i32, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "qe_model_free": (None, [vp]),
+        "qe_model_config": (i32, [vp, ctypes.POINTER(_CConfig)]),
+        "qe_weight_bytes_per_token": (u64, [vp]),
+        "qe_kv_bytes_at": (u64, [vp, u64, i32]),
+        "qe_kv_new": (i32, [vp, u64, i32, ctypes.POINTER(vp)]),
+        "qe_kv_free": (None, [vp]),
+        "qe_kv_max_seq": (u64, [vp]),
+        "qe_kv_len": (u64, [vp]),
+        "qe_forward": (i32, [vp, u32, u64, vp, f32p]),
+        "qe_prefill": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, f32p]),
+        "qe_decode": (i32, [vp, u32, u64, u64, vp, ON_TOKEN, vp, f32p]),
+        "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
+        "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
+        "qe_op_matvec_bf16": (i32, [vp, vp, vp, u64, u64, vp]),
+        "qe_op_attention_work_bytes": (u64, [u64, u64, u64]),
+        "qe_op_attention": (i32, [vp, vp, vp, vp, u64, u64, u64, u64, u32, vp, vp]),
+        "qe_op_read_sum": (i32, [vp, u64, vp, u32, vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(rc: int) -> None:
+    if rc != QE_OK:
+        raise QeError(rc, lib().qe_last_error().decode(errors="replace"))
+
+
+def _fptr(a: np.ndarray):
+    return a.ctypes.data_as(ctypes.POINTER(ctypes.c_float))
+
+
+class Model:
+    """GPU engine handle: MetalModel (metal_inference.rs:100-113, 156-170)."""
+
+    def __init__(self, handle: int):
+        self._h = ctypes.c_void_p(handle)
+        cfg = _CConfig()
+        _check(lib().qe_model_config(self._h, ctypes.byref(cfg)))
+        self._cfg = Config.from_c(cfg)
+
+    @classmethod
+    def load_model(cls, path: str) -> "Model":
+        h = ctypes.c_void_p()
+        _check(lib().qe_model_load(os.fsencode(path), ctypes.byref(h)))
+        return cls(h.value)
+
+    def config(self) -> Config:
+        return self._cfg
+
+    def weight_bytes_per_token(self) -> int:
+        return int(lib().qe_weight_bytes_per_token(self._h))
+
+    def kv_bytes_at(self, pos: int, kv_dtype: int = QE_KV_F32) -> int:
+        return int(lib().qe_kv_bytes_at(self._h, pos, kv_dtype))
+
+    def forward(self, token: int, pos: int, cache: "KVCache") -> np.ndarray:
+        """Logits [vocab] f32 for `token` at `pos`; appends its K/V (metal_inference.rs:284-291)."""
+        out = np.empty(self._cfg.vocab_size, dtype=np.float32)
+        _check(lib().qe_forward(self._h, int(token), int(pos), cache._h, _fptr(out)))
+        return out
+
+    def prefill(self, ids, start_pos: int, cache: "KVCache", want_logits: bool = True) -> Optional[np.ndarray]:
+        arr = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32))
+        out = np.empty(self._cfg.vocab_size, dtype=np.float32) if want_logits else None
+        _check(lib().qe_prefill(self._h, arr.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), arr.size, int(start_pos),
+                                cache._h, _fptr(out) if out is not None else None))
+        return out
+
+    def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",
+               on_token: Optional[Callable[[int], None]] = None, want_logits: bool = False):
+        """Greedy decode (metal_inference.rs:293-316): calls on_token(token) once per finished
+        step, in order. Returns (tokens, logits or None); logits is [steps, vocab]."""
+        toks = []
+
+        def cb(_user, tok):
+            toks.append(int(tok))
+            if on_token is not None:
+                on_token(int(tok))
+
+        ccb = ON_TOKEN(cb)
+        logits = np.empty((steps, self._cfg.vocab_size), dtype=np.float32) if want_logits else None
+        _check(lib().qe_decode(self._h, int(first), int(start_pos), int(steps), cache._h, ccb, None,
+                               _fptr(logits) if logits is not None else None))
+        return toks, logits
+
+    def close(self) -> None:
+        if self._h and self._h.value:
+            lib().qe_model_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class KVCache:
+    """MetalKVCache::new(&model, max_seq) (metal_inference.rs:115-138); kv_dtype f32 or bf16."""
+
+    def __init__(self, model: Model, max_seq: int, kv_dtype: int = QE_KV_F32):
+        h = ctypes.c_void_p()
+        _check(lib().qe_kv_new(model._h, int(max_seq), int(kv_dtype), ctypes.byref(h)))
+        self._h = h
+        self._model = model  # the cache must not outlive its model
+        self.max_seq = int(max_seq)
+
+    def __len__(self) -> int:
+        return int(lib().qe_kv_len(self._h))
+
+    def close(self) -> None:
+        if self._h and self._h.value:
+            lib().qe_kv_free(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def write_random_checkpoint(directory: str, seed: int, cfg: Config = QWEN3_0_6B) -> str:
+    """Seeded random-init checkpoint: <dir>/model.safetensors + config.json. Returns the path."""
+    os.makedirs(directory, exist_ok=True)
+    c = cfg.to_c()
+    _check(lib().qe_write_random_checkpoint(os.fsencode(directory), int(seed), ctypes.byref(c)))
+    return os.path.join(directory, "model.safetensors")
+
+
+def random_prompt(seed: int, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint32)
+    lib().qe_random_prompt(int(seed), int(n), int(vocab), out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return out
+
+
+# ---- isolated device ops on torch tensors (device memory owned by the caller) ----
+
+def _ptr(t) -> int:
+    return t.data_ptr()
+
+
+def _stream_ptr(stream) -> Optional[int]:
+    if stream is None:
+        return None
+    return int(getattr(stream, "cuda_stream", stream))
+
+
+def op_matvec_bf16(w, x, out, stream=None) -> None:
+    """out[r] = sum_c w[r, c] x[c]; w bf16 [rows, cols] (torch.bfloat16 or int16/uint16 view), x f32."""
+    rows, cols = w.shape
+    _check(lib().qe_op_matvec_bf16(_ptr(w), _ptr(x), _ptr(out), rows, cols, _stream_ptr(stream)))
+
+
+def op_attention_work_bytes(n_heads: int, n_kv_heads: int, n_pos: int) -> int:
+    return int(lib().qe_op_attention_work_bytes(n_heads, n_kv_heads, n_pos))
+
+
+def op_attention(q, k, v, out, n_pos: int, n_heads: int, n_kv_heads: int, work, n_splits: int = 0, stream=None) -> None:
+    """q [n_heads*128]; k, v [n_kv][kv_stride][128] f32; work zero-filled before first use."""
+    kv_stride = k.shape[1]
+    _check(lib().qe_op_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_pos, kv_stride, n_heads, n_kv_heads,
+                                 n_splits, _ptr(work), _stream_ptr(stream)))
+
+
+def op_read_sum(src, partial, grid: int = 0, stream=None) -> None:
+    _check(lib().qe_op_read_sum(_ptr(src), src.numel(), _ptr(partial), grid, _stream_ptr(stream)))

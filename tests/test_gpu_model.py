@@ -1,0 +1,122 @@
+"""Whole-model parity on the GPU against the CPU oracle (the reference's own bar:
+tests/metal_parity.rs -- logits max-abs < 1e-2 and equal greedy tokens at every step)."""
+import numpy as np
+import pytest
+
+import oracle
+import qe
+from conftest import TINY
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS_DIFF = 1e-2  # tests/metal_parity.rs:14
+
+
+def test_tiny_forward_matches_oracle(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    cache = qe.KVCache(m, 64)
+    oc = om.new_cache()
+    prompt = qe.random_prompt(3, 40, TINY.vocab_size)
+    worst = 0.0
+    for pos, tok in enumerate(prompt):
+        a = om.forward(int(tok), pos, oc)
+        b = m.forward(int(tok), pos, cache)
+        assert np.all(np.isfinite(b)), f"non-finite logits at pos {pos}"
+        d = float(np.max(np.abs(a - b)))
+        worst = max(worst, d)
+        assert d < 1e-4, f"pos {pos}: logits diverge by {d}"
+        assert oracle.argmax(a) == oracle.argmax(b), f"pos {pos}: different greedy token"
+    assert len(cache) == len(prompt)
+    print(f"tiny forward: worst max-abs {worst:.2e}")
+
+
+def test_tiny_decode_matches_forward(gpu, tiny_ckpt):
+    # tests/metal_parity.rs:42-71: pipelined decode with the GPU argmax == forward + CPU argmax
+    m = qe.Model.load_model(tiny_ckpt)
+    steps = 48
+    prompt = qe.random_prompt(11, 5, TINY.vocab_size)
+    max_seq = len(prompt) + steps + 1
+    cache = qe.KVCache(m, max_seq)
+    for pos, tok in enumerate(prompt):
+        logits = m.forward(int(tok), pos, cache)
+    first = oracle.argmax(logits)
+    expected = []
+    tok = first
+    for i in range(steps):
+        tok = oracle.argmax(m.forward(tok, len(prompt) + i, cache))
+        expected.append(tok)
+    cache2 = qe.KVCache(m, max_seq)
+    m.prefill(prompt, 0, cache2, want_logits=False)
+    got = []
+    toks, _ = m.decode(first, len(prompt), steps, cache2, on_token=got.append)
+    assert got == expected
+    assert toks == expected
+
+
+def test_tiny_decode_matches_oracle(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    steps = 60
+    prompt = qe.random_prompt(13, 9, TINY.vocab_size)
+    cache = qe.KVCache(m, len(prompt) + steps)
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        ol = om.forward(int(tok), pos, oc)
+    gl = m.prefill(prompt, 0, cache)
+    assert np.max(np.abs(gl - ol)) < 1e-4
+    first = oracle.argmax(ol)
+    toks, logits = m.decode(first, len(prompt), steps, cache, want_logits=True)
+    tok = first
+    for i in range(steps):
+        ol = om.forward(tok, len(prompt) + i, oc)
+        assert np.max(np.abs(ol - logits[i])) < 1e-4, f"step {i}"
+        tok = oracle.argmax(ol)
+        assert toks[i] == tok, f"step {i}: gpu {toks[i]} oracle {tok}"
+
+
+def test_prefill_equals_forward_loop(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(17, 23, TINY.vocab_size)
+    c1 = qe.KVCache(m, 32)
+    for pos, tok in enumerate(prompt):
+        a = m.forward(int(tok), pos, c1)
+    c2 = qe.KVCache(m, 32)
+    b = m.prefill(prompt, 0, c2)
+    np.testing.assert_array_equal(a, b)
+
+
+def test_position_contract(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    cache = qe.KVCache(m, 4)
+    with pytest.raises(qe.QeError) as e:
+        m.forward(1, 1, cache)  # nothing cached yet
+    assert e.value.code == qe.QE_ERR_POS
+    for pos in range(4):
+        m.forward(pos, pos, cache)
+    with pytest.raises(qe.QeError) as e:
+        m.forward(1, 4, cache)  # pos >= max_seq (metal_inference.rs:321)
+    assert e.value.code == qe.QE_ERR_POS
+    with pytest.raises(qe.QeError) as e:
+        m.forward(TINY.vocab_size, 0, cache)
+    assert e.value.code == qe.QE_ERR_ARG
+    with pytest.raises(qe.QeError) as e:
+        m.decode(1, 2, 3, cache)  # runs past max_seq
+    assert e.value.code == qe.QE_ERR_POS
+    # rewriting an earlier position is allowed, as in the reference's Metal engine
+    a = m.forward(7, 2, cache)
+    assert np.all(np.isfinite(a)) and len(cache) == 3
+
+
+def test_bf16_kv_cache_drift_is_small(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(19, 30, TINY.vocab_size)
+    c32 = qe.KVCache(m, 32)
+    c16 = qe.KVCache(m, 32, qe.QE_KV_BF16)
+    worst = 0.0
+    for pos, tok in enumerate(prompt):
+        a = m.forward(int(tok), pos, c32)
+        b = m.forward(int(tok), pos, c16)
+        worst = max(worst, float(np.max(np.abs(a - b))))
+    print(f"bf16 KV drift on the tiny model: {worst:.3e}")
+    assert worst < 5e-2
