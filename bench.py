@@ -1,0 +1,244 @@
+"""Batch-1 greedy decode benchmark of the Qwen3-0.6B-architecture bf16 model on one MI355X.
+
+Workload (the reference's bench protocol, metal_infrence_engine/src/bin/bench.rs:165-191, on
+synthetic weights): a seeded random-init checkpoint, a 130-token prompt of uniform-random ids,
+prefill, then K greedy decode steps (default 128, positions 130..257) with an f32 KV cache.
+A "step" is one decode token. Prints ONE JSON line (the last line of stdout).
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--kv f32|bf16] [--no-cpu-baseline]
+"""
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "mac-gpu-compiler_amd")
+sys.path[:0] = [ROOT, PKG]
+
+SEED = 20260101
+PROMPT_SEED = 7
+PROMPT_LEN = 130
+SPEC_HBM_GBS = 8000.0  # MI355X HBM3E spec
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def measured_read_ceiling(torch, qe) -> float:
+    """Best streaming-read GB/s over 1 and 2 GiB buffers (past the 256 MB MALL), as in
+    tests/read_bandwidth.rs:69-141: sum-checked, best of 5 trials of ~8 GiB each."""
+    best = 0.0
+    for gib in (1, 2):
+        n = (gib << 30) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        part = torch.zeros(8192, dtype=torch.float32, device="cuda")
+        grid = 8192
+        qe.op_read_sum(src, part, grid)
+        torch.cuda.synchronize()
+        total = float(part[:grid].double().sum())
+        if total != float(n):
+            raise RuntimeError(f"read_sum checksum {total} != {n}")
+        reps = max(1, 8 // gib)
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                qe.op_read_sum(src, part, grid)
+            e1.record()
+            e1.synchronize()
+            best = max(best, (gib << 30) * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+        del src, part
+    torch.cuda.empty_cache()
+    return best
+
+
+def cpu_baseline(ckpt: str, prompt, target_s: float = 12.0):
+    """The oracle (C restatement of cpu_inference.rs) on this host: a short prefill, then decode
+    steps until ~target_s of decode work; tok/s over the decode steps."""
+    import oracle
+
+    m = oracle.Model(ckpt)
+    cache = m.new_cache()
+    n_prefill = 4
+    for pos in range(n_prefill):
+        logits = m.forward(int(prompt[pos]), pos, cache)
+    tok = oracle.argmax(logits)
+    times = []
+    t_start = time.perf_counter()
+    pos = n_prefill
+    while time.perf_counter() - t_start < target_s and len(times) < 64:
+        t0 = time.perf_counter()
+        logits = m.forward(tok, pos, cache)
+        tok = oracle.argmax(logits)
+        times.append(time.perf_counter() - t0)
+        pos += 1
+    tps = len(times) / sum(times)
+    return {
+        "value": round(tps, 3),
+        "unit": "tok/s",
+        "cores": oracle.get_threads(),
+        "kind": "port",
+        "sample": f"oracle forward (C restatement of cpu_inference.rs, rows split over {oracle.get_threads()} threads "
+                  f"per matvec), {n_prefill}-token prefill then {len(times)} greedy decode steps at positions "
+                  f"{n_prefill}..{pos - 1}; median {sorted(times)[len(times) // 2] * 1e3:.1f} ms/token; host {cpu_model()}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
+    ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
+    ap.add_argument("--workdir", default=os.environ.get("QE_BENCH_DIR", "/tmp/qe_bench"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--json-out", default=None, help="also write a detailed result JSON here")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this engine runs batch-1 decode on one GPU; --gpus {args.gpus} is not supported "
+              "(the multi-GPU layout is a design note, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import qe
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    ckdir = os.path.join(args.workdir, f"qwen3_0_6b_seed{SEED}")
+    ckpt = os.path.join(ckdir, "model.safetensors")
+    if not os.path.exists(ckpt):
+        t0 = time.time()
+        qe.write_random_checkpoint(ckdir, SEED, qe.QWEN3_0_6B)
+        log(f"wrote random-init checkpoint in {time.time() - t0:.1f}s")
+
+    ceiling = measured_read_ceiling(torch, qe)
+    log(f"measured HBM read ceiling: {ceiling:.1f} GB/s")
+
+    t0 = time.time()
+    model = qe.Model.load_model(ckpt)
+    log(f"loaded model in {time.time() - t0:.1f}s")
+    cfg = model.config()
+    kv_dtype = qe.QE_KV_BF16 if args.kv == "bf16" else qe.QE_KV_F32
+    prompt = qe.random_prompt(PROMPT_SEED, args.prompt_len, cfg.vocab_size)
+    K, W = args.steps, args.warmup
+    P = args.prompt_len
+
+    # warm-up: prefill + W decode steps on a throwaway cache
+    wc = qe.KVCache(model, P + W + 1, kv_dtype)
+    logits = model.prefill(prompt, 0, wc)
+    if W:
+        model.decode(int(np.argmax(logits)), P, W, wc)
+    del wc
+
+    # timed: fresh cache, prefill, then exactly K decode steps
+    cache = qe.KVCache(model, P + K + 1, kv_dtype)
+    logits = model.prefill(prompt, 0, cache)
+    first = int(np.argmax(logits))
+    stream = torch.cuda.ExternalStream(model.stream_handle())
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    gaps = []
+    last = [0.0]
+
+    def on_token(_t):
+        now = time.perf_counter()
+        gaps.append(now - last[0])
+        last[0] = now
+
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    t_start = time.perf_counter()
+    last[0] = t_start
+    tokens, _ = model.decode(first, P, K, cache, on_token=on_token)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    gpu_s = ev0.elapsed_time(ev1) * 1e-3
+
+    weight_bytes = model.weight_bytes_per_token()
+    kv_bytes = [model.kv_bytes_at(p, kv_dtype) for p in range(P, P + K)]
+    bytes_total = K * weight_bytes + sum(kv_bytes)
+    avg_bytes = bytes_total / K
+    tps = K / wall
+    ms_per_step = wall / K * 1e3
+    per_token_gpu_s = gpu_s / K
+    achieved_gbs = avg_bytes / per_token_gpu_s / 1e9
+
+    # token parity against the oracle's committed run of the same workload
+    parity = None
+    fx = os.path.join(ROOT, "tests", "golden", "qwen3_0_6b_decode.npz")
+    if os.path.exists(fx) and P == PROMPT_LEN and kv_dtype == qe.QE_KV_F32:
+        g = np.load(fx, allow_pickle=False)
+        ref = [int(t) for t in g["tokens"]]
+        got = [first] + tokens
+        n = min(len(ref), len(got))
+        div = next((i for i in range(n) if ref[i] != got[i]), None)
+        parity = {"compared": n, "first_divergence": div}
+
+    result = {
+        "metric": "decode tok/s @ batch 1, Qwen3-0.6B-arch bf16; achieved HBM GB/s vs roofline",
+        "value": round(tps, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": W,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"Qwen3-0.6B-architecture decoder, seeded random-init bf16 weights (seed {SEED}), "
+                        f"{P}-token random prompt (seed {PROMPT_SEED}), {K} greedy decode steps at batch 1, "
+                        f"{args.kv} KV cache",
+            "prompt_tokens": P,
+            "decode_steps": K,
+            "kv_cache": args.kv,
+            "batch": 1,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved_gbs, 1),
+            "peak": SPEC_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved_gbs / SPEC_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": "decode step (one hipGraph replay per token)",
+            "bytes_per_launch": int(round(avg_bytes)),
+            "launch_us": round(per_token_gpu_s * 1e6, 2),
+            "measured_ceiling_gbs": round(ceiling, 1),
+            "frac_of_measured": round(achieved_gbs / ceiling, 4),
+        },
+        "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
+        "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),
+        "weight_bytes_per_token": weight_bytes,
+        "parity_vs_oracle_fixture": parity,
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(ckpt, prompt)
+    if args.json_out:
+        detail = dict(result, tokens=[first] + tokens, samples_ms=[round(g * 1e3, 4) for g in gaps])
+        with open(args.json_out, "w") as f:
+            json.dump(detail, f, indent=1)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

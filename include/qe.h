@@ -68,6 +68,9 @@ int qe_model_load(const char* safetensors_path, qe_model** out);
 void qe_model_free(qe_model* model);
 /* MetalModel::config (metal_inference.rs:170) */
 int qe_model_config(const qe_model* model, qe_config* out);
+/* The HIP stream (hipStream_t) every call on this model is ordered on, so a caller can time
+ * it with its own events. No reference counterpart: the Metal engine keeps its queue private. */
+void* qe_model_stream(const qe_model* model);
 /* bench.rs:106-116 (tests/mbu.rs:19-30): every tensor's bytes except the embedding table,
  * plus one embedding row */
 uint64_t qe_weight_bytes_per_token(const qe_model* model);

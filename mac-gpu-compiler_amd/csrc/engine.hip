@@ -315,6 +315,8 @@ int qe_model_config(const qe_model* model, qe_config* out) {
 
 uint64_t qe_weight_bytes_per_token(const qe_model* model) { return model ? model->weight_bytes : 0; }
 
+void* qe_model_stream(const qe_model* model) { return model ? static_cast<void*>(model->stream) : nullptr; }
+
 uint64_t qe_kv_bytes_at(const qe_model* model, uint64_t pos, int kv_dtype) {
   if (!model) return 0;
   const qe_config& c = model->cfg;

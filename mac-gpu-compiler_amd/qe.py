@@ -118,6 +118,7 @@ def lib() -> ctypes.CDLL:
         "qe_model_free": (None, [vp]),
         "qe_model_config": (i32, [vp, ctypes.POINTER(_CConfig)]),
         "qe_weight_bytes_per_token": (u64, [vp]),
+        "qe_model_stream": (vp, [vp]),
         "qe_kv_bytes_at": (u64, [vp, u64, i32]),
         "qe_kv_new": (i32, [vp, u64, i32, ctypes.POINTER(vp)]),
         "qe_kv_free": (None, [vp]),
@@ -170,6 +171,10 @@ class Model:
 
     def weight_bytes_per_token(self) -> int:
         return int(lib().qe_weight_bytes_per_token(self._h))
+
+    def stream_handle(self) -> int:
+        """The hipStream_t all of this model's work runs on (for external timing events)."""
+        return int(lib().qe_model_stream(self._h) or 0)
 
     def kv_bytes_at(self, pos: int, kv_dtype: int = QE_KV_F32) -> int:
         return int(lib().qe_kv_bytes_at(self._h, pos, kv_dtype))
