@@ -1,0 +1,77 @@
+// Device helpers shared by the decode kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qe {
+namespace {
+
+__device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40);
+  return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
+}
+
+// Cross-lane move through DPP. Lanes the control does not write keep 0.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// As dpp(), but lanes the control does not write keep -inf (the identity of max).
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_ninf(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(int(0xFF800000u), __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Max over the 64 lanes of a wave, returned to every lane (same lane pattern as wave_sum).
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_ninf<0xB1>(v));
+  v = fmaxf(v, dpp_ninf<0x4E>(v));
+  v = fmaxf(v, dpp_ninf<0x141>(v));
+  v = fmaxf(v, dpp_ninf<0x140>(v));
+  v = fmaxf(v, dpp_ninf<0x142, 0xA>(v));
+  v = fmaxf(v, dpp_ninf<0x143, 0xC>(v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// Sum over the 64 lanes of a wave, returned to every lane (wave-uniform).
+// quad xor1, quad xor2, half-row mirror, row mirror, row_bcast15 (rows 1,3), row_bcast31 (rows 2,3):
+// lane 63 then holds the total.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  v += dpp<0x142, 0xA>(v);
+  v += dpp<0x143, 0xC>(v);
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// a beats b: larger value, or equal value and lower index (first maximum wins, main.rs:37-42)
+__device__ __forceinline__ bool cand_better(float av, uint32_t ai, float bv, uint32_t bi) {
+  return av > bv || (av == bv && ai < bi);
+}
+
+// acc += sum of the 8 bf16 weights in u times the 8 floats a, b (f32 FMA)
+__device__ __forceinline__ float dot8(uint4 u, float4 a, float4 b, float acc) {
+  acc = fmaf(__uint_as_float(u.x << 16), a.x, acc);
+  acc = fmaf(__uint_as_float(u.x & 0xFFFF0000u), a.y, acc);
+  acc = fmaf(__uint_as_float(u.y << 16), a.z, acc);
+  acc = fmaf(__uint_as_float(u.y & 0xFFFF0000u), a.w, acc);
+  acc = fmaf(__uint_as_float(u.z << 16), b.x, acc);
+  acc = fmaf(__uint_as_float(u.z & 0xFFFF0000u), b.y, acc);
+  acc = fmaf(__uint_as_float(u.w << 16), b.z, acc);
+  acc = fmaf(__uint_as_float(u.w & 0xFFFF0000u), b.w, acc);
+  return acc;
+}
+
+__host__ __device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
+
+}  // namespace
+}  // namespace qe

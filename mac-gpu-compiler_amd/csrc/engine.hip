@@ -8,6 +8,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <string>
@@ -108,6 +109,8 @@ struct qe_kv {
   uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
   uint32_t tok_cap = 0;
   uint32_t attn_splits = 1;
+  uint32_t attn_chunk = 1;      // positions per attention split (fixed per cache)
+  bool narrow_kernels = false;  // the 4-wave kernels of the first version (A/B profiling)
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   std::vector<hipEvent_t> events;
@@ -286,7 +289,7 @@ int qe_model_load(const char* path, qe_model** out) {
   auto stake = [&](size_t bytes) { size_t o = so; so = align_up(so + bytes, 256); return o; };
   const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
                s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
-               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxSplits * G * (2 + D) * 4),
+               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxSplits * G * qe::kPartStride * 4),
                s_cnt = stake(c.num_key_value_heads * 4), s_err = stake(4);
   HIP_TRY(hipMalloc(&m->scratch, so));
   HIP_TRY(hipMemset(m->scratch, 0, so));
@@ -335,15 +338,23 @@ int enqueue_step(qe_model* m, qe_kv* kv) {
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
+  const bool narrow = kv->narrow_kernels;
   hipStream_t s = m->stream;
-  HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
+  auto matvec = [&](const MatvecParams& p, int pro, int epi) {
+    return narrow ? qe::launch_matvec(p, pro == qe::kEmbedNorm ? qe::kNorm : pro, epi, s)
+                  : qe::launch_matvec_wide(p, pro, epi, s);
+  };
+  // the narrow kernels have no embedding prologue: a separate embed kernel fills x first
+  if (narrow) HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     MatvecParams p{};
     p.eps = c.rms_norm_eps;
-    // input_layernorm + q|k|v projections (cpu_inference.rs:129-132)
+    // [layer 0: embedding row (cpu_inference.rs:109-111)] input_layernorm + q|k|v projections
+    // (cpu_inference.rs:129-132)
     p.w = w.w_qkv; p.x = m->x; p.nw = w.w_in; p.rows = QD + 2 * KD; p.cols = H; p.out = m->qkv;
-    HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kStore, s));
+    p.embed = m->embed; p.tokens = kv->tokens; p.state = kv->state; p.vocab = V; p.x_out = m->x; p.err = m->err;
+    HIP_TRY(matvec(p, l == 0 ? qe::kEmbedNorm : qe::kNorm, qe::kStore));
     // q/k norm + RoPE, K/V append, attention (cpu_inference.rs:134-162)
     AttnParams a{};
     a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
@@ -353,20 +364,28 @@ int enqueue_step(qe_model* m, qe_kv* kv) {
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.max_seq = uint32_t(kv->max_seq); a.eps = c.rms_norm_eps; a.scale = 1.0f / sqrtf(float(D));
     a.kv_bf16 = kv->dtype == QE_KV_BF16; a.norm_rope = 1;
-    HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
-    // o_proj + residual (cpu_inference.rs:163-164)
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
-    HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+    if (narrow) {
+      HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
+      // o_proj + residual (cpu_inference.rs:163-164)
+      HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+    } else {
+      HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
+      // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
+      p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
+      p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
+      HIP_TRY(qe::launch_matvec(p, qe::kAttnMerge, qe::kResAdd, s));
+    }
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
     p.eps = c.rms_norm_eps;
     p.w = w.w_gu; p.x = m->x; p.nw = w.w_post; p.rows = 2 * I; p.cols = H; p.out = m->h;
-    HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kSiluPair, s));
+    HIP_TRY(matvec(p, qe::kNorm, qe::kSiluPair));
     // down_proj + residual (cpu_inference.rs:171-172)
     p = MatvecParams{};
     p.w = w.w_down; p.x = m->h; p.rows = H; p.cols = I; p.out = m->x;
-    HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+    HIP_TRY(matvec(p, qe::kCopy, qe::kResAdd));
   }
   // final norm + lm_head + greedy candidates (cpu_inference.rs:175-178), then argmax
   MatvecParams p{};
@@ -450,8 +469,17 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   HIP_TRY(hipMemcpyAsync(kv->rope, table.data(), rope_bytes, hipMemcpyHostToDevice, model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
 
-  uint64_t splits = (max_seq + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk;
-  kv->attn_splits = uint32_t(std::min<uint64_t>(splits, qe::kAttnMaxSplits));
+  // QE_KERNELS=narrow selects the first version's 4-wave kernels (for A/B profiling)
+  const char* kern = getenv("QE_KERNELS");
+  kv->narrow_kernels = kern && strcmp(kern, "narrow") == 0;
+  if (kv->narrow_kernels) {
+    kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk, qe::kAttnMaxSplits));
+  } else {
+    // a fixed split of the cache into runs of >= 64 positions, at most kAttnMaxMergeSplits of
+    // them (the o_proj prologue merges that many partials per q head)
+    kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
+    kv->attn_chunk = uint32_t((max_seq + kv->attn_splits - 1) / kv->attn_splits);
+  }
 
   // capture one decode step
   HIP_TRY(hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal));
@@ -578,7 +606,11 @@ int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, 
     return fail(QE_ERR_ARG, "w and x must be 16-byte aligned");
   MatvecParams p{};
   p.w = static_cast<const uint16_t*>(w); p.x = x; p.rows = uint32_t(rows); p.cols = uint32_t(cols); p.out = out;
-  HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream)));
+  // the kernel the engine uses for this shape: per-layer projections take the wide layout,
+  // vocabulary-sized matrices (the lm_head) the LDS-staged one
+  const bool wide = cols / 8 <= 512 && rows <= 16384;
+  HIP_TRY(wide ? qe::launch_matvec_wide(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream))
+               : qe::launch_matvec(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }
 

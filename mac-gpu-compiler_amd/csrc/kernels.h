@@ -38,14 +38,26 @@ struct ArgCand {
 struct MatvecParams {
   const uint16_t* w;     // bf16 [rows][cols] row-major
   const float* x;        // [cols] input
-  const uint16_t* nw;    // bf16 [cols] RMSNorm gain (prologue kNorm)
+  const uint16_t* nw;    // bf16 [cols] RMSNorm gain (prologues kNorm, kEmbedNorm)
   float eps;
   uint32_t rows, cols;
   float* out;            // [rows] (store / residual add), [rows/2] (silu pairs)
   ArgCand* cand;         // per-workgroup argmax candidates (epilogue kLogits)
+  // prologue kEmbedNorm: x is row tokens[state->tok_idx] of the bf16 table `embed`
+  const uint16_t* embed;
+  const uint32_t* tokens;
+  const StepState* state;
+  uint32_t vocab;
+  float* x_out;          // the embedding row is also written here (the residual stream)
+  uint32_t* err;
+  uint32_t x_rep;        // copies of x to spread reads over (0/1: one)
+  uint32_t x_rep_stride; // floats between copies
+  // prologue kAttnMerge: x[h*128 + d] is merged from attention split partials
+  const float* attn_part;  // [n_kv][attn_splits][group][2 + 128]
+  uint32_t attn_splits, attn_group;
 };
 
-enum Prologue { kCopy = 0, kNorm = 1 };
+enum Prologue { kCopy = 0, kNorm = 1, kEmbedNorm = 2, kAttnMerge = 3 };
 enum Epilogue { kStore = 0, kResAdd = 1, kSiluPair = 2, kLogits = 3 };
 
 struct AttnParams {
@@ -74,7 +86,19 @@ hipError_t launch_embed(const uint16_t* table, uint32_t hidden, uint32_t vocab, 
                         const StepState* st, float* x, uint32_t* err, hipStream_t s);
 hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
 uint32_t matvec_num_blocks(uint32_t rows, uint32_t cols, int epilogue);
+// the per-layer projections: ~1000 workgroups, x read per chunk from global memory
+hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
 hipError_t launch_attention(const AttnParams& p, uint32_t grid_splits, hipStream_t s);
+// positions one attention workgroup covers before the work is split (split-K)
+constexpr int kAttnBlockPositions = 512;
+hipError_t launch_attention_wide(const AttnParams& p, uint32_t grid_splits, hipStream_t s);
+// Decode-step attention with a fixed split of the cache into `splits` runs of `chunk` positions
+// (host-chosen from max_seq): each workgroup writes (m, l, acc) partials, runs past pos write an
+// empty partial, and the o_proj matvec merges them in its prologue (kAttnMerge).
+constexpr int kAttnMaxMergeSplits = 16;
+// one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
+constexpr int kPartStride = 4 + kHeadDim;
+hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s);
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,
                          uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, hipStream_t s);
 hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, hipStream_t s);

@@ -12,55 +12,10 @@
 
 #include <cmath>
 
+#include "device_common.h"
+
 namespace qe {
 namespace {
-
-__device__ __forceinline__ float bf16f(uint16_t x) { return __uint_as_float(uint32_t(x) << 16); }
-
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return uint16_t((u >> 16) | 0x40);
-  return uint16_t((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
-}
-
-// Cross-lane move through DPP. Lanes the control does not write keep 0.
-template <int CTRL, int ROW_MASK = 0xF>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROW_MASK, 0xF, false));
-}
-
-// Sum over the 64 lanes of a wave, returned to every lane (wave-uniform).
-// quad xor1, quad xor2, half-row mirror, row mirror, row_bcast15 (rows 1,3), row_bcast31 (rows 2,3):
-// lane 63 then holds the total.
-__device__ __forceinline__ float wave_sum(float v) {
-  v += dpp<0xB1>(v);
-  v += dpp<0x4E>(v);
-  v += dpp<0x141>(v);
-  v += dpp<0x140>(v);
-  v += dpp<0x142, 0xA>(v);
-  v += dpp<0x143, 0xC>(v);
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
-
-// a beats b: larger value, or equal value and lower index (first maximum wins, main.rs:37-42)
-__device__ __forceinline__ bool cand_better(float av, uint32_t ai, float bv, uint32_t bi) {
-  return av > bv || (av == bv && ai < bi);
-}
-
-// acc += sum of the 8 bf16 weights in u times the 8 floats a, b (f32 FMA)
-__device__ __forceinline__ float dot8(uint4 u, float4 a, float4 b, float acc) {
-  acc = fmaf(__uint_as_float(u.x << 16), a.x, acc);
-  acc = fmaf(__uint_as_float(u.x & 0xFFFF0000u), a.y, acc);
-  acc = fmaf(__uint_as_float(u.y << 16), a.z, acc);
-  acc = fmaf(__uint_as_float(u.y & 0xFFFF0000u), a.w, acc);
-  acc = fmaf(__uint_as_float(u.z << 16), b.x, acc);
-  acc = fmaf(__uint_as_float(u.z & 0xFFFF0000u), b.y, acc);
-  acc = fmaf(__uint_as_float(u.w << 16), b.z, acc);
-  acc = fmaf(__uint_as_float(u.w & 0xFFFF0000u), b.w, acc);
-  return acc;
-}
-
-__host__ __device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 // ---------------------------------------------------------------------------------------------
 // embed: x = bf16 row of the token read from the device token ring (inference.metal:98-107)
@@ -109,10 +64,54 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
   const float4* x4 = reinterpret_cast<const float4*>(p.x);
   float4* xs4 = reinterpret_cast<float4*>(xs);
   float ss = 0.f;
-  for (uint32_t i = tid; i < p.cols / 4; i += 256) {
-    float4 v = x4[i];
-    xs4[i] = v;
-    if (PRO == kNorm) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  if (PRO == kAttnMerge) {
+    // xin[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max_s m_s), over the
+    // attention split partials [n_kv][splits][group][m, l, acc[128]]; empty splits (m = -inf)
+    // add 0. Thread -> 8 consecutive dims of one head; all of its split loads are issued before
+    // any is used (splits <= kAttnMaxMergeSplits).
+    constexpr int SM = kAttnMaxMergeSplits, PS = kPartStride;
+    const uint32_t G = p.attn_group, S = p.attn_splits;
+    for (uint32_t i8 = tid; i8 < p.cols / 8; i8 += 256) {
+      const uint32_t h = i8 / (kHeadDim / 8), d0 = (i8 % (kHeadDim / 8)) * 8, g = h / G, j = h % G;
+      const float* pg = p.attn_part + size_t(g) * S * G * PS + j * PS;
+      float mv[SM], lv[SM];
+      float4 a0[SM], a1[SM];
+#pragma unroll
+      for (int s = 0; s < SM; s++) {
+        if (s < int(S)) {
+          const float* q = pg + size_t(s) * G * PS;
+          mv[s] = q[0];
+          lv[s] = q[1];
+          a0[s] = *reinterpret_cast<const float4*>(q + 4 + d0);
+          a1[s] = *reinterpret_cast<const float4*>(q + 4 + d0 + 4);
+        } else {
+          mv[s] = -INFINITY;
+        }
+      }
+      float M = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < SM; s++) M = fmaxf(M, mv[s]);
+      float L = 0.f;
+      float4 A0 = make_float4(0, 0, 0, 0), A1 = A0;
+#pragma unroll
+      for (int s = 0; s < SM; s++) {
+        if (mv[s] != -INFINITY) {
+          const float e = expf(mv[s] - M);
+          L += e * lv[s];
+          A0.x += e * a0[s].x; A0.y += e * a0[s].y; A0.z += e * a0[s].z; A0.w += e * a0[s].w;
+          A1.x += e * a1[s].x; A1.y += e * a1[s].y; A1.z += e * a1[s].z; A1.w += e * a1[s].w;
+        }
+      }
+      const float inv = 1.0f / L;
+      xs4[2 * i8] = make_float4(A0.x * inv, A0.y * inv, A0.z * inv, A0.w * inv);
+      xs4[2 * i8 + 1] = make_float4(A1.x * inv, A1.y * inv, A1.z * inv, A1.w * inv);
+    }
+  } else {
+    for (uint32_t i = tid; i < p.cols / 4; i += 256) {
+      float4 v = x4[i];
+      xs4[i] = v;
+      if (PRO == kNorm) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    }
   }
   if (PRO == kNorm) {
     ss = wave_sum(ss);
@@ -200,220 +199,154 @@ __global__ __launch_bounds__(256) void k_matvec_generic(MatvecParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// attention for one new token: GQA, split-K over positions with an online softmax per split,
-// merged by the last split to finish (inference.metal:194-296, cpu_inference.rs:134-162).
-// grid (n_kv, grid_splits); one workgroup serves all G q heads of its KV head from one read of
-// K/V. Lane l holds head dims (2l, 2l+1). With norm_rope, the workgroup first applies the
-// per-head q RMSNorm + RoPE, and the split that owns `pos` also normalizes/rotates the new k
-// and appends k and v to the cache (cpu_inference.rs:137-141).
+// matvec for the per-layer projections (q|k|v, o, gate|up, down). A batch-1 projection is only
+// 4-13 MB, so a launch is latency-bound unless many workgroups have their loads in flight at
+// once: TPR threads share a row (thread t reads 16-byte chunks t, t+TPR, ...), a 256-thread
+// workgroup holds 256/TPR row groups of RR rows, giving ~1000 workgroups per launch. Each thread
+// reads only the x chunks it multiplies, straight from global memory (no LDS staging).
+// Prologue kNorm: every row group computes sum(x^2) over its own chunks (which cover the whole
+// row) and normalizes them, (x * s) * gain (cpu_inference.rs:189-194).
+// Prologue kEmbedNorm: x is the bf16 embedding row of the step's token (inference.metal:98-107),
+// which workgroup 0 also stores to x_out for the residual stream.
 // ---------------------------------------------------------------------------------------------
-template <int G, bool KV_BF16>
-__global__ __launch_bounds__(256) void k_attention(AttnParams p) {
-  constexpr int D = kHeadDim;
+template <int TPR, int CPT, int RR, int PRO, int EPI>
+__global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
+  constexpr int NG = 256 / TPR;          // row groups per workgroup
+  constexpr int WPG = TPR / 64;          // waves per row group
+  __shared__ float red[4][RR + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t g = blockIdx.x;
-  uint32_t n, pos;
-  if (p.norm_rope) {
-    pos = p.state->pos;
-    if (pos >= p.max_seq) {
-      if (g == 0 && blockIdx.y == 0 && tid == 0) atomicOr(p.err, kErrPos);
-      return;
+  const int grp = tid / TPR, t = tid % TPR;
+  const uint32_t nch = p.cols >> 3;
+  const uint32_t row0 = (blockIdx.x * NG + uint32_t(grp)) * RR;
+  const uint4* W = reinterpret_cast<const uint4*>(p.w);
+
+  uint4 wv[RR][CPT];
+#pragma unroll
+  for (int r = 0; r < RR; r++) {
+    const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
+      wv[r][k] = c < nch ? W[size_t(row) * nch + c] : make_uint4(0, 0, 0, 0);
     }
-    n = pos + 1;
+  }
+
+  // RMSNorm gains do not depend on x: load them with the weights, off the critical path
+  uint4 gains[CPT];
+  if (PRO != kCopy) {
+    const uint4* NWv = reinterpret_cast<const uint4*>(p.nw);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
+      gains[k] = c < nch ? NWv[c] : make_uint4(0, 0, 0, 0);
+    }
+  }
+  float4 xa[CPT], xb[CPT];
+  if (PRO == kEmbedNorm) {
+    uint32_t tok = p.tokens[p.state->tok_idx];
+    if (tok >= p.vocab) {
+      if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
+      tok = 0;
+    }
+    const uint4* E = reinterpret_cast<const uint4*>(p.embed) + size_t(tok) * nch;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
+      const uint4 e = c < nch ? E[c] : make_uint4(0, 0, 0, 0);
+      xa[k] = make_float4(__uint_as_float(e.x << 16), __uint_as_float(e.x & 0xFFFF0000u),
+                          __uint_as_float(e.y << 16), __uint_as_float(e.y & 0xFFFF0000u));
+      xb[k] = make_float4(__uint_as_float(e.z << 16), __uint_as_float(e.z & 0xFFFF0000u),
+                          __uint_as_float(e.w << 16), __uint_as_float(e.w & 0xFFFF0000u));
+      if (blockIdx.x == 0 && grp == 0 && c < nch) {
+        float4* xo = reinterpret_cast<float4*>(p.x_out);
+        xo[2 * c] = xa[k];
+        xo[2 * c + 1] = xb[k];
+      }
+    }
   } else {
-    n = p.n_pos_fixed;
-    pos = n - 1;
-  }
-  uint32_t nsplit = p.force_splits ? min(p.force_splits, gridDim.y) : min(gridDim.y, ceil_div(n, kAttnMinChunk));
-  const uint32_t chunk = ceil_div(n, nsplit);
-  nsplit = ceil_div(n, chunk);
-  const uint32_t s = blockIdx.y;
-  if (s >= nsplit) return;
-  const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
-  const bool owns_new = p.norm_rope && t1 == n;
-
-  __shared__ float qs[G][D];
-  __shared__ float knew[D], vnew[D], ktmp[D];
-  __shared__ float wm[4][G], wl[4][G];
-  __shared__ float wacc[4][G][D];
-  __shared__ int is_last;
-
-  for (int i = tid; i < G * D; i += 256) qs[i / D][i % D] = p.qkv[size_t(g) * G * D + i];
-  __syncthreads();
-  if (p.norm_rope) {
-    for (int j = wave; j < G; j += 4) {
-      const float a = qs[j][2 * lane], b = qs[j][2 * lane + 1];
-      const float ssum = wave_sum(a * a + b * b);
-      const float sc = 1.0f / sqrtf(ssum / float(D) + p.eps);
-      qs[j][2 * lane] = a * sc * bf16f(p.q_norm[2 * lane]);
-      qs[j][2 * lane + 1] = b * sc * bf16f(p.q_norm[2 * lane + 1]);
+    // x_rep > 1: the producer wrote x_rep copies of x, x_rep_stride floats apart; workgroups
+    // spread their reads over the copies instead of all hitting the same lines
+    const float* xsrc = p.x_rep > 1 ? p.x + size_t(blockIdx.x % p.x_rep) * p.x_rep_stride : p.x;
+    const float4* x4 = reinterpret_cast<const float4*>(xsrc);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
+      xa[k] = c < nch ? x4[2 * c] : make_float4(0, 0, 0, 0);
+      xb[k] = c < nch ? x4[2 * c + 1] : make_float4(0, 0, 0, 0);
     }
-    if (owns_new && wave == 0) {
-      const float* kr = p.qkv + size_t(p.n_heads) * D + size_t(g) * D;
-      const float* vr = p.qkv + size_t(p.n_heads) * D + size_t(p.n_kv) * D + size_t(g) * D;
-      const float a = kr[2 * lane], b = kr[2 * lane + 1];
-      const float ssum = wave_sum(a * a + b * b);
-      const float sc = 1.0f / sqrtf(ssum / float(D) + p.eps);
-      ktmp[2 * lane] = a * sc * bf16f(p.k_norm[2 * lane]);
-      ktmp[2 * lane + 1] = b * sc * bf16f(p.k_norm[2 * lane + 1]);
-      vnew[2 * lane] = vr[2 * lane];
-      vnew[2 * lane + 1] = vr[2 * lane + 1];
+  }
+  // RMSNorm: the scale s is a scalar, so sum_c W[r,c] * ((x_c * s) * g_c) is evaluated as
+  // s * sum_c W[r,c] * (x_c * g_c): the sum of squares then reduces alongside the dot products
+  // instead of in front of them (a reassociation of the reference's f32 product, well inside
+  // the logit tolerance)
+  float ss = 0.f;
+  if (PRO != kCopy) {
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      ss += (xa[k].x * xa[k].x + xa[k].y * xa[k].y + xa[k].z * xa[k].z + xa[k].w * xa[k].w) +
+            (xb[k].x * xb[k].x + xb[k].y * xb[k].y + xb[k].z * xb[k].z + xb[k].w * xb[k].w);
+      const uint4 g = gains[k];
+      xa[k].x *= __uint_as_float(g.x << 16);
+      xa[k].y *= __uint_as_float(g.x & 0xFFFF0000u);
+      xa[k].z *= __uint_as_float(g.y << 16);
+      xa[k].w *= __uint_as_float(g.y & 0xFFFF0000u);
+      xb[k].x *= __uint_as_float(g.z << 16);
+      xb[k].y *= __uint_as_float(g.z & 0xFFFF0000u);
+      xb[k].z *= __uint_as_float(g.w << 16);
+      xb[k].w *= __uint_as_float(g.w & 0xFFFF0000u);
+    }
+  }
+
+  float acc[RR];
+#pragma unroll
+  for (int r = 0; r < RR; r++) {
+    acc[r] = 0.f;
+#pragma unroll
+    for (int k = 0; k < CPT; k++) acc[r] = dot8(wv[r][k], xa[k], xb[k], acc[r]);
+    acc[r] = wave_sum(acc[r]);
+  }
+  if (PRO != kCopy) ss = wave_sum(ss);
+  if (WPG > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < RR; r++) red[wave][r] = acc[r];
+      red[wave][RR] = ss;
     }
     __syncthreads();
-    const float2* rope = reinterpret_cast<const float2*>(p.rope) + size_t(pos) * (D / 2);
-    for (int i = tid; i < G * (D / 2); i += 256) {
-      const int j = i / (D / 2), d = i % (D / 2);
-      const float2 cs = rope[d];
-      const float a = qs[j][d], b = qs[j][d + D / 2];
-      qs[j][d] = a * cs.x - b * cs.y;
-      qs[j][d + D / 2] = b * cs.x + a * cs.y;
+#pragma unroll
+    for (int r = 0; r <= RR; r++) {
+      float v = 0.f;
+#pragma unroll
+      for (int w = 0; w < WPG; w++) v += red[grp * WPG + w][r];
+      if (r < RR) acc[r] = v;
+      else ss = v;
     }
-    if (owns_new && tid < D / 2) {
-      const float2 cs = rope[tid];
-      const float a = ktmp[tid], b = ktmp[tid + D / 2];
-      knew[tid] = a * cs.x - b * cs.y;
-      knew[tid + D / 2] = b * cs.x + a * cs.y;
-    }
-    __syncthreads();
-    if (owns_new && tid < D) {
-      const size_t slot = (size_t(g) * p.max_seq + pos) * D + tid;
-      if (KV_BF16) {
-        const uint16_t kb = f32_to_bf16(knew[tid]), vb = f32_to_bf16(vnew[tid]);
-        static_cast<uint16_t*>(p.k_cache)[slot] = kb;
-        static_cast<uint16_t*>(p.v_cache)[slot] = vb;
-        knew[tid] = bf16f(kb);  // attend with what later steps will read back
-        vnew[tid] = bf16f(vb);
-      } else {
-        static_cast<float*>(p.k_cache)[slot] = knew[tid];
-        static_cast<float*>(p.v_cache)[slot] = vnew[tid];
-      }
-    }
-    __syncthreads();
   }
-
-  // per-wave online softmax over positions t0 + wave, t0 + wave + 4, ...
-  float2 q2[G];
+  if (PRO != kCopy) {
+    const float s = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
 #pragma unroll
-  for (int j = 0; j < G; j++) q2[j] = make_float2(qs[j][2 * lane], qs[j][2 * lane + 1]);
-  float m[G], l[G];
-  float2 acc[G];
+    for (int r = 0; r < RR; r++) acc[r] *= s;
+  }
+  if (t != 0) return;
+  if (EPI == kStore || EPI == kResAdd) {
 #pragma unroll
-  for (int j = 0; j < G; j++) { m[j] = -INFINITY; l[j] = 0.f; acc[j] = make_float2(0.f, 0.f); }
-
-  const size_t head_base = size_t(g) * p.max_seq * D;
-  // positions that come from the cache; with owns_new the last one (pos) comes from LDS
-  const uint32_t tc1 = owns_new ? t1 - 1 : t1;
-  constexpr int U = 4;
-  uint32_t t = t0 + wave;
-  for (; t + 4 * (U - 1) < tc1; t += 4 * U) {
-    float2 kk[U], vv[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const size_t off = head_base + size_t(t + 4 * u) * D + 2 * lane;
-      if (KV_BF16) {
-        const uint32_t kb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.k_cache) + off);
-        const uint32_t vb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.v_cache) + off);
-        kk[u] = make_float2(__uint_as_float(kb << 16), __uint_as_float(kb & 0xFFFF0000u));
-        vv[u] = make_float2(__uint_as_float(vb << 16), __uint_as_float(vb & 0xFFFF0000u));
-      } else {
-        kk[u] = *reinterpret_cast<const float2*>(static_cast<const float*>(p.k_cache) + off);
-        vv[u] = *reinterpret_cast<const float2*>(static_cast<const float*>(p.v_cache) + off);
+    for (int r = 0; r < RR; r++) {
+      const uint32_t row = row0 + r;
+      if (row < p.rows) {
+        if (EPI == kStore) p.out[row] = acc[r];
+        else p.out[row] += acc[r];
       }
     }
+  } else if (EPI == kSiluPair) {
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-#pragma unroll
-      for (int j = 0; j < G; j++) {
-        const float sc = wave_sum(q2[j].x * kk[u].x + q2[j].y * kk[u].y) * p.scale;
-        const float mn = fmaxf(m[j], sc);
-        const float co = expf(m[j] - mn), pe = expf(sc - mn);
-        l[j] = l[j] * co + pe;
-        acc[j].x = acc[j].x * co + pe * vv[u].x;
-        acc[j].y = acc[j].y * co + pe * vv[u].y;
-        m[j] = mn;
+    for (int r = 0; r + 1 < RR; r += 2) {
+      const uint32_t row = row0 + r;
+      if (row + 1 < p.rows) {
+        const float g = acc[r];
+        p.out[row >> 1] = g / (1.0f + expf(-g)) * acc[r + 1];
       }
     }
   }
-  for (; t < tc1 + (owns_new ? 1u : 0u); t += 4) {
-    float2 kk, vv;
-    if (owns_new && t == tc1) {
-      kk = make_float2(knew[2 * lane], knew[2 * lane + 1]);
-      vv = make_float2(vnew[2 * lane], vnew[2 * lane + 1]);
-    } else {
-      const size_t off = head_base + size_t(t) * D + 2 * lane;
-      if (KV_BF16) {
-        const uint32_t kb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.k_cache) + off);
-        const uint32_t vb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.v_cache) + off);
-        kk = make_float2(__uint_as_float(kb << 16), __uint_as_float(kb & 0xFFFF0000u));
-        vv = make_float2(__uint_as_float(vb << 16), __uint_as_float(vb & 0xFFFF0000u));
-      } else {
-        kk = *reinterpret_cast<const float2*>(static_cast<const float*>(p.k_cache) + off);
-        vv = *reinterpret_cast<const float2*>(static_cast<const float*>(p.v_cache) + off);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < G; j++) {
-      const float sc = wave_sum(q2[j].x * kk.x + q2[j].y * kk.y) * p.scale;
-      const float mn = fmaxf(m[j], sc);
-      const float co = expf(m[j] - mn), pe = expf(sc - mn);
-      l[j] = l[j] * co + pe;
-      acc[j].x = acc[j].x * co + pe * vv.x;
-      acc[j].y = acc[j].y * co + pe * vv.y;
-      m[j] = mn;
-    }
-  }
-
-  // combine the 4 waves
-#pragma unroll
-  for (int j = 0; j < G; j++) {
-    if (lane == 0) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
-    wacc[wave][j][2 * lane] = acc[j].x;
-    wacc[wave][j][2 * lane + 1] = acc[j].y;
-  }
-  __syncthreads();
-  const uint32_t nsplit_f = nsplit;
-  float* part = p.partial + (size_t(g) * kAttnMaxSplits + s) * G * (2 + D);
-  for (int i = tid; i < G * D; i += 256) {
-    const int j = i / D, d = i % D;
-    float M = -INFINITY;
-    for (int w = 0; w < 4; w++) M = fmaxf(M, wm[w][j]);
-    float L = 0.f, A = 0.f;
-    for (int w = 0; w < 4; w++) {
-      const float e = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);
-      L += e * wl[w][j];
-      A += e * wacc[w][j][d];
-    }
-    if (nsplit_f == 1) {
-      p.att[(size_t(g) * G + j) * D + d] = A / L;
-    } else {
-      if (d == 0) { part[j * (2 + D)] = M; part[j * (2 + D) + 1] = L; }
-      part[j * (2 + D) + 2 + d] = A;
-    }
-  }
-  if (nsplit_f == 1) return;
-
-  // last split to arrive merges (release/acquire through device-scope fences)
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&p.counter[g], 1u) == nsplit_f - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const float* pg = p.partial + size_t(g) * kAttnMaxSplits * G * (2 + D);
-  for (int i = tid; i < G * D; i += 256) {
-    const int j = i / D, d = i % D;
-    float M = -INFINITY;
-    for (uint32_t q = 0; q < nsplit_f; q++) M = fmaxf(M, pg[(q * G + j) * (2 + D)]);
-    float L = 0.f, A = 0.f;
-    for (uint32_t q = 0; q < nsplit_f; q++) {
-      const float* pq = pg + (q * G + j) * (2 + D);
-      const float e = pq[0] == -INFINITY ? 0.f : expf(pq[0] - M);
-      L += e * pq[1];
-      A += e * pq[2 + d];
-    }
-    p.att[(size_t(g) * G + j) * D + d] = A / L;
-  }
-  if (tid == 0) atomicExch(&p.counter[g], 0u);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -428,9 +361,17 @@ __global__ __launch_bounds__(1024) void k_argmax(const ArgCand* __restrict__ can
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
-  for (uint32_t i = tid; i < n_cand; i += 1024) {
-    const ArgCand c = cand[i];
-    if (cand_better(c.v, c.i, bv, bi)) { bv = c.v; bi = c.i; }
+  constexpr int U = 16;  // candidates per thread loaded together, so their latencies overlap
+  for (uint32_t base = 0; base < n_cand; base += 1024u * U) {
+    ArgCand c[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t i = base + uint32_t(tid) + 1024u * u;
+      c[u] = i < n_cand ? cand[i] : ArgCand{-INFINITY, 0xFFFFFFFFu};
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (cand_better(c[u].v, c[u].i, bv, bi)) { bv = c[u].v; bi = c[u].i; }
   }
   for (int o = 1; o < 64; o <<= 1) {
     const float ov = __shfl_xor(bv, o);
@@ -493,6 +434,25 @@ hipError_t launch_mv(const MatvecParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int TPR, int CPT, int PRO, int EPI>
+hipError_t launch_wide(const MatvecParams& p, hipStream_t s) {
+  constexpr int RR = (EPI == kSiluPair || TPR <= 128) ? 2 : 1;
+  constexpr int rows_per_block = (256 / TPR) * RR;
+  const uint32_t blocks = ceil_div(p.rows, rows_per_block);
+  hipLaunchKernelGGL((k_mv_wide<TPR, CPT, RR, PRO, EPI>), dim3(blocks), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+template <int PRO, int EPI>
+hipError_t launch_wide_cols(const MatvecParams& p, hipStream_t s) {
+  const uint32_t nch = p.cols / 8;
+  if (nch <= 64) return launch_wide<64, 1, PRO, EPI>(p, s);
+  if (nch <= 128) return launch_wide<128, 1, PRO, EPI>(p, s);
+  if (nch <= 256) return launch_wide<256, 1, PRO, EPI>(p, s);
+  if (nch <= 512) return launch_wide<256, 2, PRO, EPI>(p, s);
+  return hipErrorInvalidValue;
+}
+
 template <int PRO, int EPI>
 hipError_t launch_mv_cpl(const MatvecParams& p, hipStream_t s) {
   const uint32_t nch = p.cols / 8;
@@ -531,25 +491,21 @@ hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipS
   if (prologue == kNorm && epilogue == kStore) return launch_mv_cpl<kNorm, kStore>(p, s);
   if (prologue == kNorm && epilogue == kSiluPair) return launch_mv_cpl<kNorm, kSiluPair>(p, s);
   if (prologue == kNorm && epilogue == kLogits) return launch_mv_cpl<kNorm, kLogits>(p, s);
+  if (prologue == kAttnMerge && epilogue == kResAdd) {
+    if (!p.attn_part || p.attn_splits == 0 || p.attn_group == 0 || p.cols % kHeadDim) return hipErrorInvalidValue;
+    return launch_mv_cpl<kAttnMerge, kResAdd>(p, s);
+  }
   return hipErrorInvalidValue;
 }
 
-hipError_t launch_attention(const AttnParams& p, uint32_t grid_splits, hipStream_t s) {
-  const uint32_t G = p.n_kv ? p.n_heads / p.n_kv : 0;
-  if (!p.n_kv || p.n_heads % p.n_kv || grid_splits == 0 || grid_splits > uint32_t(kAttnMaxSplits))
-    return hipErrorInvalidValue;
-  dim3 grid(p.n_kv, grid_splits);
-#define QE_ATT(GG)                                                                     \
-  if (G == GG) {                                                                       \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attention<GG, true>), grid, dim3(256), 0, s, p);  \
-    else hipLaunchKernelGGL((k_attention<GG, false>), grid, dim3(256), 0, s, p);           \
-    return hipGetLastError();                                                          \
-  }
-  QE_ATT(1)
-  QE_ATT(2)
-  QE_ATT(4)
-  QE_ATT(8)
-#undef QE_ATT
+hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue, hipStream_t s) {
+  if (p.cols % 8 || p.rows == 0 || p.cols == 0 || p.cols / 8 > 512) return hipErrorInvalidValue;
+  if (epilogue == kSiluPair && p.rows % 2) return hipErrorInvalidValue;
+  if (prologue == kCopy && epilogue == kStore) return launch_wide_cols<kCopy, kStore>(p, s);
+  if (prologue == kCopy && epilogue == kResAdd) return launch_wide_cols<kCopy, kResAdd>(p, s);
+  if (prologue == kNorm && epilogue == kStore) return launch_wide_cols<kNorm, kStore>(p, s);
+  if (prologue == kEmbedNorm && epilogue == kStore) return launch_wide_cols<kEmbedNorm, kStore>(p, s);
+  if (prologue == kNorm && epilogue == kSiluPair) return launch_wide_cols<kNorm, kSiluPair>(p, s);
   return hipErrorInvalidValue;
 }
 
