@@ -140,12 +140,11 @@ def main():
     K, W = args.steps, args.warmup
     P = args.prompt_len
 
-    # warm-up: prefill + W decode steps on a throwaway cache
-    wc = qe.KVCache(model, P + W + 1, kv_dtype)
+    # warm-up: prefill + W decode steps on a throwaway cache (kept for the per-kernel profile)
+    n_prof = 8
+    wc = qe.KVCache(model, P + max(W, n_prof) + 1, kv_dtype)
     logits = model.prefill(prompt, 0, wc)
-    if W:
-        model.decode(int(np.argmax(logits)), P, W, wc)
-    del wc
+    warm_tokens, _ = model.decode(int(np.argmax(logits)), P, max(W, n_prof), wc)
 
     # timed: fresh cache, prefill, then exactly K decode steps
     cache = qe.KVCache(model, P + K + 1, kv_dtype)
@@ -179,6 +178,39 @@ def main():
     ms_per_step = wall / K * 1e3
     per_token_gpu_s = gpu_s / K
     achieved_gbs = avg_bytes / per_token_gpu_s / 1e9
+
+    # per-kernel durations from HIP events between the launches of one step (n_prof steps on the
+    # warm cache), and each stage's algorithmic bytes per launch
+    stages = {}
+    prof_positions = list(range(P, P + n_prof))
+    for i, pos in enumerate(prof_positions):
+        for name, us in model.profile_step(warm_tokens[i], pos, wc):
+            stages.setdefault(name, []).append(us)
+    del wc
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    QD, KD, L = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim, cfg.num_hidden_layers
+    el = 2 if kv_dtype == qe.QE_KV_BF16 else 4
+    mean_pos = sum(prof_positions) / n_prof
+    stage_bytes = {  # weights + activations in/out per launch (out*in*2 + in*4 + out*4 for a matvec)
+        "embed": H * 2 + H * 4,
+        "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
+        "attention": 2 * KD * (mean_pos + 1) * el + (QD + 2 * KD) * 4 + QD * 4,
+        "o_proj": H * QD * 2 + QD * 4 + 2 * H * 4,
+        "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
+        "down": H * I * 2 + I * 4 + 2 * H * 4,
+        "lm_head": V * H * 2 + H * 2 + H * 4 + V * 4,
+        "argmax": 8 * ((V + 15) // 16),
+    }
+    kernel_table = {}
+    for name, durs in stages.items():
+        per_step = len(durs) / n_prof
+        mean_us = sum(durs) / len(durs)
+        b = stage_bytes.get(name, 0)
+        kernel_table[name] = {"launches_per_step": per_step, "mean_us": round(mean_us, 3),
+                              "us_per_step": round(mean_us * per_step, 2), "bytes_per_launch": int(b),
+                              "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
+    dom_name = max(kernel_table, key=lambda k: kernel_table[k]["us_per_step"])
+    dom = kernel_table[dom_name]
 
     # token parity against the oracle's committed run of the same workload
     parity = None
@@ -215,17 +247,28 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
+            "achieved": dom["achieved_gbs"],
+            "peak": SPEC_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["achieved_gbs"] / SPEC_HBM_GBS, 4),
+            "traffic": None,
+            "kernel": dom_name,
+            "bytes_per_launch": dom["bytes_per_launch"],
+            "launch_us": dom["mean_us"],
+            "launches_per_step": dom["launches_per_step"],
+            "measured_ceiling_gbs": round(ceiling, 1),
+        },
+        "roofline_step": {
+            "bound": "hbm",
             "achieved": round(achieved_gbs, 1),
             "peak": SPEC_HBM_GBS,
             "unit": "GB/s",
             "frac": round(achieved_gbs / SPEC_HBM_GBS, 4),
-            "traffic": None,
-            "kernel": "decode step (one hipGraph replay per token)",
-            "bytes_per_launch": int(round(avg_bytes)),
-            "launch_us": round(per_token_gpu_s * 1e6, 2),
-            "measured_ceiling_gbs": round(ceiling, 1),
             "frac_of_measured": round(achieved_gbs / ceiling, 4),
+            "bytes_per_token": int(round(avg_bytes)),
+            "gpu_us_per_token": round(per_token_gpu_s * 1e6, 2),
         },
+        "kernels": kernel_table,
         "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
         "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),
         "weight_bytes_per_token": weight_bytes,

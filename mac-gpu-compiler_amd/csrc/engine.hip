@@ -332,7 +332,17 @@ uint64_t qe_kv_bytes_at(const qe_model* model, uint64_t pos, int kv_dtype) {
 namespace {
 
 // Enqueue one decode step (reads tokens[tok_idx] at state.pos) on the model stream.
-int enqueue_step(qe_model* m, qe_kv* kv) {
+// Timing marks for qe_profile_step: an event recorded before each kernel launch (and one after
+// the last), with the stage name of the kernel that follows it.
+struct Marks {
+  std::vector<hipEvent_t> events;
+  std::vector<const char*> names;
+  ~Marks() {
+    for (auto e : events) (void)hipEventDestroy(e);
+  }
+};
+
+int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -340,12 +350,24 @@ int enqueue_step(qe_model* m, qe_kv* kv) {
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
   const bool narrow = kv->narrow_kernels;
   hipStream_t s = m->stream;
+  auto mark = [&](const char* name) -> hipError_t {
+    if (!marks) return hipSuccess;
+    hipEvent_t e;
+    hipError_t r = hipEventCreate(&e);
+    if (r != hipSuccess) return r;
+    marks->events.push_back(e);
+    marks->names.push_back(name);
+    return hipEventRecord(e, s);
+  };
   auto matvec = [&](const MatvecParams& p, int pro, int epi) {
     return narrow ? qe::launch_matvec(p, pro == qe::kEmbedNorm ? qe::kNorm : pro, epi, s)
                   : qe::launch_matvec_wide(p, pro, epi, s);
   };
   // the narrow kernels have no embedding prologue: a separate embed kernel fills x first
-  if (narrow) HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
+  if (narrow) {
+    HIP_TRY(mark("embed"));
+    HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
+  }
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     MatvecParams p{};
@@ -354,6 +376,7 @@ int enqueue_step(qe_model* m, qe_kv* kv) {
     // (cpu_inference.rs:129-132)
     p.w = w.w_qkv; p.x = m->x; p.nw = w.w_in; p.rows = QD + 2 * KD; p.cols = H; p.out = m->qkv;
     p.embed = m->embed; p.tokens = kv->tokens; p.state = kv->state; p.vocab = V; p.x_out = m->x; p.err = m->err;
+    HIP_TRY(mark("qkv"));
     HIP_TRY(matvec(p, l == 0 ? qe::kEmbedNorm : qe::kNorm, qe::kStore));
     // q/k norm + RoPE, K/V append, attention (cpu_inference.rs:134-162)
     AttnParams a{};
@@ -367,32 +390,41 @@ int enqueue_step(qe_model* m, qe_kv* kv) {
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
     if (narrow) {
+      HIP_TRY(mark("attention"));
       HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
       // o_proj + residual (cpu_inference.rs:163-164)
+      HIP_TRY(mark("o_proj"));
       HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
     } else {
+      HIP_TRY(mark("attention"));
       HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
       // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
       p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
       p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
+      HIP_TRY(mark("o_proj"));
       HIP_TRY(qe::launch_matvec(p, qe::kAttnMerge, qe::kResAdd, s));
     }
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
     p.eps = c.rms_norm_eps;
     p.w = w.w_gu; p.x = m->x; p.nw = w.w_post; p.rows = 2 * I; p.cols = H; p.out = m->h;
+    HIP_TRY(mark("gate_up"));
     HIP_TRY(matvec(p, qe::kNorm, qe::kSiluPair));
     // down_proj + residual (cpu_inference.rs:171-172)
     p = MatvecParams{};
     p.w = w.w_down; p.x = m->h; p.rows = H; p.cols = I; p.out = m->x;
+    HIP_TRY(mark("down"));
     HIP_TRY(matvec(p, qe::kCopy, qe::kResAdd));
   }
   // final norm + lm_head + greedy candidates (cpu_inference.rs:175-178), then argmax
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
+  HIP_TRY(mark("lm_head"));
   HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  HIP_TRY(mark("argmax"));
   HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err, s));
+  HIP_TRY(mark(nullptr));
   return QE_OK;
 }
 
@@ -516,6 +548,30 @@ int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* 
   HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
   if ((rc = check_err(model))) return rc;
   memcpy(logits_out, model->h_logits, V * 4);
+  kv->len = pos + 1;
+  return QE_OK;
+}
+
+int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out, const char** names_out,
+                    uint32_t max_kernels, uint32_t* n_out) {
+  if (!model || !kv || !us_out || !n_out) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (pos >= kv->max_seq) return fail(QE_ERR_POS, "pos %llu exceeds KV cache size %llu", (unsigned long long)pos, (unsigned long long)kv->max_seq);
+  if (pos > kv->len) return fail(QE_ERR_POS, "pos %llu is past the %llu cached positions", (unsigned long long)pos, (unsigned long long)kv->len);
+  if (token >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab", token);
+  int rc = set_state(model, kv, token, pos);
+  if (rc) return rc;
+  Marks marks;
+  if ((rc = enqueue_step(model, kv, &marks))) return rc;
+  if ((rc = check_err(model))) return rc;
+  const uint32_t n = uint32_t(marks.events.size()) - 1;
+  *n_out = n;
+  for (uint32_t i = 0; i < n && i < max_kernels; i++) {
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, marks.events[i], marks.events[i + 1]));
+    us_out[i] = ms * 1e3f;
+    if (names_out) names_out[i] = marks.names[i];
+  }
   kv->len = pos + 1;
   return QE_OK;
 }

@@ -126,6 +126,8 @@ def lib() -> ctypes.CDLL:
         "qe_kv_len": (u64, [vp]),
         "qe_forward": (i32, [vp, u32, u64, vp, f32p]),
         "qe_prefill": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, f32p]),
+        "qe_profile_step": (i32, [vp, u32, u64, vp, f32p, ctypes.POINTER(ctypes.c_char_p), u32,
+                                  ctypes.POINTER(u32)]),
         "qe_decode": (i32, [vp, u32, u64, u64, vp, ON_TOKEN, vp, f32p]),
         "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
         "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
@@ -191,6 +193,16 @@ class Model:
         _check(lib().qe_prefill(self._h, arr.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), arr.size, int(start_pos),
                                 cache._h, _fptr(out) if out is not None else None))
         return out
+
+    def profile_step(self, token: int, pos: int, cache: "KVCache"):
+        """One decode step launched kernel by kernel with HIP events between them:
+        returns [(stage name, microseconds)] in launch order."""
+        cap = 4096
+        us = np.empty(cap, dtype=np.float32)
+        names = (ctypes.c_char_p * cap)()
+        n = ctypes.c_uint32(0)
+        _check(lib().qe_profile_step(self._h, int(token), int(pos), cache._h, _fptr(us), names, cap, ctypes.byref(n)))
+        return [(names[i].decode(), float(us[i])) for i in range(min(n.value, cap))]
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",
                on_token: Optional[Callable[[int], None]] = None, want_logits: bool = False):
