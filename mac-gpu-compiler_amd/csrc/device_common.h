@@ -53,6 +53,15 @@ __device__ __forceinline__ float wave_sum(float v) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
+// Sum over each aligned group of 8 lanes, returned to the 8 lanes of the group
+// (quad xor1, quad xor2, half-row mirror).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  return v;
+}
+
 // a beats b: larger value, or equal value and lower index (first maximum wins, main.rs:37-42)
 __device__ __forceinline__ bool cand_better(float av, uint32_t ai, float bv, uint32_t bi) {
   return av > bv || (av == bv && ai < bi);

@@ -104,6 +104,7 @@ struct qe_kv {
   void* k = nullptr;       // [L][n_kv][max_seq][D]
   void* v = nullptr;
   float* rope = nullptr;   // [max_seq][D/2][2]
+  float* rope_cur = nullptr;  // [D/2][2]: the row of the current position (split attention)
   StepState* state = nullptr;
   uint32_t* tokens = nullptr;       // device token ring [tok_cap]
   uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
@@ -380,7 +381,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
     HIP_TRY(matvec(p, l == 0 ? qe::kEmbedNorm : qe::kNorm, qe::kStore));
     // q/k norm + RoPE, K/V append, attention (cpu_inference.rs:134-162)
     AttnParams a{};
-    a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
+    a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope; a.rope_cur = kv->rope_cur;
     a.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
     a.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
     a.partial = m->attn_part; a.counter = m->attn_cnt; a.att = m->att; a.state = kv->state; a.err = m->err;
@@ -402,7 +403,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
       p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
       p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
       HIP_TRY(mark("o_proj"));
-      HIP_TRY(qe::launch_matvec(p, qe::kAttnMerge, qe::kResAdd, s));
+      HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
     }
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
@@ -423,19 +424,23 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
   HIP_TRY(mark("lm_head"));
   HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
   HIP_TRY(mark("argmax"));
-  HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err, s));
+  HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err, kv->rope,
+                            kv->rope_cur, D / 2, s));
   HIP_TRY(mark(nullptr));
   return QE_OK;
 }
 
-// host -> device: state {pos, tok_idx = 0} and tokens[0] = token, through pinned staging
+// host -> device: state {pos, tok_idx = 0} and tokens[0] = token, through pinned staging; the
+// RoPE row of pos becomes rope_cur (k_argmax advances it with pos after every step)
 int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
   HIP_TRY(hipStreamSynchronize(m->stream));
   StepState st{uint32_t(pos), 0u, uint32_t(kv->max_seq), kv->tok_cap};
   memcpy(m->h_small, &st, sizeof(st));
   m->h_small[8] = token;
+  const size_t D = m->cfg.head_dim;
   HIP_TRY(hipMemcpyAsync(kv->state, m->h_small, sizeof(st), hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipMemcpyAsync(kv->tokens, m->h_small + 8, 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipMemcpyAsync(kv->rope_cur, kv->rope + pos * D, D * 4, hipMemcpyDeviceToDevice, m->stream));
   return QE_OK;
 }
 
@@ -473,14 +478,15 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   const size_t rope_bytes = max_seq * D * 4;
   size_t off = 0;
   auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
-  const size_t ok_ = take(kv_bytes), ov = take(kv_bytes), orope = take(rope_bytes), ost = take(sizeof(StepState)),
-               otok = take(size_t(kv->tok_cap) * 4);
+  const size_t ok_ = take(kv_bytes), ov = take(kv_bytes), orope = take(rope_bytes), ocur = take(D * 4),
+               ost = take(sizeof(StepState)), otok = take(size_t(kv->tok_cap) * 4);
   HIP_TRY(hipSetDevice(model->device));
   HIP_TRY(hipMalloc(&kv->mem, off));
   HIP_TRY(hipMemsetAsync(kv->mem, 0, off, model->stream));
   kv->k = kv->mem + ok_;
   kv->v = kv->mem + ov;
   kv->rope = reinterpret_cast<float*>(kv->mem + orope);
+  kv->rope_cur = reinterpret_cast<float*>(kv->mem + ocur);
   kv->state = reinterpret_cast<StepState*>(kv->mem + ost);
   kv->tokens = reinterpret_cast<uint32_t*>(kv->mem + otok);
   HIP_TRY(hipHostMalloc(&kv->host_tokens, size_t(kv->tok_cap) * 4, hipHostMallocDefault));

@@ -50,10 +50,8 @@ struct MatvecParams {
   uint32_t vocab;
   float* x_out;          // the embedding row is also written here (the residual stream)
   uint32_t* err;
-  uint32_t x_rep;        // copies of x to spread reads over (0/1: one)
-  uint32_t x_rep_stride; // floats between copies
   // prologue kAttnMerge: x[h*128 + d] is merged from attention split partials
-  const float* attn_part;  // [n_kv][attn_splits][group][2 + 128]
+  const float* attn_part;  // [n_kv][attn_splits][group][kPartStride]
   uint32_t attn_splits, attn_group;
 };
 
@@ -65,7 +63,8 @@ struct AttnParams {
   const uint16_t* q_norm;  // bf16 [D]
   const uint16_t* k_norm;  // bf16 [D]
   const float* rope;       // [max_seq][D/2][2] (cos, sin)
-  void* k_cache;           // layer base, [n_kv][max_seq][D], f32 or bf16
+  const float* rope_cur;   // [D/2][2]: the rope row of state->pos (split kernel)
+  void* k_cache;          // layer base, [n_kv][max_seq][D], f32 or bf16
   void* v_cache;
   float* partial;          // [n_kv][kAttnMaxSplits][group][2 + D]
   uint32_t* counter;       // [n_kv] split arrival counters (zero between launches)
@@ -99,8 +98,11 @@ constexpr int kAttnMaxMergeSplits = 16;
 // one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
 constexpr int kPartStride = 4 + kHeadDim;
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s);
+// Greedy token from the lm_head candidates; advances the step state and, with `rope`, copies the
+// RoPE row of the next position ([half] (cos, sin) pairs) to rope_cur for the next step.
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,
-                         uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, hipStream_t s);
+                         uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, const float* rope,
+                         float* rope_cur, uint32_t half, hipStream_t s);
 hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, hipStream_t s);
 
 }  // namespace qe

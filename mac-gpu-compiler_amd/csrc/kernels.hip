@@ -49,69 +49,24 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
   const uint32_t row0 = (blockIdx.x * 4u + uint32_t(wave)) * R;
   const uint4* W = reinterpret_cast<const uint4*>(p.w);
 
+  // unconditional loads (a load behind a divergent branch is waited for on the spot): chunk
+  // indexes past the row end re-read the last chunk and are skipped in the dot product
   uint4 wv[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; r++) {
     const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);  // past the end: re-read the last row
     const uint4* wr = W + size_t(row) * nch;
 #pragma unroll
-    for (int k = 0; k < CPL; k++) {
-      const uint32_t c = uint32_t(lane) + 64u * k;
-      wv[r][k] = c < nch ? wr[c] : make_uint4(0, 0, 0, 0);
-    }
+    for (int k = 0; k < CPL; k++) wv[r][k] = wr[min(uint32_t(lane) + 64u * k, nch - 1)];
   }
 
   const float4* x4 = reinterpret_cast<const float4*>(p.x);
   float4* xs4 = reinterpret_cast<float4*>(xs);
   float ss = 0.f;
-  if (PRO == kAttnMerge) {
-    // xin[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s, e_s = exp(m_s - max_s m_s), over the
-    // attention split partials [n_kv][splits][group][m, l, acc[128]]; empty splits (m = -inf)
-    // add 0. Thread -> 8 consecutive dims of one head; all of its split loads are issued before
-    // any is used (splits <= kAttnMaxMergeSplits).
-    constexpr int SM = kAttnMaxMergeSplits, PS = kPartStride;
-    const uint32_t G = p.attn_group, S = p.attn_splits;
-    for (uint32_t i8 = tid; i8 < p.cols / 8; i8 += 256) {
-      const uint32_t h = i8 / (kHeadDim / 8), d0 = (i8 % (kHeadDim / 8)) * 8, g = h / G, j = h % G;
-      const float* pg = p.attn_part + size_t(g) * S * G * PS + j * PS;
-      float mv[SM], lv[SM];
-      float4 a0[SM], a1[SM];
-#pragma unroll
-      for (int s = 0; s < SM; s++) {
-        if (s < int(S)) {
-          const float* q = pg + size_t(s) * G * PS;
-          mv[s] = q[0];
-          lv[s] = q[1];
-          a0[s] = *reinterpret_cast<const float4*>(q + 4 + d0);
-          a1[s] = *reinterpret_cast<const float4*>(q + 4 + d0 + 4);
-        } else {
-          mv[s] = -INFINITY;
-        }
-      }
-      float M = -INFINITY;
-#pragma unroll
-      for (int s = 0; s < SM; s++) M = fmaxf(M, mv[s]);
-      float L = 0.f;
-      float4 A0 = make_float4(0, 0, 0, 0), A1 = A0;
-#pragma unroll
-      for (int s = 0; s < SM; s++) {
-        if (mv[s] != -INFINITY) {
-          const float e = expf(mv[s] - M);
-          L += e * lv[s];
-          A0.x += e * a0[s].x; A0.y += e * a0[s].y; A0.z += e * a0[s].z; A0.w += e * a0[s].w;
-          A1.x += e * a1[s].x; A1.y += e * a1[s].y; A1.z += e * a1[s].z; A1.w += e * a1[s].w;
-        }
-      }
-      const float inv = 1.0f / L;
-      xs4[2 * i8] = make_float4(A0.x * inv, A0.y * inv, A0.z * inv, A0.w * inv);
-      xs4[2 * i8 + 1] = make_float4(A1.x * inv, A1.y * inv, A1.z * inv, A1.w * inv);
-    }
-  } else {
-    for (uint32_t i = tid; i < p.cols / 4; i += 256) {
-      float4 v = x4[i];
-      xs4[i] = v;
-      if (PRO == kNorm) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-    }
+  for (uint32_t i = tid; i < p.cols / 4; i += 256) {
+    float4 v = x4[i];
+    xs4[i] = v;
+    if (PRO == kNorm) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   }
   if (PRO == kNorm) {
     ss = wave_sum(ss);
@@ -208,71 +163,143 @@ __global__ __launch_bounds__(256) void k_matvec_generic(MatvecParams p) {
 // row) and normalizes them, (x * s) * gain (cpu_inference.rs:189-194).
 // Prologue kEmbedNorm: x is the bf16 embedding row of the step's token (inference.metal:98-107),
 // which workgroup 0 also stores to x_out for the residual stream.
+// Prologue kAttnMerge: x[h*128 + d] is the attention output merged from the split partials
+// [n_kv][splits][group][kPartStride] of the split attention kernel; each thread merges exactly
+// the 8 dims of its own chunks, so no LDS is involved (SM >= splits partials are loaded).
+// Every load is unconditional (chunk indexes past the row end re-read the last chunk and get
+// x = 0) and all of them are issued before the first use: a load behind a divergent branch
+// makes the compiler wait for it before issuing the next one. Inputs that come from L2 (x,
+// gains, partials) are issued before the weights, which stream from HBM, so that prologue
+// arithmetic overlaps the weight transfer; the embedding row depends on the token and goes last.
 // ---------------------------------------------------------------------------------------------
-template <int TPR, int CPT, int RR, int PRO, int EPI>
+template <int TPR, int CPT, int RR, int PRO, int EPI, int SM = 1>
 __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
   constexpr int NG = 256 / TPR;          // row groups per workgroup
   constexpr int WPG = TPR / 64;          // waves per row group
+  constexpr bool NORM = PRO == kNorm || PRO == kEmbedNorm;
   __shared__ float red[4][RR + 1];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = tid / TPR, t = tid % TPR;
   const uint32_t nch = p.cols >> 3;
   const uint32_t row0 = (blockIdx.x * NG + uint32_t(grp)) * RR;
   const uint4* W = reinterpret_cast<const uint4*>(p.w);
+  uint32_t cc[CPT];  // clamped chunk index
+#pragma unroll
+  for (int k = 0; k < CPT; k++) cc[k] = min(uint32_t(t) + uint32_t(TPR) * k, nch - 1);
 
   uint4 wv[RR][CPT];
+  auto load_weights = [&]() {
 #pragma unroll
-  for (int r = 0; r < RR; r++) {
-    const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);
+    for (int r = 0; r < RR; r++) {
+      const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);
 #pragma unroll
-    for (int k = 0; k < CPT; k++) {
-      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
-      wv[r][k] = c < nch ? W[size_t(row) * nch + c] : make_uint4(0, 0, 0, 0);
+      for (int k = 0; k < CPT; k++) wv[r][k] = W[size_t(row) * nch + cc[k]];
     }
-  }
-
-  // RMSNorm gains do not depend on x: load them with the weights, off the critical path
+  };
   uint4 gains[CPT];
-  if (PRO != kCopy) {
+  auto load_gains = [&]() {
     const uint4* NWv = reinterpret_cast<const uint4*>(p.nw);
 #pragma unroll
-    for (int k = 0; k < CPT; k++) {
-      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
-      gains[k] = c < nch ? NWv[c] : make_uint4(0, 0, 0, 0);
+    for (int k = 0; k < CPT; k++) gains[k] = NWv[cc[k]];
+  };
+
+  // residual rows (epilogue kResAdd: out += acc), read up front instead of after the reduction
+  float res[RR];
+  auto load_res = [&]() {
+    if constexpr (EPI == kResAdd) {
+#pragma unroll
+      for (int r = 0; r < RR; r++) res[r] = p.out[min(row0 + uint32_t(r), p.rows - 1)];
     }
-  }
+  };
+
+  // Loads first, then a scheduling barrier: without it the scheduler sinks loads towards their
+  // uses (to save registers), behind waits for the earlier ones.
   float4 xa[CPT], xb[CPT];
-  if (PRO == kEmbedNorm) {
+  if constexpr (PRO == kEmbedNorm) {
+    load_weights();
+    load_gains();
+    load_res();
     uint32_t tok = p.tokens[p.state->tok_idx];
     if (tok >= p.vocab) {
       if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
       tok = 0;
     }
     const uint4* E = reinterpret_cast<const uint4*>(p.embed) + size_t(tok) * nch;
+    uint4 e[CPT];
+#pragma unroll
+    for (int k = 0; k < CPT; k++) e[k] = E[cc[k]];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
+      xa[k] = make_float4(__uint_as_float(e[k].x << 16), __uint_as_float(e[k].x & 0xFFFF0000u),
+                          __uint_as_float(e[k].y << 16), __uint_as_float(e[k].y & 0xFFFF0000u));
+      xb[k] = make_float4(__uint_as_float(e[k].z << 16), __uint_as_float(e[k].z & 0xFFFF0000u),
+                          __uint_as_float(e[k].w << 16), __uint_as_float(e[k].w & 0xFFFF0000u));
       const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
-      const uint4 e = c < nch ? E[c] : make_uint4(0, 0, 0, 0);
-      xa[k] = make_float4(__uint_as_float(e.x << 16), __uint_as_float(e.x & 0xFFFF0000u),
-                          __uint_as_float(e.y << 16), __uint_as_float(e.y & 0xFFFF0000u));
-      xb[k] = make_float4(__uint_as_float(e.z << 16), __uint_as_float(e.z & 0xFFFF0000u),
-                          __uint_as_float(e.w << 16), __uint_as_float(e.w & 0xFFFF0000u));
       if (blockIdx.x == 0 && grp == 0 && c < nch) {
         float4* xo = reinterpret_cast<float4*>(p.x_out);
         xo[2 * c] = xa[k];
         xo[2 * c + 1] = xb[k];
       }
     }
-  } else {
-    // x_rep > 1: the producer wrote x_rep copies of x, x_rep_stride floats apart; workgroups
-    // spread their reads over the copies instead of all hitting the same lines
-    const float* xsrc = p.x_rep > 1 ? p.x + size_t(blockIdx.x % p.x_rep) * p.x_rep_stride : p.x;
-    const float4* x4 = reinterpret_cast<const float4*>(xsrc);
+  } else if constexpr (PRO == kAttnMerge) {
+    // out_h = sum_s e_s acc_s / sum_s e_s l_s with e_s = exp(m_s - max m); empty runs (m = -inf)
+    // and loads past the last split (s >= splits re-read the last one) weigh 0
+    const uint32_t G = p.attn_group, S = p.attn_splits;
+    float2 ml[CPT][SM];
+    float4 a0[CPT][SM], a1[CPT][SM];
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
-      const uint32_t c = uint32_t(t) + uint32_t(TPR) * k;
-      xa[k] = c < nch ? x4[2 * c] : make_float4(0, 0, 0, 0);
-      xb[k] = c < nch ? x4[2 * c + 1] : make_float4(0, 0, 0, 0);
+      const uint32_t h = cc[k] >> 4, d0 = (cc[k] & 15) * 8, g = h / G, j = h % G;
+      const float* base = p.attn_part + (size_t(g) * S * G + j) * kPartStride;
+#pragma unroll
+      for (int s = 0; s < SM; s++) {
+        const float* q = base + size_t(min(uint32_t(s), S - 1)) * G * kPartStride;
+        ml[k][s] = *reinterpret_cast<const float2*>(q);
+        a0[k][s] = *reinterpret_cast<const float4*>(q + 4 + d0);
+        a1[k][s] = *reinterpret_cast<const float4*>(q + 8 + d0);
+      }
+    }
+    load_res();
+    load_weights();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int s = 0; s < SM; s++) M = uint32_t(s) < S ? fmaxf(M, ml[k][s].x) : M;
+      float L = 0.f;
+      float4 A0 = make_float4(0.f, 0.f, 0.f, 0.f), A1 = A0;
+#pragma unroll
+      for (int s = 0; s < SM; s++) {
+        const float e = (uint32_t(s) < S && ml[k][s].x != -INFINITY) ? expf(ml[k][s].x - M) : 0.f;
+        L += e * ml[k][s].y;
+        A0.x += e * a0[k][s].x; A0.y += e * a0[k][s].y; A0.z += e * a0[k][s].z; A0.w += e * a0[k][s].w;
+        A1.x += e * a1[k][s].x; A1.y += e * a1[k][s].y; A1.z += e * a1[k][s].z; A1.w += e * a1[k][s].w;
+      }
+      const float inv = 1.0f / L;
+      xa[k] = make_float4(A0.x * inv, A0.y * inv, A0.z * inv, A0.w * inv);
+      xb[k] = make_float4(A1.x * inv, A1.y * inv, A1.z * inv, A1.w * inv);
+    }
+  } else {
+    const float4* x4 = reinterpret_cast<const float4*>(p.x);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      xa[k] = x4[2 * cc[k]];
+      xb[k] = x4[2 * cc[k] + 1];
+    }
+    if constexpr (NORM) load_gains();
+    load_res();
+    load_weights();
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (uint32_t(TPR) * CPT > nch) {  // chunks past the row end contribute 0
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      const bool in = uint32_t(t) + uint32_t(TPR) * k < nch;
+      const float z = 0.f;
+      xa[k] = make_float4(in ? xa[k].x : z, in ? xa[k].y : z, in ? xa[k].z : z, in ? xa[k].w : z);
+      xb[k] = make_float4(in ? xb[k].x : z, in ? xb[k].y : z, in ? xb[k].z : z, in ? xb[k].w : z);
     }
   }
   // RMSNorm: the scale s is a scalar, so sum_c W[r,c] * ((x_c * s) * g_c) is evaluated as
@@ -280,7 +307,7 @@ __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
   // instead of in front of them (a reassociation of the reference's f32 product, well inside
   // the logit tolerance)
   float ss = 0.f;
-  if (PRO != kCopy) {
+  if constexpr (NORM) {
 #pragma unroll
     for (int k = 0; k < CPT; k++) {
       ss += (xa[k].x * xa[k].x + xa[k].y * xa[k].y + xa[k].z * xa[k].z + xa[k].w * xa[k].w) +
@@ -305,7 +332,7 @@ __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
     for (int k = 0; k < CPT; k++) acc[r] = dot8(wv[r][k], xa[k], xb[k], acc[r]);
     acc[r] = wave_sum(acc[r]);
   }
-  if (PRO != kCopy) ss = wave_sum(ss);
+  if constexpr (NORM) ss = wave_sum(ss);
   if (WPG > 1) {
     if (lane == 0) {
 #pragma unroll
@@ -322,7 +349,7 @@ __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
       else ss = v;
     }
   }
-  if (PRO != kCopy) {
+  if constexpr (NORM) {
     const float s = 1.0f / sqrtf(ss / float(p.cols) + p.eps);
 #pragma unroll
     for (int r = 0; r < RR; r++) acc[r] *= s;
@@ -334,7 +361,7 @@ __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
       const uint32_t row = row0 + r;
       if (row < p.rows) {
         if (EPI == kStore) p.out[row] = acc[r];
-        else p.out[row] += acc[r];
+        else p.out[row] = res[r] + acc[r];
       }
     }
   } else if (EPI == kSiluPair) {
@@ -355,20 +382,27 @@ __global__ __launch_bounds__(256) void k_mv_wide(MatvecParams p) {
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(1024) void k_argmax(const ArgCand* __restrict__ cand, uint32_t n_cand,
                                                  const float* __restrict__ logits, StepState* st,
-                                                 uint32_t* tokens, uint32_t* host_tokens, uint32_t* err) {
+                                                 uint32_t* tokens, uint32_t* host_tokens, uint32_t* err,
+                                                 const float* __restrict__ rope, float* rope_cur, uint32_t half) {
   __shared__ float sv[16];
   __shared__ uint32_t si[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // the RoPE row of the next position, which the next step's attention reads as rope_cur
+  const uint32_t next = st->pos + 1, max_seq = st->max_seq;
+  float2 rc = make_float2(0.f, 0.f);
+  if (rope) {
+    rc = reinterpret_cast<const float2*>(rope)[size_t(min(next, max_seq - 1)) * half + min(uint32_t(tid), half - 1)];
+  }
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
-  constexpr int U = 16;  // candidates per thread loaded together, so their latencies overlap
+  // candidates per thread loaded together, so their latencies overlap; indexes past the end
+  // re-read the last candidate, which cannot change the result
+  constexpr int U = 16;
   for (uint32_t base = 0; base < n_cand; base += 1024u * U) {
     ArgCand c[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const uint32_t i = base + uint32_t(tid) + 1024u * u;
-      c[u] = i < n_cand ? cand[i] : ArgCand{-INFINITY, 0xFFFFFFFFu};
-    }
+    for (int u = 0; u < U; u++) c[u] = cand[min(base + uint32_t(tid) + 1024u * u, n_cand - 1)];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; u++)
       if (cand_better(c[u].v, c[u].i, bv, bi)) { bv = c[u].v; bi = c[u].i; }
@@ -391,9 +425,10 @@ __global__ __launch_bounds__(1024) void k_argmax(const ArgCand* __restrict__ can
     } else {
       atomicOr(err, kErrRing);
     }
-    st->pos += 1;
+    st->pos = next;
     st->tok_idx = k;
   }
+  if (rope_cur && uint32_t(tid) < half && next < max_seq) reinterpret_cast<float2*>(rope_cur)[tid] = rc;
 }
 
 // streaming read (tests/read_bandwidth.rs:16-54): grid-stride float4, 4 accumulators
@@ -434,22 +469,41 @@ hipError_t launch_mv(const MatvecParams& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-template <int TPR, int CPT, int PRO, int EPI>
+template <int TPR, int CPT, int RR, int PRO, int EPI, int SM = 1>
 hipError_t launch_wide(const MatvecParams& p, hipStream_t s) {
-  constexpr int RR = (EPI == kSiluPair || TPR <= 128) ? 2 : 1;
   constexpr int rows_per_block = (256 / TPR) * RR;
   const uint32_t blocks = ceil_div(p.rows, rows_per_block);
-  hipLaunchKernelGGL((k_mv_wide<TPR, CPT, RR, PRO, EPI>), dim3(blocks), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((k_mv_wide<TPR, CPT, RR, PRO, EPI, SM>), dim3(blocks), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 
+// rows per row group: silu needs the (gate, up) pair; one-chunk rows of <= 128 threads take two
+template <int TPR, int CPT, int PRO, int EPI>
+hipError_t launch_wide_rr(const MatvecParams& p, hipStream_t s) {
+  constexpr int RR = (EPI == kSiluPair || (TPR <= 128 && CPT == 1)) ? 2 : 1;
+  return launch_wide<TPR, CPT, RR, PRO, EPI>(p, s);
+}
+
+// threads per row x chunks per thread: an exact fit where one exists, so no lane idles
 template <int PRO, int EPI>
 hipError_t launch_wide_cols(const MatvecParams& p, hipStream_t s) {
   const uint32_t nch = p.cols / 8;
-  if (nch <= 64) return launch_wide<64, 1, PRO, EPI>(p, s);
-  if (nch <= 128) return launch_wide<128, 1, PRO, EPI>(p, s);
-  if (nch <= 256) return launch_wide<256, 1, PRO, EPI>(p, s);
-  if (nch <= 512) return launch_wide<256, 2, PRO, EPI>(p, s);
+  if (nch <= 64) return launch_wide_rr<64, 1, PRO, EPI>(p, s);
+  if (nch <= 128) return launch_wide_rr<128, 1, PRO, EPI>(p, s);
+  if (nch <= 256) return launch_wide_rr<256, 1, PRO, EPI>(p, s);
+  if (nch == 384) return launch_wide_rr<128, 3, PRO, EPI>(p, s);
+  if (nch <= 512) return launch_wide_rr<256, 2, PRO, EPI>(p, s);
+  return hipErrorInvalidValue;
+}
+
+// attention merge + o_proj + residual: four rows per workgroup amortize the merge, which every
+// workgroup repeats for the whole input
+template <int SM>
+hipError_t launch_merge_cols(const MatvecParams& p, hipStream_t s) {
+  const uint32_t nch = p.cols / 8;
+  if (nch <= 128) return launch_wide<128, 1, 4, kAttnMerge, kResAdd, SM>(p, s);
+  if (nch <= 256) return launch_wide<256, 1, 4, kAttnMerge, kResAdd, SM>(p, s);
+  if (nch <= 512) return launch_wide<256, 2, 4, kAttnMerge, kResAdd, SM>(p, s);
   return hipErrorInvalidValue;
 }
 
@@ -491,10 +545,6 @@ hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipS
   if (prologue == kNorm && epilogue == kStore) return launch_mv_cpl<kNorm, kStore>(p, s);
   if (prologue == kNorm && epilogue == kSiluPair) return launch_mv_cpl<kNorm, kSiluPair>(p, s);
   if (prologue == kNorm && epilogue == kLogits) return launch_mv_cpl<kNorm, kLogits>(p, s);
-  if (prologue == kAttnMerge && epilogue == kResAdd) {
-    if (!p.attn_part || p.attn_splits == 0 || p.attn_group == 0 || p.cols % kHeadDim) return hipErrorInvalidValue;
-    return launch_mv_cpl<kAttnMerge, kResAdd>(p, s);
-  }
   return hipErrorInvalidValue;
 }
 
@@ -506,12 +556,23 @@ hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue,
   if (prologue == kNorm && epilogue == kStore) return launch_wide_cols<kNorm, kStore>(p, s);
   if (prologue == kEmbedNorm && epilogue == kStore) return launch_wide_cols<kEmbedNorm, kStore>(p, s);
   if (prologue == kNorm && epilogue == kSiluPair) return launch_wide_cols<kNorm, kSiluPair>(p, s);
+  if (prologue == kAttnMerge && epilogue == kResAdd) {
+    if (!p.attn_part || p.attn_splits == 0 || p.attn_splits > uint32_t(kAttnMaxMergeSplits) ||
+        p.attn_group == 0 || p.cols % kHeadDim)
+      return hipErrorInvalidValue;
+    if (p.attn_splits <= 4) return launch_merge_cols<4>(p, s);
+    if (p.attn_splits <= 8) return launch_merge_cols<8>(p, s);
+    return launch_merge_cols<16>(p, s);
+  }
   return hipErrorInvalidValue;
 }
 
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st, uint32_t* tokens,
-                         uint32_t* host_tokens, uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, cand, n_cand, logits, st, tokens, host_tokens, err);
+                         uint32_t* host_tokens, uint32_t* err, const float* rope, float* rope_cur, uint32_t half,
+                         hipStream_t s) {
+  if (n_cand == 0 || (rope && (half == 0 || half > 1024))) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_argmax, dim3(1), dim3(1024), 0, s, cand, n_cand, logits, st, tokens, host_tokens, err, rope,
+                     rope_cur, half);
   return hipGetLastError();
 }
 

@@ -75,6 +75,27 @@ def test_tiny_decode_matches_oracle(gpu, tiny_ckpt):
         assert toks[i] == tok, f"step {i}: gpu {toks[i]} oracle {tok}"
 
 
+@pytest.mark.parametrize("max_seq,n_pos", [(300, 290), (2100, 2050)])
+def test_tiny_long_cache_matches_oracle(gpu, tiny_ckpt, max_seq, n_pos):
+    # A cache of 300 positions is split into 5 runs of 60 (one tile each, runs past pos empty);
+    # 2100 positions give 16 runs of 132, i.e. three 64-position tiles per run, so the
+    # double-buffered tile loop and the 16-way merge in o_proj are both exercised.
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    cache = qe.KVCache(m, max_seq)
+    oc = om.new_cache()
+    prompt = qe.random_prompt(23, n_pos, TINY.vocab_size)
+    worst = 0.0
+    for pos, tok in enumerate(prompt):
+        a = om.forward(int(tok), pos, oc)
+        b = m.forward(int(tok), pos, cache)
+        d = float(np.max(np.abs(a - b)))
+        worst = max(worst, d)
+        assert d < 1e-4, f"pos {pos}: logits diverge by {d}"
+        assert oracle.argmax(a) == oracle.argmax(b), f"pos {pos}: different greedy token"
+    print(f"tiny model, cache {max_seq}, {n_pos} positions: worst max-abs {worst:.2e}")
+
+
 def test_prefill_equals_forward_loop(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     prompt = qe.random_prompt(17, 23, TINY.vocab_size)
