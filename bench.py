@@ -66,6 +66,42 @@ def measured_read_ceiling(torch, qe) -> float:
     return best
 
 
+def measured_copy(torch) -> float:
+    """A plain 1 GiB device copy (torch's elementwise copy kernel): GB/s moved (read + write).
+    Its known size (1 GiB read, 1 GiB written per launch) is also the scale for the rocprofv3
+    FETCH_SIZE / WRITE_SIZE counters of the traffic summary."""
+    n = (1 << 30) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    best = 0.0
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        best = max(best, 2 * (1 << 30) / (e0.elapsed_time(e1) * 1e-3) / 1e9)
+    del src, dst
+    torch.cuda.empty_cache()
+    return best
+
+
+def pmc_traffic(stage: str):
+    """HBM bytes per launch of `stage` from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the same counter's reading for the
+    1 GiB copy), or None when the summary does not cover that stage."""
+    path = os.path.join(ROOT, "profiles", "decode_step_qwen3_0_6b_pmc.json")
+    try:
+        with open(path) as f:
+            summary = json.load(f)
+    except (OSError, ValueError):
+        return None
+    row = summary.get("stages", {}).get(stage)
+    return int(row["traffic_bytes"]) if row and "traffic_bytes" in row else None
+
+
 def cpu_baseline(ckpt: str, prompt, target_s: float = 12.0):
     """The oracle (C restatement of cpu_inference.rs) on this host: a short prefill, then decode
     steps until ~target_s of decode work; tok/s over the decode steps."""
@@ -107,6 +143,8 @@ def main():
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
     ap.add_argument("--workdir", default=os.environ.get("QE_BENCH_DIR", "/tmp/qe_bench"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-profile", action="store_true",
+                    help="skip the per-stage timing graphs (for counter-collection runs under QE_LAUNCH=eager)")
     ap.add_argument("--json-out", default=None, help="also write a detailed result JSON here")
     args = ap.parse_args()
 
@@ -130,6 +168,8 @@ def main():
 
     ceiling = measured_read_ceiling(torch, qe)
     log(f"measured HBM read ceiling: {ceiling:.1f} GB/s")
+    copy_gbs = measured_copy(torch)
+    log(f"measured 1 GiB device copy: {copy_gbs:.1f} GB/s (read + write)")
 
     t0 = time.time()
     model = qe.Model.load_model(ckpt)
@@ -179,38 +219,30 @@ def main():
     per_token_gpu_s = gpu_s / K
     achieved_gbs = avg_bytes / per_token_gpu_s / 1e9
 
-    # per-kernel durations from HIP events between the launches of one step (n_prof steps on the
-    # warm cache), and each stage's algorithmic bytes per launch
+    # per-stage launch durations: each stage's launches alone as a graph, replayed between two
+    # HIP events on the engine stream (qe_profile_step), on the warm cache at n_prof positions
     stages = {}
     prof_positions = list(range(P, P + n_prof))
-    for i, pos in enumerate(prof_positions):
-        for name, us in model.profile_step(warm_tokens[i], pos, wc):
-            stages.setdefault(name, []).append(us)
+    for i, pos in enumerate([] if args.no_profile else prof_positions):
+        for name, us, launches in model.profile_step(warm_tokens[i], pos, wc):
+            stages.setdefault(name, ([], launches))[0].append(us)
     del wc
-    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
-    QD, KD, L = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim, cfg.num_hidden_layers
     el = 2 if kv_dtype == qe.QE_KV_BF16 else 4
     mean_pos = sum(prof_positions) / n_prof
-    stage_bytes = {  # weights + activations in/out per launch (out*in*2 + in*4 + out*4 for a matvec)
-        "embed": H * 2 + H * 4,
-        "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
-        "attention": 2 * KD * (mean_pos + 1) * el + (QD + 2 * KD) * 4 + QD * 4,
-        "o_proj": H * QD * 2 + QD * 4 + 2 * H * 4,
-        "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
-        "down": H * I * 2 + I * 4 + 2 * H * 4,
-        "lm_head": V * H * 2 + H * 2 + H * 4 + V * 4,
-        "argmax": 8 * ((V + 15) // 16),
-    }
+    stage_bytes = qe.stage_bytes(cfg, mean_pos, el)
     kernel_table = {}
-    for name, durs in stages.items():
-        per_step = len(durs) / n_prof
+    for name, (durs, per_step) in stages.items():
         mean_us = sum(durs) / len(durs)
         b = stage_bytes.get(name, 0)
         kernel_table[name] = {"launches_per_step": per_step, "mean_us": round(mean_us, 3),
                               "us_per_step": round(mean_us * per_step, 2), "bytes_per_launch": int(b),
                               "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
-    dom_name = max(kernel_table, key=lambda k: kernel_table[k]["us_per_step"])
-    dom = kernel_table[dom_name]
+    if kernel_table:
+        dom_name = max(kernel_table, key=lambda k: kernel_table[k]["us_per_step"])
+        dom = kernel_table[dom_name]
+    else:
+        dom_name, dom = None, {"achieved_gbs": None, "bytes_per_launch": None, "mean_us": None,
+                               "launches_per_step": None}
 
     # token parity against the oracle's committed run of the same workload
     parity = None
@@ -250,13 +282,14 @@ def main():
             "achieved": dom["achieved_gbs"],
             "peak": SPEC_HBM_GBS,
             "unit": "GB/s",
-            "frac": round(dom["achieved_gbs"] / SPEC_HBM_GBS, 4),
-            "traffic": None,
+            "frac": round(dom["achieved_gbs"] / SPEC_HBM_GBS, 4) if dom["achieved_gbs"] else None,
+            "traffic": pmc_traffic(dom_name),
             "kernel": dom_name,
             "bytes_per_launch": dom["bytes_per_launch"],
             "launch_us": dom["mean_us"],
             "launches_per_step": dom["launches_per_step"],
             "measured_ceiling_gbs": round(ceiling, 1),
+            "measured_copy_gbs": round(copy_gbs, 1),
         },
         "roofline_step": {
             "bound": "hbm",

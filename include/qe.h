@@ -104,13 +104,16 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
 int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv,
               qe_on_token on_token, void* user, float* logits_per_step);
 
-/* ---- per-kernel timing of one decode step: runs `token` at `pos` like qe_forward, but
- *      launches the step's kernels one by one with a HIP event between launches, and writes
- *      each kernel's duration in microseconds (launch order) to us_out and its stage name to
- *      names_out (static strings). No reference counterpart: the reference timed kernels by
- *      removing them by hand (README.md:64-71). ---- */
+/* ---- per-stage kernel timing: runs `token` at `pos` like qe_forward, then times each stage
+ *      of the step (qkv, attention, o_proj, gate_up, down, lm_head, argmax) as a graph of that
+ *      stage's launches only (28 per-layer launches, or one), replayed 8 times between two HIP
+ *      events. Writes, per stage, the mean duration of one launch in microseconds to us_out,
+ *      the launches per decode step to launches_out (nullable) and the stage name (a static
+ *      string) to names_out (nullable); *n_out = stages written. The replays leave the cache's
+ *      step state advanced; the next forward/prefill/decode call resets it. No reference
+ *      counterpart: the reference timed kernels by removing them by hand (README.md:64-71). ---- */
 int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out,
-                    const char** names_out, uint32_t max_kernels, uint32_t* n_out);
+                    uint32_t* launches_out, const char** names_out, uint32_t max_stages, uint32_t* n_out);
 
 /* ---- synthetic inputs (the reference loads a real checkpoint; this build writes a seeded
  *      random-init one with the same tensor names, shapes and file format) ---- */

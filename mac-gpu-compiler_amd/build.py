@@ -53,8 +53,51 @@ def build(verbose: bool = False) -> str:
     if verbose and out.strip():
         print(out)
     os.replace(tmp, LIB)
+    build_cli(verbose)
+    build_stage_pmc(verbose)
     return LIB
 
+
+CLI_SRC = os.path.join(CSRC, "qe_decode_cli.cpp")
+CLI = os.path.join(PKG, "qe_decode")
+
+
+def build_cli(verbose: bool = False) -> str:
+    """qe_decode: the command-line decode loop over libqe.so (rpath $ORIGIN)."""
+    tmp = CLI + ".tmp"
+    cmd = [hipcc(), "-O2", "-std=c++17", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall",
+           "-I", os.path.join(ROOT, "include"), "-o", tmp, CLI_SRC, "-L", PKG, "-lqe", "-Wl,-rpath,$ORIGIN"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError("qe_decode build failed:\n" + out)
+    os.replace(tmp, CLI)
+    return CLI
+
+
+
+PMC_SRCS = ["qe_stage_pmc.hip", "kernels.hip", "attention.hip"]
+PMC = os.path.join(PKG, "qe_stage_pmc")
+
+
+def build_stage_pmc(verbose: bool = False) -> str:
+    """qe_stage_pmc: each decode-step kernel on synthetic inputs, for counter collection."""
+    tmp = PMC + ".tmp"
+    flags = [f for f in HIPCC_FLAGS if f not in ("-fPIC", "-shared")]
+    cmd = [hipcc(), *flags, "-I", os.path.join(ROOT, "include"), "-o", tmp,
+           *[os.path.join(CSRC, f) for f in PMC_SRCS]]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    noise = "is not a recognized feature for this target"
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    if res.returncode != 0:
+        raise RuntimeError("qe_stage_pmc build failed:\n" + out)
+    os.replace(tmp, PMC)
+    return PMC
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))

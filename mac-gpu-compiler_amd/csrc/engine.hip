@@ -112,6 +112,7 @@ struct qe_kv {
   uint32_t attn_splits = 1;
   uint32_t attn_chunk = 1;      // positions per attention split (fixed per cache)
   bool narrow_kernels = false;  // the 4-wave kernels of the first version (A/B profiling)
+  bool eager = false;           // launch the step kernel by kernel instead of replaying the graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   std::vector<hipEvent_t> events;
@@ -335,15 +336,9 @@ namespace {
 // Enqueue one decode step (reads tokens[tok_idx] at state.pos) on the model stream.
 // Timing marks for qe_profile_step: an event recorded before each kernel launch (and one after
 // the last), with the stage name of the kernel that follows it.
-struct Marks {
-  std::vector<hipEvent_t> events;
-  std::vector<const char*> names;
-  ~Marks() {
-    for (auto e : events) (void)hipEventDestroy(e);
-  }
-};
-
-int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
+// Enqueues one decode step on the model's stream. With `only` set, just the kernels of that
+// stage are enqueued (qe_profile_step times each stage this way); `launches` counts them.
+int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* launches = nullptr) {
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -351,14 +346,10 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
   const bool narrow = kv->narrow_kernels;
   hipStream_t s = m->stream;
-  auto mark = [&](const char* name) -> hipError_t {
-    if (!marks) return hipSuccess;
-    hipEvent_t e;
-    hipError_t r = hipEventCreate(&e);
-    if (r != hipSuccess) return r;
-    marks->events.push_back(e);
-    marks->names.push_back(name);
-    return hipEventRecord(e, s);
+  auto want = [&](const char* name) {
+    const bool w = !only || strcmp(only, name) == 0;
+    if (w && launches) ++*launches;
+    return w;
   };
   auto matvec = [&](const MatvecParams& p, int pro, int epi) {
     return narrow ? qe::launch_matvec(p, pro == qe::kEmbedNorm ? qe::kNorm : pro, epi, s)
@@ -366,8 +357,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
   };
   // the narrow kernels have no embedding prologue: a separate embed kernel fills x first
   if (narrow) {
-    HIP_TRY(mark("embed"));
-    HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
+    if (want("embed")) HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
   }
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
@@ -377,8 +367,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
     // (cpu_inference.rs:129-132)
     p.w = w.w_qkv; p.x = m->x; p.nw = w.w_in; p.rows = QD + 2 * KD; p.cols = H; p.out = m->qkv;
     p.embed = m->embed; p.tokens = kv->tokens; p.state = kv->state; p.vocab = V; p.x_out = m->x; p.err = m->err;
-    HIP_TRY(mark("qkv"));
-    HIP_TRY(matvec(p, l == 0 ? qe::kEmbedNorm : qe::kNorm, qe::kStore));
+    if (want("qkv")) HIP_TRY(matvec(p, l == 0 ? qe::kEmbedNorm : qe::kNorm, qe::kStore));
     // q/k norm + RoPE, K/V append, attention (cpu_inference.rs:134-162)
     AttnParams a{};
     a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope; a.rope_cur = kv->rope_cur;
@@ -391,42 +380,35 @@ int enqueue_step(qe_model* m, qe_kv* kv, Marks* marks = nullptr) {
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
     if (narrow) {
-      HIP_TRY(mark("attention"));
-      HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
+      if (want("attention")) HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
       // o_proj + residual (cpu_inference.rs:163-164)
-      HIP_TRY(mark("o_proj"));
-      HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
+      if (want("o_proj")) HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
     } else {
-      HIP_TRY(mark("attention"));
-      HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
+      if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
       // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
       p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
       p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
-      HIP_TRY(mark("o_proj"));
-      HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
+      if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
     }
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
     p.eps = c.rms_norm_eps;
     p.w = w.w_gu; p.x = m->x; p.nw = w.w_post; p.rows = 2 * I; p.cols = H; p.out = m->h;
-    HIP_TRY(mark("gate_up"));
-    HIP_TRY(matvec(p, qe::kNorm, qe::kSiluPair));
+    if (want("gate_up")) HIP_TRY(matvec(p, qe::kNorm, qe::kSiluPair));
     // down_proj + residual (cpu_inference.rs:171-172)
     p = MatvecParams{};
     p.w = w.w_down; p.x = m->h; p.rows = H; p.cols = I; p.out = m->x;
-    HIP_TRY(mark("down"));
-    HIP_TRY(matvec(p, qe::kCopy, qe::kResAdd));
+    if (want("down")) HIP_TRY(matvec(p, qe::kCopy, qe::kResAdd));
   }
   // final norm + lm_head + greedy candidates (cpu_inference.rs:175-178), then argmax
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
-  HIP_TRY(mark("lm_head"));
-  HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
-  HIP_TRY(mark("argmax"));
-  HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err, kv->rope,
-                            kv->rope_cur, D / 2, s));
-  HIP_TRY(mark(nullptr));
+  if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  if (want("argmax")) {
+    HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err,
+                              kv->rope, kv->rope_cur, D / 2, s));
+  }
   return QE_OK;
 }
 
@@ -441,6 +423,13 @@ int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
   HIP_TRY(hipMemcpyAsync(kv->state, m->h_small, sizeof(st), hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipMemcpyAsync(kv->tokens, m->h_small + 8, 4, hipMemcpyHostToDevice, m->stream));
   HIP_TRY(hipMemcpyAsync(kv->rope_cur, kv->rope + pos * D, D * 4, hipMemcpyDeviceToDevice, m->stream));
+  return QE_OK;
+}
+
+// one decode step on the model stream: a replay of the captured graph, or eager launches
+int launch_step(qe_model* m, qe_kv* kv) {
+  if (kv->eager) return enqueue_step(m, kv);
+  HIP_TRY(hipGraphLaunch(kv->exec, m->stream));
   return QE_OK;
 }
 
@@ -519,7 +508,16 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
     kv->attn_chunk = uint32_t((max_seq + kv->attn_splits - 1) / kv->attn_splits);
   }
 
-  // capture one decode step
+  // QE_LAUNCH=eager launches each step kernel by kernel (for tools that do not follow graph
+  // replays, such as counter collection); otherwise one decode step is captured and replayed
+  const char* launch = getenv("QE_LAUNCH");
+  kv->eager = launch && strcmp(launch, "eager") == 0;
+  kv->events.resize(4);
+  for (auto& ev : kv->events) HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
+  if (kv->eager) {
+    *out = kv.release();
+    return QE_OK;
+  }
   HIP_TRY(hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal));
   int rc = enqueue_step(model, kv.get());
   hipGraph_t g = nullptr;
@@ -531,8 +529,6 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   if (e != hipSuccess) return fail(QE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
   kv->graph = g;
   HIP_TRY(hipGraphInstantiate(&kv->exec, g, nullptr, nullptr, 0));
-  kv->events.resize(4);
-  for (auto& ev : kv->events) HIP_TRY(hipEventCreateWithFlags(&ev, hipEventDisableTiming));
   *out = kv.release();
   return QE_OK;
 }
@@ -549,7 +545,7 @@ int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* 
   if (token >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab %llu", token, (unsigned long long)model->cfg.vocab_size);
   int rc = set_state(model, kv, token, pos);
   if (rc) return rc;
-  HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+  if ((rc = launch_step(model, kv))) return rc;
   const size_t V = model->cfg.vocab_size;
   HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
   if ((rc = check_err(model))) return rc;
@@ -558,27 +554,63 @@ int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* 
   return QE_OK;
 }
 
-int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out, const char** names_out,
-                    uint32_t max_kernels, uint32_t* n_out) {
+int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out, uint32_t* launches_out,
+                    const char** names_out, uint32_t max_stages, uint32_t* n_out) {
   if (!model || !kv || !us_out || !n_out) return fail(QE_ERR_ARG, "null argument");
   if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
   if (pos >= kv->max_seq) return fail(QE_ERR_POS, "pos %llu exceeds KV cache size %llu", (unsigned long long)pos, (unsigned long long)kv->max_seq);
   if (pos > kv->len) return fail(QE_ERR_POS, "pos %llu is past the %llu cached positions", (unsigned long long)pos, (unsigned long long)kv->len);
   if (token >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab", token);
+  // the full step first, so that every stage reads the activations of a real step
   int rc = set_state(model, kv, token, pos);
   if (rc) return rc;
-  Marks marks;
-  if ((rc = enqueue_step(model, kv, &marks))) return rc;
+  if ((rc = launch_step(model, kv))) return rc;
   if ((rc = check_err(model))) return rc;
-  const uint32_t n = uint32_t(marks.events.size()) - 1;
-  *n_out = n;
-  for (uint32_t i = 0; i < n && i < max_kernels; i++) {
-    float ms = 0.f;
-    HIP_TRY(hipEventElapsedTime(&ms, marks.events[i], marks.events[i + 1]));
-    us_out[i] = ms * 1e3f;
-    if (names_out) names_out[i] = marks.names[i];
-  }
   kv->len = pos + 1;
+  // then each stage alone: a graph of its launches (28 per-layer launches, or the one lm_head /
+  // argmax), replayed kReps times between two events; argmax replays advance the step state,
+  // which the next call's set_state resets
+  static const char* const kStages[] = {"embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"};
+  constexpr int kReps = 8;
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  HIP_TRY(hipEventCreate(&e0));
+  hipError_t he = hipEventCreate(&e1);
+  uint32_t n = 0;
+  for (const char* stage : kStages) {
+    if (he != hipSuccess || rc != QE_OK) break;
+    uint32_t launches = 0;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    if ((he = hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal)) != hipSuccess) break;
+    rc = enqueue_step(model, kv, stage, &launches);
+    he = hipStreamEndCapture(model->stream, &g);
+    if (rc == QE_OK && he == hipSuccess && launches > 0) {
+      he = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+      if (he == hipSuccess) he = hipGraphLaunch(ge, model->stream);  // warm-up replay
+      if (he == hipSuccess) he = hipEventRecord(e0, model->stream);
+      for (int r = 0; r < kReps && he == hipSuccess; r++) he = hipGraphLaunch(ge, model->stream);
+      if (he == hipSuccess) he = hipEventRecord(e1, model->stream);
+      if (he == hipSuccess) he = hipEventSynchronize(e1);
+      float ms = 0.f;
+      if (he == hipSuccess) he = hipEventElapsedTime(&ms, e0, e1);
+      if (he == hipSuccess && n < max_stages) {
+        us_out[n] = ms * 1e3f / float(kReps * launches);
+        if (launches_out) launches_out[n] = launches;
+        if (names_out) names_out[n] = stage;
+      }
+      if (he == hipSuccess) n++;
+    }
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+  }
+  (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (rc != QE_OK) return rc;
+  if (he != hipSuccess) return fail(QE_ERR_HIP, "stage timing failed: %s", hipGetErrorString(he));
+  // argmax replays may leave ring/position error bits on this profiling state: clear them
+  HIP_TRY(hipMemsetAsync(model->err, 0, 4, model->stream));
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  *n_out = n;
   return QE_OK;
 }
 
@@ -599,7 +631,7 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
       // overwrite the slot the previous step's argmax wrote with the next prompt id
       HIP_TRY(hipMemcpyAsync(kv->tokens + i, ids + i, 4, hipMemcpyHostToDevice, model->stream));
     }
-    HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+    if ((rc = launch_step(model, kv))) return rc;
   }
   if (last_logits) {
     HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost, model->stream));
@@ -626,7 +658,7 @@ int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t step
   for (uint64_t i = 0; i <= steps; i++) {
     if (i < steps) {
       if (i >= nev) HIP_TRY(hipEventSynchronize(kv->events[i % nev]));  // ring slot free
-      HIP_TRY(hipGraphLaunch(kv->exec, model->stream));
+      if ((rc = launch_step(model, kv))) return rc;
       if (logits_per_step) {
         HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
       }

@@ -1,0 +1,154 @@
+// qe_stage_pmc: launches each decode-step kernel of the Qwen3-0.6B shapes on synthetic inputs,
+// eight times per stage with the weights rotating over four copies (past the 4 MB L2), after a
+// 1 GiB device copy of known traffic. Meant to run under `rocprofv3 --pmc FETCH_SIZE` and
+// `--pmc WRITE_SIZE`: the counters per dispatch, scaled by the copy's, give each stage's HBM
+// bytes per launch. Stage order and kernels are those of the engine's decode step.
+//
+//   qe_stage_pmc [--pos P]     (attention attends positions 0..P, default 193)
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <vector>
+
+#include "kernels.h"
+
+namespace {
+
+#define CK(x)                                                                                  \
+  do {                                                                                         \
+    hipError_t e_ = (x);                                                                       \
+    if (e_ != hipSuccess) {                                                                    \
+      std::fprintf(stderr, "qe_stage_pmc: %s failed: %s\n", #x, hipGetErrorString(e_));        \
+      std::exit(1);                                                                            \
+    }                                                                                          \
+  } while (0)
+
+__global__ void k_copy(const float4* __restrict__ s, float4* __restrict__ d, size_t n) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) d[i] = s[i];
+}
+
+// bf16 ~ small values, so sums stay finite
+__global__ void k_fill_bf16(uint16_t* p, size_t n, uint32_t seed) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) {
+    uint32_t h = uint32_t(i) * 2654435761u ^ seed;
+    h ^= h >> 15;
+    p[i] = uint16_t(0x3C00u | (h & 0x7Fu));  // 2^-7 .. ~2^-6, positive
+  }
+}
+
+__global__ void k_fill_f32(float* p, size_t n, float v) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) p[i] = v;
+}
+
+template <typename T>
+T* dalloc(size_t n) {
+  T* p = nullptr;
+  CK(hipMalloc(&p, n * sizeof(T)));
+  return p;
+}
+
+}  // namespace
+
+int main(int argc, char** argv) {
+  uint32_t pos = 193;
+  for (int i = 1; i < argc; i++) {
+    if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
+  }
+  const uint32_t H = 1024, I = 3072, V = 151936, NH = 16, NKV = 8, D = qe::kHeadDim, G = NH / NKV;
+  const uint32_t QD = NH * D, KD = NKV * D, max_seq = 258;
+  if (pos >= max_seq) pos = max_seq - 1;
+  CK(hipSetDevice(0));
+  hipStream_t s;
+  CK(hipStreamCreate(&s));
+
+  // 1 GiB copy: 1 GiB read, 1 GiB written
+  {
+    const size_t n4 = (size_t(1) << 30) / 16;
+    float4* a = dalloc<float4>(n4);
+    float4* b = dalloc<float4>(n4);
+    k_fill_f32<<<4096, 256, 0, s>>>(reinterpret_cast<float*>(a), n4 * 4, 1.f);
+    hipLaunchKernelGGL(k_copy, dim3(8192), dim3(256), 0, s, a, b, n4);
+    CK(hipStreamSynchronize(s));
+    CK(hipFree(a));
+    CK(hipFree(b));
+  }
+
+  // weights: four copies of each per-layer matrix, one lm_head
+  const size_t n_qkv = size_t(QD + 2 * KD) * H, n_o = size_t(H) * QD, n_gu = size_t(2) * I * H, n_dn = size_t(H) * I;
+  const size_t per_copy = n_qkv + n_o + n_gu + n_dn;
+  uint16_t* W = dalloc<uint16_t>(per_copy * 4);
+  uint16_t* LM = dalloc<uint16_t>(size_t(V) * H);
+  uint16_t* gains = dalloc<uint16_t>(H);
+  k_fill_bf16<<<8192, 256, 0, s>>>(W, per_copy * 4, 1u);
+  k_fill_bf16<<<8192, 256, 0, s>>>(LM, size_t(V) * H, 2u);
+  k_fill_bf16<<<4, 256, 0, s>>>(gains, H, 3u);
+  // activations and attention state
+  float* x = dalloc<float>(H);
+  float* qkv = dalloc<float>(QD + 2 * KD);
+  float* h = dalloc<float>(I);
+  float* logits = dalloc<float>(V);
+  const uint32_t n_cand = qe::matvec_num_blocks(V, H, qe::kLogits);
+  qe::ArgCand* cand = dalloc<qe::ArgCand>(n_cand);
+  float* kc = dalloc<float>(size_t(NKV) * max_seq * D);
+  float* vc = dalloc<float>(size_t(NKV) * max_seq * D);
+  const uint32_t splits = (max_seq + 63) / 64, chunk = (max_seq + splits - 1) / splits;
+  float* part = dalloc<float>(size_t(NKV) * splits * G * qe::kPartStride);
+  float* rope = dalloc<float>(size_t(max_seq) * D);
+  float* rope_cur = dalloc<float>(D);
+  qe::StepState* st = dalloc<qe::StepState>(1);
+  uint32_t* tokens = dalloc<uint32_t>(max_seq + 2);
+  uint32_t* err = dalloc<uint32_t>(1);
+  k_fill_f32<<<4, 256, 0, s>>>(x, H, 0.5f);
+  k_fill_f32<<<16, 256, 0, s>>>(qkv, QD + 2 * KD, 0.25f);
+  k_fill_f32<<<16, 256, 0, s>>>(h, I, 0.125f);
+  k_fill_f32<<<512, 256, 0, s>>>(kc, size_t(NKV) * max_seq * D, 0.01f);
+  k_fill_f32<<<512, 256, 0, s>>>(vc, size_t(NKV) * max_seq * D, 0.02f);
+  k_fill_f32<<<64, 256, 0, s>>>(rope, size_t(max_seq) * D, 0.5f);
+  k_fill_f32<<<1, 256, 0, s>>>(rope_cur, D, 0.5f);
+  const qe::StepState st_h{pos, 0u, max_seq, max_seq + 2};
+  CK(hipMemcpyAsync(st, &st_h, sizeof(st_h), hipMemcpyHostToDevice, s));
+  CK(hipMemsetAsync(tokens, 0, (max_seq + 2) * 4, s));
+  CK(hipMemsetAsync(err, 0, 4, s));
+  CK(hipStreamSynchronize(s));
+
+  for (int it = 0; it < 8; it++) {
+    const uint16_t* Wc = W + per_copy * (it % 4);
+    qe::MatvecParams p{};
+    p.eps = 1e-6f;
+    // q|k|v with the input RMSNorm
+    p.w = Wc; p.x = x; p.nw = gains; p.rows = QD + 2 * KD; p.cols = H; p.out = qkv;
+    CK(qe::launch_matvec_wide(p, qe::kNorm, qe::kStore, s));
+    // attention: q/k norm + RoPE, K/V append at pos, split partials
+    qe::AttnParams a{};
+    a.qkv = qkv; a.q_norm = gains; a.k_norm = gains; a.rope = rope; a.rope_cur = rope_cur;
+    a.k_cache = kc; a.v_cache = vc; a.partial = part; a.state = st; a.err = err;
+    a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f; a.norm_rope = 1;
+    CK(qe::launch_attention_split(a, splits, chunk, s));
+    // merge + o_proj + residual
+    p = qe::MatvecParams{};
+    p.w = Wc + n_qkv; p.rows = H; p.cols = QD; p.out = x;
+    p.attn_part = part; p.attn_splits = splits; p.attn_group = G;
+    CK(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
+    // post-attention RMSNorm + gate|up + silu*up
+    p = qe::MatvecParams{};
+    p.eps = 1e-6f; p.w = Wc + n_qkv + n_o; p.x = x; p.nw = gains; p.rows = 2 * I; p.cols = H; p.out = h;
+    CK(qe::launch_matvec_wide(p, qe::kNorm, qe::kSiluPair, s));
+    // down + residual
+    p = qe::MatvecParams{};
+    p.w = Wc + n_qkv + n_o + n_gu; p.x = h; p.rows = H; p.cols = I; p.out = x;
+    CK(qe::launch_matvec_wide(p, qe::kCopy, qe::kResAdd, s));
+    CK(hipStreamSynchronize(s));
+  }
+  for (int it = 0; it < 2; it++) {
+    qe::MatvecParams p{};
+    p.eps = 1e-6f; p.w = LM; p.x = x; p.nw = gains; p.rows = V; p.cols = H; p.out = logits; p.cand = cand;
+    CK(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+    CK(qe::launch_argmax(cand, n_cand, logits, st, tokens, nullptr, err, nullptr, nullptr, 0, s));
+    CK(hipStreamSynchronize(s));
+  }
+  uint32_t e = 0;
+  CK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
+  std::printf("qe_stage_pmc: 8 x (qkv, attention at pos %u, o_proj, gate_up, down), 2 x (lm_head, argmax); error bits 0x%x\n",
+              pos, e);
+  return 0;
+}

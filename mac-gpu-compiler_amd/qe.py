@@ -96,6 +96,24 @@ ON_TOKEN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32)
 _lib = None
 
 
+def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> dict:
+    """Algorithmic bytes per launch of each decode-step stage: a matvec moves its bf16 weights
+    plus its f32 input and output once (out*in*2 + in*4 + out*4, bench.rs:106-119 counts the
+    weights), attention its K/V history at mean_pos plus q/k/v in and the output out."""
+    H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
+    QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
+    return {
+        "embed": H * 2 + H * 4,
+        "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
+        "attention": 2 * KD * (mean_pos + 1) * kv_el + (QD + 2 * KD) * 4 + QD * 4,
+        "o_proj": H * QD * 2 + QD * 4 + 2 * H * 4,
+        "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
+        "down": H * I * 2 + I * 4 + 2 * H * 4,
+        "lm_head": V * H * 2 + H * 2 + H * 4 + V * 4,
+        "argmax": 8 * ((V + 15) // 16),
+    }
+
+
 def lib() -> ctypes.CDLL:
     """Load libqe.so (raises if it has not been built)."""
     global _lib
@@ -126,8 +144,8 @@ def lib() -> ctypes.CDLL:
         "qe_kv_len": (u64, [vp]),
         "qe_forward": (i32, [vp, u32, u64, vp, f32p]),
         "qe_prefill": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, f32p]),
-        "qe_profile_step": (i32, [vp, u32, u64, vp, f32p, ctypes.POINTER(ctypes.c_char_p), u32,
-                                  ctypes.POINTER(u32)]),
+        "qe_profile_step": (i32, [vp, u32, u64, vp, f32p, ctypes.POINTER(u32), ctypes.POINTER(ctypes.c_char_p),
+                                  u32, ctypes.POINTER(u32)]),
         "qe_decode": (i32, [vp, u32, u64, u64, vp, ON_TOKEN, vp, f32p]),
         "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
         "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
@@ -195,14 +213,16 @@ class Model:
         return out
 
     def profile_step(self, token: int, pos: int, cache: "KVCache"):
-        """One decode step launched kernel by kernel with HIP events between them:
-        returns [(stage name, microseconds)] in launch order."""
-        cap = 4096
+        """Runs `token` at `pos`, then times every stage of the step as a graph of that stage's
+        launches: returns [(stage name, microseconds per launch, launches per step)]."""
+        cap = 16
         us = np.empty(cap, dtype=np.float32)
+        launches = (ctypes.c_uint32 * cap)()
         names = (ctypes.c_char_p * cap)()
         n = ctypes.c_uint32(0)
-        _check(lib().qe_profile_step(self._h, int(token), int(pos), cache._h, _fptr(us), names, cap, ctypes.byref(n)))
-        return [(names[i].decode(), float(us[i])) for i in range(min(n.value, cap))]
+        _check(lib().qe_profile_step(self._h, int(token), int(pos), cache._h, _fptr(us), launches, names, cap,
+                                     ctypes.byref(n)))
+        return [(names[i].decode(), float(us[i]), int(launches[i])) for i in range(min(n.value, cap))]
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",
                on_token: Optional[Callable[[int], None]] = None, want_logits: bool = False):
