@@ -134,6 +134,99 @@ def cpu_baseline(ckpt: str, prompt, target_s: float = 12.0):
     }
 
 
+def by_position(gaps, start: int, window: int):
+    """tok/s per window of `window` decode steps (from the host-side gaps between tokens)."""
+    out = []
+    for i in range(0, len(gaps), window):
+        w = gaps[i:i + window]
+        out.append({"positions": f"{start + i}..{start + i + len(w) - 1}", "tok_s": round(len(w) / sum(w), 1)})
+    return out
+
+
+def graph_time_us(torch, launch, n: int, reps: int = 3) -> float:
+    """Mean duration of one of n back-to-back launches: launch(i) for i < n captured as one
+    graph on a side stream, replayed between two events; best of `reps` replays."""
+    stream = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        launch(0)  # warm-up outside the capture (first launch, lazy setup)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=stream):
+            for i in range(n):
+                launch(i)
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        e1.synchronize()
+        best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+    del g
+    return best
+
+
+MALL_BYTES = 256 << 20
+
+
+def sweep_matvec(torch, qe, ceiling: float, repeats: int):
+    """The isolated matvec at the model's shapes (in -> out; 4096 and 6144 are the fused q|k|v and gate|up), bf16 W ~ N(0, 0.02), f32 x;
+    `repeats` launches per shape rotating over distinct W copies worth >= 2x the 256 MB MALL, so
+    every launch streams its weights from HBM (bench.rs-style bytes: out*in*2 + in*4 + out*4)."""
+    rows = []
+    shapes = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 4096), (1024, 6144), (1024, 151936)]
+    for cin, cout in shapes:
+        wbytes = cout * cin * 2
+        copies = max(2, -(-2 * MALL_BYTES // wbytes))
+        W = (torch.randn(copies, cout, cin, device="cuda") * 0.02).to(torch.bfloat16)
+        x = torch.randn(cin, device="cuda")
+        out = torch.empty(cout, device="cuda")
+        us = graph_time_us(torch, lambda i: qe.op_matvec_bf16(W[i % copies], x, out,
+                                                              stream=torch.cuda.current_stream()), repeats)
+        b = wbytes + cin * 4 + cout * 4
+        gbs = b / (us * 1e-6) / 1e9
+        rows.append({"in": cin, "out": cout, "us": round(us, 3), "bytes": b, "gb_s": round(gbs, 1),
+                     "frac_of_measured": round(gbs / ceiling, 4), "frac_of_spec": round(gbs / SPEC_HBM_GBS, 4),
+                     "w_copies": copies})
+        log(f"matvec {cin:5d} -> {cout:6d}: {us:8.3f} us  {gbs:7.1f} GB/s ({gbs / ceiling:.1%} of measured)")
+        del W, x, out
+        torch.cuda.empty_cache()
+    return rows
+
+
+def sweep_attention(torch, qe, ceiling: float, repeats: int):
+    """The isolated decode attention (16 q heads, 8 KV heads, head_dim 128) over L cached
+    positions, f32 q/K/V ~ N(0, 1); buffers rotate past the MALL for L <= 8192. Split into runs
+    of 64 positions (the default) and single-pass (one workgroup per KV head).
+    Bytes = 8192 L (K and V) + 2 * 16 * 128 * 4 (q in, out)."""
+    rows = []
+    n_heads, n_kv, D = 16, 8, 128
+    for L in (128, 512, 2048, 8192, 32768):
+        kvbytes = 2 * n_kv * L * D * 4
+        copies = max(1, -(-2 * MALL_BYTES // kvbytes)) if L <= 8192 else 1
+        K = torch.randn(copies, n_kv, L, D, device="cuda")
+        V = torch.randn(copies, n_kv, L, D, device="cuda")
+        q = torch.randn(n_heads * D, device="cuda")
+        out = torch.empty(n_heads * D, device="cuda")
+        work = torch.empty(qe.op_attention_work_bytes(n_heads, n_kv, L), dtype=torch.uint8, device="cuda")
+        b = 8192 * L + 2 * n_heads * D * 4
+        row = {"positions": L, "bytes": b, "kv_copies": copies}
+        for name, splits in (("split", 0), ("single_pass", 1)):
+            us = graph_time_us(torch, lambda i: qe.op_attention(q, K[i % copies], V[i % copies], out, L, n_heads, n_kv,
+                                                               work, n_splits=splits,
+                                                               stream=torch.cuda.current_stream()),
+                               repeats if splits == 0 or L <= 2048 else max(4, repeats // 16))
+            gbs = b / (us * 1e-6) / 1e9
+            row[name] = {"us": round(us, 3), "gb_s": round(gbs, 1), "frac_of_measured": round(gbs / ceiling, 4)}
+            log(f"attention L={L:6d} {name:11s}: {us:9.3f} us  {gbs:7.1f} GB/s")
+        rows.append(row)
+        del K, V, q, out, work
+        torch.cuda.empty_cache()
+    return rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -146,6 +239,10 @@ def main():
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the per-stage timing graphs (for counter-collection runs under QE_LAUNCH=eager)")
     ap.add_argument("--json-out", default=None, help="also write a detailed result JSON here")
+    ap.add_argument("--mode", choices=["decode", "matvec-sweep", "attention-sweep"], default="decode",
+                    help="decode: the batch-1 decode benchmark (one JSON line); the sweeps time the isolated "
+                         "matvec at every model shape or the isolated attention at 128..32768 positions")
+    ap.add_argument("--repeats", type=int, default=1000, help="launches per shape in the sweeps")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -168,6 +265,17 @@ def main():
 
     ceiling = measured_read_ceiling(torch, qe)
     log(f"measured HBM read ceiling: {ceiling:.1f} GB/s")
+    if args.mode != "decode":
+        sweep = sweep_matvec if args.mode == "matvec-sweep" else sweep_attention
+        rows = sweep(torch, qe, ceiling, args.repeats)
+        result = {"metric": f"isolated {args.mode.split('-')[0]} GB/s (algorithmic bytes / launch time)",
+                  "unit": "GB/s", "n_gpus": 1, "repeats": args.repeats, "measured_ceiling_gbs": round(ceiling, 1),
+                  "peak": SPEC_HBM_GBS, "data": "synthetic", "rows": rows}
+        if args.json_out:
+            with open(args.json_out, "w") as f:
+                json.dump(result, f, indent=1)
+        print(json.dumps(result), flush=True)
+        return
     copy_gbs = measured_copy(torch)
     log(f"measured 1 GiB device copy: {copy_gbs:.1f} GB/s (read + write)")
 
@@ -303,6 +411,7 @@ def main():
         },
         "kernels": kernel_table,
         "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
+        "by_position": by_position(gaps, P, 512) if K >= 1024 else None,
         "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),
         "weight_bytes_per_token": weight_bytes,
         "parity_vs_oracle_fixture": parity,

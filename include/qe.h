@@ -132,8 +132,10 @@ int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, 
 /* One decode step of GQA attention (cpu_inference.rs:144-162, inference.metal:234-296) for
  * head_dim 128: q [n_heads*128] (post q-norm and RoPE), k/v caches laid out
  * [n_kv_heads][kv_stride][128] f32, attending positions 0..n_pos-1; out [n_heads*128].
- * n_splits == 0 picks the split-K count from n_pos; 1 forces the single-pass kernel. `work`
- * must hold qe_op_attention_work_bytes(...) bytes of device memory. */
+ * The positions are split into n_splits runs (1..128; 0 picks runs of 64 positions), each
+ * attended by one workgroup per KV head, and a second kernel merges the runs' partial softmax
+ * sums. `work` (partials, overwritten by every call) must hold qe_op_attention_work_bytes(...)
+ * bytes of device memory. */
 uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint64_t n_pos);
 int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
                     uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,

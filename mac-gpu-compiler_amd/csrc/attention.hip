@@ -1,13 +1,12 @@
 // GQA decode attention for one new token (inference.metal:194-296, cpu_inference.rs:134-162).
 //
-// grid (n_kv, splits): one workgroup per (KV head, run of positions) serves all G q heads of
-// that KV head from a single read of K and V. Lane l of a wave holds head dims (2l, 2l+1); wave w
-// of NW takes positions t0 + w, t0 + w + NW, ... in batches of U whose K/V loads are all issued
-// before any is used, with an online softmax (running max m, sum l, accumulator) per wave.
-// With norm_rope, the workgroup first applies the per-head q RMSNorm and RoPE, and the workgroup
-// whose run holds the new position also normalizes/rotates the new k and appends k and v to the
-// cache (cpu_inference.rs:134-141). One split writes att directly; several splits write
-// (m, l, acc) partials and the last split to finish merges them.
+// grid (n_kv, splits): workgroup (g, s) serves all G q heads of KV head g over the run of
+// positions [s*chunk, (s+1)*chunk) from a single read of that run's K and V, and writes one
+// (m, l, acc) partial per q head. In the decode step the workgroups also apply the per-head q/k
+// RMSNorm and RoPE, and the one whose run holds the new position appends k and v to the cache
+// (cpu_inference.rs:134-141); the o_proj matvec merges the partials in its prologue. The
+// isolated op (qe_op_attention) runs the same kernel on a final q and a complete cache, then
+// k_attn_merge.
 #include "kernels.h"
 
 #include <cmath>
@@ -17,213 +16,8 @@
 namespace qe {
 namespace {
 
-template <bool KV_BF16>
-__device__ __forceinline__ void load_kv(const AttnParams& p, size_t off, float2& k, float2& v) {
-  if (KV_BF16) {
-    const uint32_t kb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.k_cache) + off);
-    const uint32_t vb = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p.v_cache) + off);
-    k = make_float2(__uint_as_float(kb << 16), __uint_as_float(kb & 0xFFFF0000u));
-    v = make_float2(__uint_as_float(vb << 16), __uint_as_float(vb & 0xFFFF0000u));
-  } else {
-    k = *reinterpret_cast<const float2*>(static_cast<const float*>(p.k_cache) + off);
-    v = *reinterpret_cast<const float2*>(static_cast<const float*>(p.v_cache) + off);
-  }
-}
-
-template <int G>
-__device__ __forceinline__ void online_update(const float2 (&q2)[G], float2 k, float2 v, float scale, float (&m)[G],
-                                              float (&l)[G], float2 (&acc)[G]) {
-#pragma unroll
-  for (int j = 0; j < G; j++) {
-    const float sc = wave_sum(q2[j].x * k.x + q2[j].y * k.y) * scale;  // dot(q, k) * scale
-    const float mn = fmaxf(m[j], sc);
-    const float co = expf(m[j] - mn), pe = expf(sc - mn);
-    l[j] = l[j] * co + pe;
-    acc[j].x = acc[j].x * co + pe * v.x;
-    acc[j].y = acc[j].y * co + pe * v.y;
-    m[j] = mn;
-  }
-}
-
-template <int G, int NW, bool KV_BF16>
-__global__ __launch_bounds__(NW * 64) void k_attention(AttnParams p, uint32_t chunk_min) {
-  constexpr int D = kHeadDim, NT = NW * 64, U = 8;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t g = blockIdx.x;
-  uint32_t n, pos;
-  if (p.norm_rope) {
-    pos = p.state->pos;
-    if (pos >= p.max_seq) {
-      if (g == 0 && blockIdx.y == 0 && tid == 0) atomicOr(p.err, kErrPos);
-      return;
-    }
-    n = pos + 1;
-  } else {
-    n = p.n_pos_fixed;
-    pos = n - 1;
-  }
-  uint32_t nsplit = p.force_splits ? min(p.force_splits, gridDim.y) : min(gridDim.y, ceil_div(n, chunk_min));
-  const uint32_t chunk = ceil_div(n, nsplit);
-  nsplit = ceil_div(n, chunk);  // every split below nsplit starts before n
-  const uint32_t s = blockIdx.y;
-  if (s >= nsplit) return;
-  const uint32_t t0 = s * chunk, t1 = min(n, t0 + chunk);
-  const bool owns_new = p.norm_rope && t1 == n;
-  // positions read from the cache; with owns_new the last one (pos) comes from LDS instead
-  const uint32_t tc1 = owns_new ? t1 - 1 : t1;
-  const size_t head_base = size_t(g) * p.max_seq * D;
-
-  __shared__ float qs[G][D];
-  __shared__ float knew[D], vnew[D], ktmp[D];
-  __shared__ float wm[NW][G], wl[NW][G];
-  __shared__ float wacc[NW][G][D];
-  __shared__ int is_last;
-
-  // the first K/V batch does not depend on q: issue it before the q/k prologue
-  float2 kk[U], vv[U];
-  uint32_t t = t0 + wave;
-  bool preloaded = t + NW * (U - 1) < tc1;
-  if (preloaded) {
-#pragma unroll
-    for (int u = 0; u < U; u++) load_kv<KV_BF16>(p, head_base + size_t(t + NW * u) * D + 2 * lane, kk[u], vv[u]);
-  }
-
-  for (int i = tid; i < G * D; i += NT) qs[i / D][i % D] = p.qkv[size_t(g) * G * D + i];
-  __syncthreads();
-  if (p.norm_rope) {
-    for (int j = wave; j < G; j += NW) {
-      const float a = qs[j][2 * lane], b = qs[j][2 * lane + 1];
-      const float ssum = wave_sum(a * a + b * b);
-      const float sc = 1.0f / sqrtf(ssum / float(D) + p.eps);
-      qs[j][2 * lane] = a * sc * bf16f(p.q_norm[2 * lane]);
-      qs[j][2 * lane + 1] = b * sc * bf16f(p.q_norm[2 * lane + 1]);
-    }
-    if (owns_new && wave == NW - 1) {
-      const float* kr = p.qkv + size_t(p.n_heads) * D + size_t(g) * D;
-      const float* vr = p.qkv + size_t(p.n_heads) * D + size_t(p.n_kv) * D + size_t(g) * D;
-      const float a = kr[2 * lane], b = kr[2 * lane + 1];
-      const float ssum = wave_sum(a * a + b * b);
-      const float sc = 1.0f / sqrtf(ssum / float(D) + p.eps);
-      ktmp[2 * lane] = a * sc * bf16f(p.k_norm[2 * lane]);
-      ktmp[2 * lane + 1] = b * sc * bf16f(p.k_norm[2 * lane + 1]);
-      vnew[2 * lane] = vr[2 * lane];
-      vnew[2 * lane + 1] = vr[2 * lane + 1];
-    }
-    __syncthreads();
-    // rotate-half RoPE from the table row of pos (metal_inference.rs:140-154)
-    const float2* rope = reinterpret_cast<const float2*>(p.rope) + size_t(pos) * (D / 2);
-    for (int i = tid; i < G * (D / 2); i += NT) {
-      const int j = i / (D / 2), d = i % (D / 2);
-      const float2 cs = rope[d];
-      const float a = qs[j][d], b = qs[j][d + D / 2];
-      qs[j][d] = a * cs.x - b * cs.y;
-      qs[j][d + D / 2] = b * cs.x + a * cs.y;
-    }
-    if (owns_new && tid < D / 2) {
-      const float2 cs = rope[tid];
-      const float a = ktmp[tid], b = ktmp[tid + D / 2];
-      knew[tid] = a * cs.x - b * cs.y;
-      knew[tid + D / 2] = b * cs.x + a * cs.y;
-    }
-    __syncthreads();
-    if (owns_new && tid < D) {
-      const size_t slot = (size_t(g) * p.max_seq + pos) * D + tid;
-      if (KV_BF16) {
-        const uint16_t kb = f32_to_bf16(knew[tid]), vb = f32_to_bf16(vnew[tid]);
-        static_cast<uint16_t*>(p.k_cache)[slot] = kb;
-        static_cast<uint16_t*>(p.v_cache)[slot] = vb;
-        knew[tid] = bf16f(kb);  // attend with the values later steps read back
-        vnew[tid] = bf16f(vb);
-      } else {
-        static_cast<float*>(p.k_cache)[slot] = knew[tid];
-        static_cast<float*>(p.v_cache)[slot] = vnew[tid];
-      }
-    }
-    __syncthreads();
-  }
-
-  float2 q2[G];
-#pragma unroll
-  for (int j = 0; j < G; j++) q2[j] = make_float2(qs[j][2 * lane], qs[j][2 * lane + 1]);
-  float m[G], l[G];
-  float2 acc[G];
-#pragma unroll
-  for (int j = 0; j < G; j++) { m[j] = -INFINITY; l[j] = 0.f; acc[j] = make_float2(0.f, 0.f); }
-
-  for (; t + NW * (U - 1) < tc1; t += NW * U) {
-    if (!preloaded) {
-#pragma unroll
-      for (int u = 0; u < U; u++) load_kv<KV_BF16>(p, head_base + size_t(t + NW * u) * D + 2 * lane, kk[u], vv[u]);
-    }
-    preloaded = false;
-#pragma unroll
-    for (int u = 0; u < U; u++) online_update<G>(q2, kk[u], vv[u], p.scale, m, l, acc);
-  }
-  for (; t < t1; t += NW) {
-    float2 k1, v1;
-    if (owns_new && t == tc1) {
-      k1 = make_float2(knew[2 * lane], knew[2 * lane + 1]);
-      v1 = make_float2(vnew[2 * lane], vnew[2 * lane + 1]);
-    } else {
-      load_kv<KV_BF16>(p, head_base + size_t(t) * D + 2 * lane, k1, v1);
-    }
-    online_update<G>(q2, k1, v1, p.scale, m, l, acc);
-  }
-
-  // combine the NW waves
-#pragma unroll
-  for (int j = 0; j < G; j++) {
-    if (lane == 0) { wm[wave][j] = m[j]; wl[wave][j] = l[j]; }
-    wacc[wave][j][2 * lane] = acc[j].x;
-    wacc[wave][j][2 * lane + 1] = acc[j].y;
-  }
-  __syncthreads();
-  float* part = p.partial + (size_t(g) * kAttnMaxSplits + s) * G * (2 + D);
-  for (int i = tid; i < G * D; i += NT) {
-    const int j = i / D, d = i % D;
-    float M = -INFINITY;
-    for (int w = 0; w < NW; w++) M = fmaxf(M, wm[w][j]);
-    float L = 0.f, A = 0.f;
-    for (int w = 0; w < NW; w++) {
-      const float e = wm[w][j] == -INFINITY ? 0.f : expf(wm[w][j] - M);  // a wave with no positions adds 0
-      L += e * wl[w][j];
-      A += e * wacc[w][j][d];
-    }
-    if (nsplit == 1) {
-      p.att[(size_t(g) * G + j) * D + d] = A / L;
-    } else {
-      if (d == 0) { part[j * (2 + D)] = M; part[j * (2 + D) + 1] = L; }
-      part[j * (2 + D) + 2 + d] = A;
-    }
-  }
-  if (nsplit == 1) return;
-
-  // the last split to arrive merges (release/acquire through device-scope fences)
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) is_last = atomicAdd(&p.counter[g], 1u) == nsplit - 1;
-  __syncthreads();
-  if (!is_last) return;
-  __threadfence();
-  const float* pg = p.partial + size_t(g) * kAttnMaxSplits * G * (2 + D);
-  for (int i = tid; i < G * D; i += NT) {
-    const int j = i / D, d = i % D;
-    float M = -INFINITY;
-    for (uint32_t q = 0; q < nsplit; q++) M = fmaxf(M, pg[(q * G + j) * (2 + D)]);
-    float L = 0.f, A = 0.f;
-    for (uint32_t q = 0; q < nsplit; q++) {
-      const float* pq = pg + (q * G + j) * (2 + D);
-      const float e = pq[0] == -INFINITY ? 0.f : expf(pq[0] - M);
-      L += e * pq[1];
-      A += e * pq[2 + d];
-    }
-    p.att[(size_t(g) * G + j) * D + d] = A / L;
-  }
-  if (tid == 0) atomicExch(&p.counter[g], 0u);
-}
-
 // ---------------------------------------------------------------------------------------------
-// Decode-step attention over a fixed split of the cache: workgroup (g, s) covers positions
+// Attention over a fixed split of the cache: workgroup (g, s) covers positions
 // [s*chunk, (s+1)*chunk) of KV head g, in tiles of T = 64 positions, for all G q heads of g.
 // Every global load of a tile is issued before any of its values is used, and no load sits
 // behind a divergent branch (the compiler waits for such a load on the spot): positions past
@@ -238,8 +32,8 @@ __global__ __launch_bounds__(NW * 64) void k_attention(AttnParams p, uint32_t ch
 //   softmax:  wave j reduces head j's 64 scores once per tile (online max, exp, sum)
 //   PV:       thread (dg = tid%32, pp = tid/32) accumulates dims [4dg, 4dg+4) over positions
 //             tile+8pp .. tile+8pp+7; the 8 position groups meet in LDS at the end
-// The workgroup writes its (m, l, acc) partial per q head; a run past pos writes an empty one
-// (m = -inf, l = 0, acc = 0). The o_proj matvec merges the partials in its prologue.
+// The workgroup writes its (m, l, acc) partial per q head; a run past the last position writes
+// an empty one (m = -inf, l = 0, acc = 0).
 // ---------------------------------------------------------------------------------------------
 template <bool KV_BF16>
 struct KVTile;
@@ -318,9 +112,11 @@ __device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16>& X, int i) {
   }
 }
 
-template <int G, bool KV_BF16>
+template <int G, bool KV_BF16, bool DECODE>
 __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk) {
-  constexpr int D = kHeadDim, T = 64, NR = G + 2, RPW = (NR + 3) / 4;
+  // DECODE: q/k RMSNorm + RoPE on the raw q|k|v rows, append of the new K/V row, positions
+  // 0..state->pos; otherwise (the isolated op) q is final and positions are 0..n_pos_fixed-1
+  constexpr int D = kHeadDim, T = 64, NR = DECODE ? G + 2 : G, RPW = (NR + 3) / 4;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so branches on it are scalar
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
@@ -345,21 +141,34 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     ra[i] = p.qkv[off + lane];
     rb[i] = p.qkv[off + lane + 64];
   }
-  const float gqa = bf16f(p.q_norm[lane]), gqb = bf16f(p.q_norm[lane + 64]);
-  const float gka = bf16f(p.k_norm[lane]), gkb = bf16f(p.k_norm[lane + 64]);
-  const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  float gqa = 0.f, gqb = 0.f, gka = 0.f, gkb = 0.f;
+  float2 cs = make_float2(0.f, 0.f);
+  if constexpr (DECODE) {
+    gqa = bf16f(p.q_norm[lane]);
+    gqb = bf16f(p.q_norm[lane + 64]);
+    gka = bf16f(p.k_norm[lane]);
+    gkb = bf16f(p.k_norm[lane + 64]);
+    cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  }
   KVTile<KV_BF16> A, B;
   load_tile<KV_BF16>(A, p, head_base, t0, tid);
   __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from sinking these loads to their uses
 
-  const uint32_t pos = p.state->pos;
-  const bool bad = pos >= p.max_seq;
-  if (bad && g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
   // a run with no cached position (t1 <= t0) goes through one all-masked tile and writes the
   // empty partial m = -inf, l = 0, acc = 0
-  const uint32_t n = bad ? 0u : pos + 1;
+  uint32_t pos, n;
+  bool owns_new = false;  // this run holds the new position
+  if constexpr (DECODE) {
+    pos = p.state->pos;
+    const bool bad = pos >= p.max_seq;
+    if (bad && g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
+    n = bad ? 0u : pos + 1;
+    owns_new = !bad && pos >= t0 && pos < t0 + chunk;
+  } else {
+    n = p.n_pos_fixed;
+    pos = n - 1;
+  }
   const uint32_t t1 = min(n, t0 + chunk);
-  const bool owns_new = !bad && pos >= t0 && pos < t0 + chunk;  // this run holds the new position
   float* part = p.partial + (size_t(g) * gridDim.y + s) * G * kPartStride;
 
   // ---- q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215) ----
@@ -368,7 +177,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     const int r = wave + 4 * i;
     if (r < NR) {
       float a = ra[i], b = rb[i];
-      if (r <= G) {
+      if (DECODE && r <= G) {
         const float ss = wave_sum(a * a + b * b);
         const float scl = 1.0f / sqrtf(ss / float(D) + p.eps);
         a = a * scl * (r < G ? gqa : gka);
@@ -495,15 +304,62 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   }
 }
 
-template <int NW>
-hipError_t launch_nw(const AttnParams& p, uint32_t grid_splits, uint32_t chunk_min, hipStream_t s) {
+
+// ---------------------------------------------------------------------------------------------
+// The isolated op's merge: out[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s over the split
+// partials of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. One workgroup per
+// q head, one thread per dim; loads in batches of 16 splits, unconditional (clamped).
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
+                                                         float* __restrict__ out) {
+  constexpr int U = 16, PS = kPartStride;
+  const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x;
+  const float* base = part + (size_t(g) * splits * G + j) * PS;
+  float M = -INFINITY;
+  for (uint32_t s0 = 0; s0 < splits; s0 += U) {
+    float mv[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) mv[u] = base[size_t(min(s0 + u, splits - 1)) * G * PS];
+#pragma unroll
+    for (int u = 0; u < U; u++) M = s0 + u < splits ? fmaxf(M, mv[u]) : M;
+  }
+  float L = 0.f, A = 0.f;
+  for (uint32_t s0 = 0; s0 < splits; s0 += U) {
+    float mv[U], lv[U], av[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float* q = base + size_t(min(s0 + u, splits - 1)) * G * PS;
+      mv[u] = q[0];
+      lv[u] = q[1];
+      av[u] = q[4 + d];
+    }
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float e = (s0 + u < splits && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
+      L += e * lv[u];
+      A += e * av[u];
+    }
+  }
+  out[size_t(h) * kHeadDim + d] = A / L;
+}
+
+// shapes the kernels support; the runs [s*chunk, (s+1)*chunk) must cover positions 0..n-1
+bool attn_args_ok(const AttnParams& p, uint32_t splits, uint32_t chunk, uint32_t n) {
+  if (!p.n_kv || p.n_heads % p.n_kv || !p.qkv || !p.k_cache || !p.v_cache || !p.partial || p.max_seq == 0)
+    return false;
   const uint32_t G = p.n_heads / p.n_kv;
-  dim3 grid(p.n_kv, grid_splits);
-#define QE_ATT(GG)                                                                                       \
-  if (G == GG) {                                                                                         \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attention<GG, NW, true>), grid, dim3(NW * 64), 0, s, p, chunk_min);  \
-    else hipLaunchKernelGGL((k_attention<GG, NW, false>), grid, dim3(NW * 64), 0, s, p, chunk_min);           \
-    return hipGetLastError();                                                                            \
+  return (G == 1 || G == 2 || G == 4 || G == 8) && splits > 0 && chunk > 0 && uint64_t(splits) * chunk >= n;
+}
+
+template <bool DECODE>
+hipError_t launch_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s) {
+  const uint32_t G = p.n_heads / p.n_kv;
+  dim3 grid(p.n_kv, splits);
+#define QE_ATT(GG)                                                                                          \
+  if (G == GG) {                                                                                            \
+    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_split<GG, true, DECODE>), grid, dim3(256), 0, s, p, chunk);   \
+    else hipLaunchKernelGGL((k_attn_split<GG, false, DECODE>), grid, dim3(256), 0, s, p, chunk);            \
+    return hipGetLastError();                                                                               \
   }
   QE_ATT(1)
   QE_ATT(2)
@@ -511,50 +367,26 @@ hipError_t launch_nw(const AttnParams& p, uint32_t grid_splits, uint32_t chunk_m
   QE_ATT(8)
 #undef QE_ATT
   return hipErrorInvalidValue;
-}
-
-bool attn_args_ok(const AttnParams& p, uint32_t grid_splits) {
-  if (!p.n_kv || p.n_heads % p.n_kv) return false;
-  const uint32_t G = p.n_heads / p.n_kv;
-  return (G == 1 || G == 2 || G == 4 || G == 8) && grid_splits > 0 && grid_splits <= uint32_t(kAttnMaxSplits);
 }
 
 }  // namespace
 
-// 4-wave workgroups, splits of at least kAttnMinChunk positions (the isolated op's default)
-hipError_t launch_attention(const AttnParams& p, uint32_t grid_splits, hipStream_t s) {
-  if (!attn_args_ok(p, grid_splits)) return hipErrorInvalidValue;
-  return launch_nw<4>(p, grid_splits, kAttnMinChunk, s);
-}
-
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s) {
-  if (!attn_args_ok(p, splits) || splits > uint32_t(kAttnMaxMergeSplits) || chunk == 0 || !p.norm_rope ||
-      !p.rope_cur || uint64_t(splits) * chunk < p.max_seq)
+  if (!attn_args_ok(p, splits, chunk, p.max_seq) || splits > uint32_t(kAttnMaxMergeSplits) || !p.state || !p.rope_cur ||
+      !p.q_norm || !p.k_norm || !p.err)
     return hipErrorInvalidValue;
-  const uint32_t G = p.n_heads / p.n_kv;
-  dim3 grid(p.n_kv, splits);
-#define QE_ATT(GG)                                                                                   \
-  if (G == GG) {                                                                                     \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_split<GG, true>), grid, dim3(256), 0, s, p, chunk);   \
-    else hipLaunchKernelGGL((k_attn_split<GG, false>), grid, dim3(256), 0, s, p, chunk);            \
-    return hipGetLastError();                                                                        \
-  }
-  QE_ATT(1)
-  QE_ATT(2)
-  QE_ATT(4)
-  QE_ATT(8)
-#undef QE_ATT
-  return hipErrorInvalidValue;
+  return launch_split<true>(p, splits, chunk, s);
 }
 
-// 16-wave workgroups (fewer for wide GQA groups, to bound LDS), splits of kAttnBlockPositions:
-// a single workgroup per KV head up to 512 positions, so no merge round trip at short context
-hipError_t launch_attention_wide(const AttnParams& p, uint32_t grid_splits, hipStream_t s) {
-  if (!attn_args_ok(p, grid_splits)) return hipErrorInvalidValue;
-  const uint32_t G = p.n_heads / p.n_kv;
-  if (G <= 2) return launch_nw<16>(p, grid_splits, kAttnBlockPositions, s);
-  if (G == 4) return launch_nw<8>(p, grid_splits, kAttnBlockPositions, s);
-  return launch_nw<4>(p, grid_splits, kAttnBlockPositions, s);
+hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
+  if (p.n_pos_fixed == 0 || p.n_pos_fixed > p.max_seq || splits == 0 || splits > uint32_t(kAttnMaxSplits) || !out)
+    return hipErrorInvalidValue;
+  const uint32_t chunk = ceil_div(p.n_pos_fixed, splits);
+  if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16) return hipErrorInvalidValue;
+  hipError_t e = launch_split<false>(p, splits, chunk, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out);
+  return hipGetLastError();
 }
 
 }  // namespace qe

@@ -78,7 +78,6 @@ struct qe_model {
   ArgCand* cand = nullptr;
   uint32_t n_cand = 0;
   float* attn_part = nullptr;
-  uint32_t* attn_cnt = nullptr;
   uint32_t* err = nullptr;  // device error word
   uint8_t* scratch = nullptr;
   // pinned host staging
@@ -111,7 +110,6 @@ struct qe_kv {
   uint32_t tok_cap = 0;
   uint32_t attn_splits = 1;
   uint32_t attn_chunk = 1;      // positions per attention split (fixed per cache)
-  bool narrow_kernels = false;  // the 4-wave kernels of the first version (A/B profiling)
   bool eager = false;           // launch the step kernel by kernel instead of replaying the graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -291,8 +289,8 @@ int qe_model_load(const char* path, qe_model** out) {
   auto stake = [&](size_t bytes) { size_t o = so; so = align_up(so + bytes, 256); return o; };
   const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
                s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
-               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxSplits * G * qe::kPartStride * 4),
-               s_cnt = stake(c.num_key_value_heads * 4), s_err = stake(4);
+               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxMergeSplits * G * qe::kPartStride * 4),
+               s_err = stake(4);
   HIP_TRY(hipMalloc(&m->scratch, so));
   HIP_TRY(hipMemset(m->scratch, 0, so));
   m->x = reinterpret_cast<float*>(m->scratch + s_x);
@@ -302,7 +300,6 @@ int qe_model_load(const char* path, qe_model** out) {
   m->logits = reinterpret_cast<float*>(m->scratch + s_logits);
   m->cand = reinterpret_cast<ArgCand*>(m->scratch + s_cand);
   m->attn_part = reinterpret_cast<float*>(m->scratch + s_part);
-  m->attn_cnt = reinterpret_cast<uint32_t*>(m->scratch + s_cnt);
   m->err = reinterpret_cast<uint32_t*>(m->scratch + s_err);
   HIP_TRY(hipHostMalloc(&m->h_logits, V * 4, hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(&m->h_small, 64, hipHostMallocDefault));
@@ -344,21 +341,13 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
-  const bool narrow = kv->narrow_kernels;
   hipStream_t s = m->stream;
   auto want = [&](const char* name) {
     const bool w = !only || strcmp(only, name) == 0;
     if (w && launches) ++*launches;
     return w;
   };
-  auto matvec = [&](const MatvecParams& p, int pro, int epi) {
-    return narrow ? qe::launch_matvec(p, pro == qe::kEmbedNorm ? qe::kNorm : pro, epi, s)
-                  : qe::launch_matvec_wide(p, pro, epi, s);
-  };
-  // the narrow kernels have no embedding prologue: a separate embed kernel fills x first
-  if (narrow) {
-    if (want("embed")) HIP_TRY(qe::launch_embed(m->embed, H, V, kv->tokens, kv->state, m->x, m->err, s));
-  }
+  auto matvec = [&](const MatvecParams& p, int pro, int epi) { return qe::launch_matvec_wide(p, pro, epi, s); };
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     MatvecParams p{};
@@ -373,23 +362,17 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     a.qkv = m->qkv; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope; a.rope_cur = kv->rope_cur;
     a.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
     a.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
-    a.partial = m->attn_part; a.counter = m->attn_cnt; a.att = m->att; a.state = kv->state; a.err = m->err;
+    a.partial = m->attn_part; a.state = kv->state; a.err = m->err;
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.max_seq = uint32_t(kv->max_seq); a.eps = c.rms_norm_eps; a.scale = 1.0f / sqrtf(float(D));
-    a.kv_bf16 = kv->dtype == QE_KV_BF16; a.norm_rope = 1;
+    a.kv_bf16 = kv->dtype == QE_KV_BF16;
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
-    if (narrow) {
-      if (want("attention")) HIP_TRY(qe::launch_attention(a, kv->attn_splits, s));
-      // o_proj + residual (cpu_inference.rs:163-164)
-      if (want("o_proj")) HIP_TRY(qe::launch_matvec(p, qe::kCopy, qe::kResAdd, s));
-    } else {
-      if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
-      // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
-      p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
-      p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
-      if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
-    }
+    if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
+    // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
+    p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
+    p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
+    if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
     p.eps = c.rms_norm_eps;
@@ -496,17 +479,10 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   HIP_TRY(hipMemcpyAsync(kv->rope, table.data(), rope_bytes, hipMemcpyHostToDevice, model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
 
-  // QE_KERNELS=narrow selects the first version's 4-wave kernels (for A/B profiling)
-  const char* kern = getenv("QE_KERNELS");
-  kv->narrow_kernels = kern && strcmp(kern, "narrow") == 0;
-  if (kv->narrow_kernels) {
-    kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk, qe::kAttnMaxSplits));
-  } else {
-    // a fixed split of the cache into runs of >= 64 positions, at most kAttnMaxMergeSplits of
-    // them (the o_proj prologue merges that many partials per q head)
-    kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
-    kv->attn_chunk = uint32_t((max_seq + kv->attn_splits - 1) / kv->attn_splits);
-  }
+  // a fixed split of the cache into runs of >= 64 positions, at most kAttnMaxMergeSplits of them
+  // (the o_proj prologue merges that many partials per q head)
+  kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
+  kv->attn_chunk = uint32_t((max_seq + kv->attn_splits - 1) / kv->attn_splits);
 
   // QE_LAUNCH=eager launches each step kernel by kernel (for tools that do not follow graph
   // replays, such as counter collection); otherwise one decode step is captured and replayed
@@ -709,9 +685,10 @@ int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, 
 }
 
 uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint64_t n_pos) {
-  if (!n_kv_heads) return 0;
+  (void)n_pos;  // the partials are sized for the most runs, kAttnMaxSplits per KV head
+  if (!n_kv_heads || n_heads % n_kv_heads) return 0;
   const uint64_t G = n_heads / n_kv_heads;
-  return align_up(n_kv_heads * qe::kAttnMaxSplits * G * (2 + qe::kHeadDim) * 4, 256) + align_up(n_kv_heads * 4, 256) + 256;
+  return align_up(n_kv_heads * qe::kAttnMaxSplits * G * qe::kPartStride * 4, 256);
 }
 
 int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos, uint64_t kv_stride,
@@ -722,19 +699,15 @@ int qe_op_attention(const float* q, const float* k, const float* v, float* out, 
   const uint64_t G = n_heads / n_kv_heads;
   if (G != 1 && G != 2 && G != 4 && G != 8) return fail(QE_ERR_UNSUPPORTED, "q heads per KV head must be 1, 2, 4 or 8");
   if (n_splits > qe::kAttnMaxSplits) return fail(QE_ERR_ARG, "n_splits above %d", qe::kAttnMaxSplits);
-  uint8_t* w8 = static_cast<uint8_t*>(work);
-  const size_t part_bytes = align_up(n_kv_heads * qe::kAttnMaxSplits * G * (2 + qe::kHeadDim) * 4, 256);
   AttnParams a{};
   a.qkv = q; a.k_cache = const_cast<float*>(k); a.v_cache = const_cast<float*>(v);
-  a.partial = reinterpret_cast<float*>(w8);
-  a.counter = reinterpret_cast<uint32_t*>(w8 + part_bytes);
-  a.err = reinterpret_cast<uint32_t*>(w8 + part_bytes + align_up(n_kv_heads * 4, 256));
-  a.att = out; a.n_heads = uint32_t(n_heads); a.n_kv = uint32_t(n_kv_heads); a.max_seq = uint32_t(kv_stride);
-  a.scale = 1.0f / sqrtf(float(qe::kHeadDim)); a.norm_rope = 0; a.n_pos_fixed = uint32_t(n_pos);
-  a.force_splits = n_splits;
-  uint64_t splits = n_splits ? n_splits : (n_pos + qe::kAttnMinChunk - 1) / qe::kAttnMinChunk;
+  a.partial = static_cast<float*>(work);
+  a.n_heads = uint32_t(n_heads); a.n_kv = uint32_t(n_kv_heads); a.max_seq = uint32_t(kv_stride);
+  a.scale = 1.0f / sqrtf(float(qe::kHeadDim)); a.n_pos_fixed = uint32_t(n_pos);
+  // default: runs of 64 positions (one tile each), at most kAttnMaxSplits of them
+  uint64_t splits = n_splits ? n_splits : (n_pos + 63) / 64;
   splits = std::min<uint64_t>(std::max<uint64_t>(splits, 1), qe::kAttnMaxSplits);
-  HIP_TRY(qe::launch_attention(a, uint32_t(splits), static_cast<hipStream_t>(stream)));
+  HIP_TRY(qe::launch_attention_op(a, uint32_t(splits), out, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }
 

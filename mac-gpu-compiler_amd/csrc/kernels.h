@@ -7,10 +7,8 @@
 
 namespace qe {
 
-constexpr int kHeadDim = 128;        // the attention kernels' lane layout: 64 lanes x float2
-constexpr int kMaxGroup = 8;         // q heads per KV head handled by one attention workgroup
-constexpr int kAttnMinChunk = 16;    // fewest positions per split-K workgroup
-constexpr int kAttnMaxSplits = 128;  // most split-K workgroups per KV head
+constexpr int kHeadDim = 128;        // head dimension the attention kernels are written for
+constexpr int kAttnMaxSplits = 128;  // most position runs per KV head (isolated attention op)
 
 // Per-sequence device state, advanced by the last kernel of each step so a captured step can
 // be replayed without host writes: step i reads tokens[tok_idx] at position pos and writes its
@@ -66,31 +64,20 @@ struct AttnParams {
   const float* rope_cur;   // [D/2][2]: the rope row of state->pos (split kernel)
   void* k_cache;          // layer base, [n_kv][max_seq][D], f32 or bf16
   void* v_cache;
-  float* partial;          // [n_kv][kAttnMaxSplits][group][2 + D]
-  uint32_t* counter;       // [n_kv] split arrival counters (zero between launches)
-  float* att;              // [n_heads*D]
+  float* partial;          // [n_kv][splits][group][kPartStride]
   const StepState* state;
   uint32_t* err;
   uint32_t n_heads, n_kv, max_seq;
   float eps, scale;
   int kv_bf16;
-  int norm_rope;           // 1: q/k are raw and this kernel applies q/k-norm + RoPE and writes
-                           //    the new K/V slot; 0: q is final and the cache is complete
-  uint32_t n_pos_fixed;    // norm_rope == 0: attend 0..n_pos_fixed-1
-  uint32_t force_splits;   // 0: choose from n_pos
+  uint32_t n_pos_fixed;    // isolated op: attend positions 0..n_pos_fixed-1 with a final q
 };
 
 // --- launch wrappers (kernels.hip) ---
-hipError_t launch_embed(const uint16_t* table, uint32_t hidden, uint32_t vocab, const uint32_t* tokens,
-                        const StepState* st, float* x, uint32_t* err, hipStream_t s);
 hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
 uint32_t matvec_num_blocks(uint32_t rows, uint32_t cols, int epilogue);
 // the per-layer projections: ~1000 workgroups, x read per chunk from global memory
 hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
-hipError_t launch_attention(const AttnParams& p, uint32_t grid_splits, hipStream_t s);
-// positions one attention workgroup covers before the work is split (split-K)
-constexpr int kAttnBlockPositions = 512;
-hipError_t launch_attention_wide(const AttnParams& p, uint32_t grid_splits, hipStream_t s);
 // Decode-step attention with a fixed split of the cache into `splits` runs of `chunk` positions
 // (host-chosen from max_seq): each workgroup writes (m, l, acc) partials, runs past pos write an
 // empty partial, and the o_proj matvec merges them in its prologue (kAttnMerge).
@@ -98,6 +85,9 @@ constexpr int kAttnMaxMergeSplits = 16;
 // one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
 constexpr int kPartStride = 4 + kHeadDim;
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s);
+// The isolated op: final q [n_heads][D], complete K/V [n_kv][max_seq][D] (f32), positions
+// 0..n_pos_fixed-1 in `splits` runs (<= kAttnMaxSplits), partials merged into out [n_heads][D].
+hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);
 // Greedy token from the lm_head candidates; advances the step state and, with `rope`, copies the
 // RoPE row of the next position ([half] (cos, sin) pairs) to rope_cur for the next step.
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,

@@ -1,12 +1,14 @@
 // gfx950 kernels of the batch-1 decode step: one kernel per dependent stage.
 //
 // Stage map (reference: metal_infrence_engine/src/shaders/inference.metal, cpu_inference.rs):
-//   embed            -> k_embed                        (inference.metal:98-107)
-//   rmsnorm + matvec -> k_matvec<.., kNorm, ..>          (inference.metal:113-130, 143-186)
-//   qk_norm_rope + attention + K/V append -> k_attention (inference.metal:194-296)
-//   silu_mul         -> k_matvec epilogue kSiluPair      (inference.metal:325-334)
-//   add_inplace      -> k_matvec epilogue kResAdd        (inference.metal:338-346)
-//   argmax           -> k_matvec epilogue kLogits + k_argmax (inference.metal:300-321)
+//   embed + rmsnorm + q|k|v  -> k_mv_wide<.., kEmbedNorm, kStore>   (inference.metal:98-130, 143-186)
+//   rmsnorm + matvec         -> k_mv_wide<.., kNorm, ..>            (inference.metal:113-130, 143-186)
+//   qk_norm_rope + attention + K/V append -> k_attn_split (attention.hip, inference.metal:194-296)
+//   attention merge + o_proj + add_inplace -> k_mv_wide<.., kAttnMerge, kResAdd>
+//   silu_mul                 -> k_mv_wide epilogue kSiluPair          (inference.metal:325-334)
+//   add_inplace              -> k_mv_wide epilogue kResAdd            (inference.metal:338-346)
+//   final rmsnorm + lm_head  -> k_matvec<.., kNorm, kLogits>          (inference.metal:113-186)
+//   argmax                   -> kLogits candidates + k_argmax         (inference.metal:300-321)
 // All arithmetic is f32 with bf16 weights widened exactly (u16 << 16).
 #include "kernels.h"
 
@@ -16,21 +18,6 @@
 
 namespace qe {
 namespace {
-
-// ---------------------------------------------------------------------------------------------
-// embed: x = bf16 row of the token read from the device token ring (inference.metal:98-107)
-// ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_embed(const uint16_t* __restrict__ table, uint32_t hidden, uint32_t vocab,
-                                               const uint32_t* __restrict__ tokens, const StepState* __restrict__ st,
-                                               float* __restrict__ x, uint32_t* err) {
-  uint32_t tok = tokens[st->tok_idx];
-  if (tok >= vocab) {
-    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(err, kErrToken);
-    tok = 0;
-  }
-  uint32_t i = blockIdx.x * 256 + threadIdx.x;
-  if (i < hidden) x[i] = bf16f(table[size_t(tok) * hidden + i]);
-}
 
 // ---------------------------------------------------------------------------------------------
 // matvec: out[r] = sum_c bf16(W[r,c]) * xin[c]   (cpu_inference.rs:225-257, inference.metal:143-186)
@@ -519,12 +506,6 @@ hipError_t launch_mv_cpl(const MatvecParams& p, hipStream_t s) {
 }
 
 }  // namespace
-
-hipError_t launch_embed(const uint16_t* table, uint32_t hidden, uint32_t vocab, const uint32_t* tokens,
-                        const StepState* st, float* x, uint32_t* err, hipStream_t s) {
-  hipLaunchKernelGGL(k_embed, dim3(ceil_div(hidden, 256)), dim3(256), 0, s, table, hidden, vocab, tokens, st, x, err);
-  return hipGetLastError();
-}
 
 uint32_t matvec_num_blocks(uint32_t rows, uint32_t cols, int epilogue) {
   const uint32_t nch = cols / 8;

@@ -122,7 +122,7 @@ int main(int argc, char** argv) {
     qe::AttnParams a{};
     a.qkv = qkv; a.q_norm = gains; a.k_norm = gains; a.rope = rope; a.rope_cur = rope_cur;
     a.k_cache = kc; a.v_cache = vc; a.partial = part; a.state = st; a.err = err;
-    a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f; a.norm_rope = 1;
+    a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f;
     CK(qe::launch_attention_split(a, splits, chunk, s));
     // merge + o_proj + residual
     p = qe::MatvecParams{};

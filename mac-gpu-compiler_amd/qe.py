@@ -315,7 +315,7 @@ def op_attention_work_bytes(n_heads: int, n_kv_heads: int, n_pos: int) -> int:
 
 
 def op_attention(q, k, v, out, n_pos: int, n_heads: int, n_kv_heads: int, work, n_splits: int = 0, stream=None) -> None:
-    """q [n_heads*128]; k, v [n_kv][kv_stride][128] f32; work zero-filled before first use."""
+    """q [n_heads*128]; k, v [n_kv][kv_stride][128] f32; work: op_attention_work_bytes() device bytes."""
     kv_stride = k.shape[1]
     _check(lib().qe_op_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_pos, kv_stride, n_heads, n_kv_heads,
                                  n_splits, _ptr(work), _stream_ptr(stream)))
