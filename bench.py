@@ -154,16 +154,17 @@ def graph_time_us(torch, launch, n: int, reps: int = 3) -> float:
         with torch.cuda.graph(g, stream=stream):
             for i in range(n):
                 launch(i)
-    g.replay()
-    torch.cuda.synchronize()
     best = float("inf")
-    for _ in range(reps):
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream)
+    with torch.cuda.stream(stream):  # replay() launches on the current stream: time it there
         g.replay()
-        e1.record(stream)
-        e1.synchronize()
-        best = min(best, e0.elapsed_time(e1) * 1e3 / n)
+        torch.cuda.synchronize()
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            g.replay()
+            e1.record(stream)
+            e1.synchronize()
+            best = min(best, e0.elapsed_time(e1) * 1e3 / n)
     del g
     return best
 

@@ -120,8 +120,11 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so branches on it are scalar
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
-  const uint32_t g = blockIdx.x, s = blockIdx.y, t0 = s * chunk;
+  const uint32_t g = blockIdx.x, s = blockIdx.y;
   const size_t head_base = size_t(g) * p.max_seq * D;
+  // Decode sizes the runs from the current length (below); the first tile is loaded up front
+  // for runs of a single tile, which is what every step up to 64 * splits positions has.
+  const uint32_t t0_first = DECODE ? s * T : s * chunk;
 
   __shared__ __align__(16) float qs[G][D];
   __shared__ __align__(16) float knew[D];
@@ -151,24 +154,30 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
   }
   KVTile<KV_BF16> A, B;
-  load_tile<KV_BF16>(A, p, head_base, t0, tid);
+  load_tile<KV_BF16>(A, p, head_base, t0_first, tid);
   __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from sinking these loads to their uses
 
   // a run with no cached position (t1 <= t0) goes through one all-masked tile and writes the
   // empty partial m = -inf, l = 0, acc = 0
-  uint32_t pos, n;
+  uint32_t pos, n, run, t0;
   bool owns_new = false;  // this run holds the new position
   if constexpr (DECODE) {
     pos = p.state->pos;
     const bool bad = pos >= p.max_seq;
     if (bad && g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
     n = bad ? 0u : pos + 1;
-    owns_new = !bad && pos >= t0 && pos < t0 + chunk;
+    // the n positions in gridDim.y runs of a whole number of tiles
+    run = T * ceil_div(max(n, 1u), T * gridDim.y);
+    t0 = s * run;
+    owns_new = !bad && pos >= t0 && pos < t0 + run;
+    if (run != T) load_tile<KV_BF16>(A, p, head_base, t0, tid);  // longer runs start elsewhere
   } else {
     n = p.n_pos_fixed;
     pos = n - 1;
+    run = chunk;
+    t0 = t0_first;
   }
-  const uint32_t t1 = min(n, t0 + chunk);
+  const uint32_t t1 = min(n, t0 + run);
   float* part = p.partial + (size_t(g) * gridDim.y + s) * G * kPartStride;
 
   // ---- q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215) ----
@@ -307,40 +316,50 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
 
 // ---------------------------------------------------------------------------------------------
 // The isolated op's merge: out[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s over the split
-// partials of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. One workgroup per
-// q head, one thread per dim; loads in batches of 16 splits, unconditional (clamped).
+// partials of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. One workgroup of
+// 8 x 128 threads per q head: group j (thread = dim) takes splits j, j+8, ..., all of its loads
+// issued at once (indexes past the last split re-read it and weigh 0); the 8 groups meet in LDS.
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
-                                                         float* __restrict__ out) {
-  constexpr int U = 16, PS = kPartStride;
-  const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x;
+__global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
+                                                             float* __restrict__ out) {
+  constexpr int U = kAttnMaxSplits / 8, PS = kPartStride;
+  const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x & (kHeadDim - 1), grp = threadIdx.x >> 7;
   const float* base = part + (size_t(g) * splits * G + j) * PS;
+  float mv[U], lv[U], av[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const float* q = base + size_t(min(grp + 8u * u, splits - 1)) * G * PS;
+    mv[u] = q[0];
+    lv[u] = q[1];
+    av[u] = q[4 + d];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   float M = -INFINITY;
-  for (uint32_t s0 = 0; s0 < splits; s0 += U) {
-    float mv[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) mv[u] = base[size_t(min(s0 + u, splits - 1)) * G * PS];
-#pragma unroll
-    for (int u = 0; u < U; u++) M = s0 + u < splits ? fmaxf(M, mv[u]) : M;
-  }
+  for (int u = 0; u < U; u++) M = grp + 8u * u < splits ? fmaxf(M, mv[u]) : M;
   float L = 0.f, A = 0.f;
-  for (uint32_t s0 = 0; s0 < splits; s0 += U) {
-    float mv[U], lv[U], av[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-      const float* q = base + size_t(min(s0 + u, splits - 1)) * G * PS;
-      mv[u] = q[0];
-      lv[u] = q[1];
-      av[u] = q[4 + d];
-    }
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const float e = (s0 + u < splits && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
-      L += e * lv[u];
-      A += e * av[u];
-    }
+  for (int u = 0; u < U; u++) {
+    const float e = (grp + 8u * u < splits && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
+    L += e * lv[u];
+    A += e * av[u];
   }
-  out[size_t(h) * kHeadDim + d] = A / L;
+  __shared__ float gm[8], gl[8], ga[8][kHeadDim];
+  if (d == 0) { gm[grp] = M; gl[grp] = L; }
+  ga[grp][d] = A;
+  __syncthreads();
+  if (grp != 0) return;
+  float MM = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < 8; k++) MM = fmaxf(MM, gm[k]);
+  float LL = 0.f, AA = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; k++) {
+    const float e = gm[k] == -INFINITY ? 0.f : expf(gm[k] - MM);  // a group with no run adds 0
+    LL += e * gl[k];
+    AA += e * ga[k][d];
+  }
+  out[size_t(h) * kHeadDim + d] = AA / LL;
 }
 
 // shapes the kernels support; the runs [s*chunk, (s+1)*chunk) must cover positions 0..n-1
@@ -371,11 +390,11 @@ hipError_t launch_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hi
 
 }  // namespace
 
-hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s) {
-  if (!attn_args_ok(p, splits, chunk, p.max_seq) || splits > uint32_t(kAttnMaxMergeSplits) || !p.state || !p.rope_cur ||
-      !p.q_norm || !p.k_norm || !p.err)
+hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, hipStream_t s) {
+  if (!attn_args_ok(p, splits, ceil_div(p.max_seq, max(splits, 1u)), p.max_seq) ||
+      splits > uint32_t(kAttnMaxMergeSplits) || !p.state || !p.rope_cur || !p.q_norm || !p.k_norm || !p.err)
     return hipErrorInvalidValue;
-  return launch_split<true>(p, splits, chunk, s);
+  return launch_split<true>(p, splits, 0, s);
 }
 
 hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
@@ -385,7 +404,7 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out);
+  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out);
   return hipGetLastError();
 }
 

@@ -109,7 +109,6 @@ struct qe_kv {
   uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
   uint32_t tok_cap = 0;
   uint32_t attn_splits = 1;
-  uint32_t attn_chunk = 1;      // positions per attention split (fixed per cache)
   bool eager = false;           // launch the step kernel by kernel instead of replaying the graph
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
@@ -368,7 +367,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     a.kv_bf16 = kv->dtype == QE_KV_BF16;
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
-    if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, kv->attn_chunk, s));
+    if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, s));
     // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
     p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
     p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
@@ -479,10 +478,10 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   HIP_TRY(hipMemcpyAsync(kv->rope, table.data(), rope_bytes, hipMemcpyHostToDevice, model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
 
-  // a fixed split of the cache into runs of >= 64 positions, at most kAttnMaxMergeSplits of them
-  // (the o_proj prologue merges that many partials per q head)
+  // attention workgroups per KV head: one per 64 cached positions, at most kAttnMaxMergeSplits
+  // (the o_proj prologue merges that many partials per q head); each step cuts its positions
+  // into that many runs of whole 64-position tiles
   kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
-  kv->attn_chunk = uint32_t((max_seq + kv->attn_splits - 1) / kv->attn_splits);
 
   // QE_LAUNCH=eager launches each step kernel by kernel (for tools that do not follow graph
   // replays, such as counter collection); otherwise one decode step is captured and replayed

@@ -78,13 +78,14 @@ hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipS
 uint32_t matvec_num_blocks(uint32_t rows, uint32_t cols, int epilogue);
 // the per-layer projections: ~1000 workgroups, x read per chunk from global memory
 hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue, hipStream_t s);
-// Decode-step attention with a fixed split of the cache into `splits` runs of `chunk` positions
-// (host-chosen from max_seq): each workgroup writes (m, l, acc) partials, runs past pos write an
-// empty partial, and the o_proj matvec merges them in its prologue (kAttnMerge).
+// Decode-step attention: grid (n_kv, splits); at each step the n = pos + 1 cached positions are
+// cut into `splits` runs of a whole number of 64-position tiles, each workgroup writes its (m, l,
+// acc) partials (runs past pos write empty ones), and the o_proj matvec merges them in its
+// prologue (kAttnMerge).
 constexpr int kAttnMaxMergeSplits = 16;
 // one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
 constexpr int kPartStride = 4 + kHeadDim;
-hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s);
+hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, hipStream_t s);
 // The isolated op: final q [n_heads][D], complete K/V [n_kv][max_seq][D] (f32), positions
 // 0..n_pos_fixed-1 in `splits` runs (<= kAttnMaxSplits), partials merged into out [n_heads][D].
 hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);

@@ -91,7 +91,7 @@ int main(int argc, char** argv) {
   qe::ArgCand* cand = dalloc<qe::ArgCand>(n_cand);
   float* kc = dalloc<float>(size_t(NKV) * max_seq * D);
   float* vc = dalloc<float>(size_t(NKV) * max_seq * D);
-  const uint32_t splits = (max_seq + 63) / 64, chunk = (max_seq + splits - 1) / splits;
+  const uint32_t splits = (max_seq + 63) / 64;
   float* part = dalloc<float>(size_t(NKV) * splits * G * qe::kPartStride);
   float* rope = dalloc<float>(size_t(max_seq) * D);
   float* rope_cur = dalloc<float>(D);
@@ -123,7 +123,7 @@ int main(int argc, char** argv) {
     a.qkv = qkv; a.q_norm = gains; a.k_norm = gains; a.rope = rope; a.rope_cur = rope_cur;
     a.k_cache = kc; a.v_cache = vc; a.partial = part; a.state = st; a.err = err;
     a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f;
-    CK(qe::launch_attention_split(a, splits, chunk, s));
+    CK(qe::launch_attention_split(a, splits, s));
     // merge + o_proj + residual
     p = qe::MatvecParams{};
     p.w = Wc + n_qkv; p.rows = H; p.cols = QD; p.out = x;
