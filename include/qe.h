@@ -104,6 +104,21 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
 int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv,
               qe_on_token on_token, void* user, float* logits_per_step);
 
+/* ---- multi-token forward on the matrix cores (no reference counterpart: the reference's
+ *      prompt loop calls forward once per token, bench.rs:174-176) ---- */
+/* Chunked prefill: runs ids[0..n) at positions start_pos.. through the model in chunks of up to
+ * `chunk` tokens (0 = 512, at most 512): one bf16 MFMA GEMM per projection and chunk, f32
+ * activations split into two bf16 halves (about 16 mantissa bits), causal attention over the
+ * cache and the chunk. Appends the K/V of every position and writes the last token's logits
+ * (nullable). Same position contract as qe_prefill; logits agree with it within 1e-2, not bit for
+ * bit. The model's chunk buffers are allocated on first use. */
+int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv,
+                     uint32_t chunk, float* last_logits);
+/* Verify k (1..64) tokens at positions start_pos.. in one pass (the k-token check of speculative
+ * decoding): appends their K/V and writes all k logit rows, logits_out [k][vocab_size]. */
+int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv,
+              float* logits_out);
+
 /* ---- per-stage kernel timing: runs `token` at `pos` like qe_forward, then times each stage
  *      of the step (qkv, attention, o_proj, gate_up, down, lm_head, argmax) as a graph of that
  *      stage's launches only (28 per-layer launches, or one), replayed 8 times between two HIP
@@ -129,6 +144,11 @@ void qe_random_prompt(uint64_t seed, uint64_t n, uint32_t vocab, uint32_t* out);
  * inference.metal:143-186 / cpu_inference.rs:225-257. cols % 8 == 0, w 16-byte aligned. */
 int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, uint64_t cols,
                       void* stream);
+/* c[i][j] = sum_k a[i][k] bf16(w[j][k]): the chunked prefill's GEMM (a f32 [m][k] split into two
+ * bf16 halves, w bf16 [n][k], f32 accumulate on the matrix cores). n even, k % 32 == 0,
+ * a and w 16-byte aligned. No reference counterpart (the reference has no batched path). */
+int qe_op_gemm_bf16(const float* a, const void* w, float* c, uint64_t m, uint64_t n, uint64_t k,
+                    void* stream);
 /* One decode step of GQA attention (cpu_inference.rs:144-162, inference.metal:234-296) for
  * head_dim 128: q [n_heads*128] (post q-norm and RoPE), k/v caches laid out
  * [n_kv_heads][kv_stride][128] f32, attending positions 0..n_pos-1; out [n_heads*128].

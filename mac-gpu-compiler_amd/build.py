@@ -13,7 +13,7 @@ ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libqe.so")
 
-SOURCES = ["engine.hip", "kernels.hip", "attention.hip", "checkpoint.cpp"]
+SOURCES = ["engine.hip", "kernels.hip", "attention.hip", "batch.hip", "checkpoint.cpp"]
 
 HIPCC_FLAGS = [
     "-O3",

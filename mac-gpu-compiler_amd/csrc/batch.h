@@ -1,0 +1,49 @@
+// Launch wrappers of the multi-token (chunked prefill / verify) kernels, gfx950 bf16 MFMA.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "kernels.h"
+
+namespace qe {
+
+enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2 };
+
+// C[m][n] (=, +=) sum_k A'[m][k] W[n][k] for m < M, n < N; A' = A, or A x rowscale[m] x gain[k]
+// (an RMSNorm) when the launch asks for the norm. kGemmSiluPair: W rows 2i / 2i+1 are gate_i /
+// up_i and C[m][i] = silu(gate) * up. N even, K % 32 == 0, lda % 4 == 0.
+struct GemmParams {
+  const float* A;
+  uint32_t lda;
+  const float* rowscale;  // [M]
+  const uint16_t* gain;   // bf16 [K]
+  const uint16_t* W;      // bf16 [N][K]
+  uint32_t M, N, K;
+  float* C;
+  uint32_t ldc;
+};
+
+struct BatchAttnParams {
+  const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections
+  float* q;                // [M][n_heads][128] normalized + rotated q
+  float* att;              // [M][n_heads][128] attention output
+  const uint16_t* q_norm;  // bf16 [128]
+  const uint16_t* k_norm;
+  const float* rope;       // [max_seq][64](cos, sin)
+  void* k_cache;           // layer base [n_kv][max_seq][128]
+  void* v_cache;
+  uint32_t M, start, max_seq, n_heads, n_kv;
+  float eps, scale;
+  int kv_bf16;
+};
+
+hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
+hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
+hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
+hipError_t launch_attn_causal(const BatchAttnParams& p, hipStream_t st);
+hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
+                             hipStream_t st);
+
+}  // namespace qe

@@ -5,6 +5,7 @@
 // decode, commit_step) and cpu_inference.rs (the loader contract and the byte formula).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -15,6 +16,7 @@
 #include <vector>
 
 #include "../../include/qe.h"
+#include "batch.h"
 #include "checkpoint.h"
 #include "kernels.h"
 
@@ -56,6 +58,9 @@ struct Layer {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+constexpr uint32_t kBatchMaxChunk = 512;   // tokens per chunk of qe_prefill_batch
+constexpr uint32_t kVerifyMaxTokens = 64;  // tokens of one qe_verify call
+
 }  // namespace
 
 struct qe_model {
@@ -84,11 +89,18 @@ struct qe_model {
   float* h_logits = nullptr;
   uint32_t* h_small = nullptr;  // [0..3] state staging, [4] error word
   uint64_t weight_bytes = 0;
+  // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
+  uint8_t* batch_mem = nullptr;
+  uint32_t batch_cap = 0, batch_logit_rows = 0;
+  float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
+  float* blogits = nullptr;
+  uint32_t* bids = nullptr;
 
   ~qe_model() {  // teardown errors have nowhere to go; the handle is gone either way
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
     if (scratch) (void)hipFree(scratch);
+    if (batch_mem) (void)hipFree(batch_mem);
     if (h_logits) (void)hipHostFree(h_logits);
     if (h_small) (void)hipHostFree(h_small);
     if (stream) (void)hipStreamDestroy(stream);
@@ -394,6 +406,88 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
   return QE_OK;
 }
 
+// Multi-token buffers for up to `cap` tokens and `logit_rows` full logit rows.
+int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
+  if (m->batch_mem && cap <= m->batch_cap && logit_rows <= m->batch_logit_rows) return QE_OK;
+  cap = std::max(cap, m->batch_cap);
+  logit_rows = std::max(logit_rows, m->batch_logit_rows);
+  const qe_config& c = m->cfg;
+  const size_t H = c.hidden_size, I = c.intermediate_size, D = c.head_dim;
+  const size_t QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
+  size_t off = 0;
+  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
+  const size_t ox = take(cap * H * 4), os = take(cap * 4), oqkv = take(cap * (QD + 2 * KD) * 4),
+               oq = take(cap * QD * 4), oatt = take(cap * QD * 4), oh = take(cap * I * 4),
+               ologit = take(size_t(logit_rows) * c.vocab_size * 4), oids = take(cap * 4);
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  if (m->batch_mem) HIP_TRY(hipFree(m->batch_mem));
+  m->batch_mem = nullptr;
+  HIP_TRY(hipMalloc(&m->batch_mem, off));
+  m->batch_cap = cap;
+  m->batch_logit_rows = logit_rows;
+  m->bx = reinterpret_cast<float*>(m->batch_mem + ox);
+  m->bs = reinterpret_cast<float*>(m->batch_mem + os);
+  m->bqkv = reinterpret_cast<float*>(m->batch_mem + oqkv);
+  m->bq = reinterpret_cast<float*>(m->batch_mem + oq);
+  m->batt = reinterpret_cast<float*>(m->batch_mem + oatt);
+  m->bh = reinterpret_cast<float*>(m->batch_mem + oh);
+  m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
+  m->bids = reinterpret_cast<uint32_t*>(m->batch_mem + oids);
+  return QE_OK;
+}
+
+// One chunk of M tokens (ids already in m->bids) at positions start..start+M-1 through every
+// layer, appending their K/V. all_logits: logits of every row to m->blogits [M][V]; otherwise
+// the last row's logits to m->logits (the decode step's buffer).
+int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_logits) {
+  const qe_config& c = m->cfg;
+  const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
+  const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
+  const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
+  const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
+  hipStream_t s = m->stream;
+  const float eps = c.rms_norm_eps;
+  auto gemm = [&](const float* A, uint32_t lda, const uint16_t* gain, const uint16_t* W, uint32_t N, uint32_t K,
+                  float* C, uint32_t ldc, int epi) -> int {
+    if (gain) HIP_TRY(qe::launch_rownorm(A, M, K, eps, m->bs, s));
+    qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc};
+    HIP_TRY(qe::launch_gemm(g, gain != nullptr, epi, s));
+    return QE_OK;
+  };
+  int rc;
+  HIP_TRY(qe::launch_embed_rows(m->embed, m->bids, M, H, m->bx, s));
+  for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
+    const Layer& w = m->layers[l];
+    // input_layernorm + q|k|v (cpu_inference.rs:129-132)
+    if ((rc = gemm(m->bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
+    // q/k norm + RoPE, K/V append, causal attention (cpu_inference.rs:134-162)
+    qe::BatchAttnParams a{};
+    a.qkv = m->bqkv; a.q = m->bq; a.att = m->batt; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
+    a.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
+    a.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
+    a.M = M; a.start = start; a.max_seq = uint32_t(kv->max_seq);
+    a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
+    a.eps = eps; a.scale = 1.0f / sqrtf(float(D)); a.kv_bf16 = kv->dtype == QE_KV_BF16;
+    HIP_TRY(qe::launch_qk_rope(a, s));
+    HIP_TRY(qe::launch_attn_causal(a, s));
+    // o_proj + residual (cpu_inference.rs:163-164)
+    if ((rc = gemm(m->batt, QD, nullptr, w.w_o, H, QD, m->bx, H, qe::kGemmResAdd))) return rc;
+    // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)
+    if ((rc = gemm(m->bx, H, w.w_post, w.w_gu, 2 * I, H, m->bh, I, qe::kGemmSiluPair))) return rc;
+    if ((rc = gemm(m->bh, I, nullptr, w.w_down, H, I, m->bx, H, qe::kGemmResAdd))) return rc;
+  }
+  // final norm + lm_head (cpu_inference.rs:175-178)
+  if (all_logits) {
+    if ((rc = gemm(m->bx, H, m->final_norm, m->lm_head, V, H, m->blogits, V, qe::kGemmStore))) return rc;
+  } else {
+    MatvecParams p{};
+    p.eps = eps; p.w = m->lm_head; p.x = m->bx + size_t(M - 1) * H; p.nw = m->final_norm;
+    p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
+    HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  }
+  return QE_OK;
+}
+
 // host -> device: state {pos, tok_idx = 0} and tokens[0] = token, through pinned staging; the
 // RoPE row of pos becomes rope_cur (k_argmax advances it with pos after every step)
 int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
@@ -617,6 +711,58 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
   return QE_OK;
 }
 
+int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv, uint32_t chunk,
+                     float* last_logits) {
+  if (!model || !kv || (!ids && n)) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (n == 0) return QE_OK;
+  if (chunk == 0) chunk = kBatchMaxChunk;
+  if (chunk > kBatchMaxChunk) return fail(QE_ERR_ARG, "chunk %u above %u", chunk, kBatchMaxChunk);
+  if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
+  if (start_pos + n > kv->max_seq) return fail(QE_ERR_POS, "prompt end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + n), (unsigned long long)kv->max_seq);
+  for (uint64_t i = 0; i < n; i++)
+    if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
+  int rc = ensure_batch(model, chunk, 0);
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  for (uint64_t done = 0; done < n;) {
+    const uint32_t M = uint32_t(std::min<uint64_t>(chunk, n - done));
+    // the previous chunk's kernels read bids: its copy waits for them on the same stream
+    HIP_TRY(hipMemcpyAsync(model->bids, ids + done, size_t(M) * 4, hipMemcpyHostToDevice, model->stream));
+    HIP_TRY(hipStreamSynchronize(model->stream));
+    if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), false))) return rc;
+    done += M;
+  }
+  if (last_logits) {
+    HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost, model->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  if (last_logits) memcpy(last_logits, model->h_logits, model->cfg.vocab_size * 4);
+  kv->len = start_pos + n;
+  return QE_OK;
+}
+
+int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv, float* logits_out) {
+  if (!model || !kv || !ids || !logits_out) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (k == 0 || k > kVerifyMaxTokens) return fail(QE_ERR_ARG, "k must be 1..%u", kVerifyMaxTokens);
+  if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
+  if (start_pos + k > kv->max_seq) return fail(QE_ERR_POS, "verify end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + k), (unsigned long long)kv->max_seq);
+  for (uint64_t i = 0; i < k; i++)
+    if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
+  int rc = ensure_batch(model, uint32_t(k), uint32_t(k));
+  if (rc) return rc;
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  HIP_TRY(hipMemcpyAsync(model->bids, ids, size_t(k) * 4, hipMemcpyHostToDevice, model->stream));
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), true))) return rc;
+  HIP_TRY(hipMemcpyAsync(logits_out, model->blogits, size_t(k) * model->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                         model->stream));
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  kv->len = std::max<uint64_t>(kv->len, start_pos + k);
+  return QE_OK;
+}
+
 int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv, qe_on_token on_token,
               void* user, float* logits_per_step) {
   if (!model || !kv) return fail(QE_ERR_ARG, "null argument");
@@ -680,6 +826,18 @@ int qe_op_matvec_bf16(const void* w, const float* x, float* out, uint64_t rows, 
   const bool wide = cols / 8 <= 512 && rows <= 16384;
   HIP_TRY(wide ? qe::launch_matvec_wide(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream))
                : qe::launch_matvec(p, qe::kCopy, qe::kStore, static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+int qe_op_gemm_bf16(const float* a, const void* w, float* c, uint64_t m, uint64_t n, uint64_t k, void* stream) {
+  if (!a || !w || !c) return fail(QE_ERR_ARG, "null argument");
+  if (m == 0 || n == 0 || k == 0 || n % 2 || k % 32 || m > 0xFFFFFFFFull || n > 0xFFFFFFFFull || k > 0xFFFFFFFFull)
+    return fail(QE_ERR_ARG, "need m > 0, n even, k a multiple of 32");
+  if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
+    return fail(QE_ERR_ARG, "a and w must be 16-byte aligned");
+  qe::GemmParams g{a, uint32_t(k), nullptr, nullptr, static_cast<const uint16_t*>(w), uint32_t(m), uint32_t(n),
+                   uint32_t(k), c, uint32_t(n)};
+  HIP_TRY(qe::launch_gemm(g, false, qe::kGemmStore, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }
 

@@ -147,6 +147,9 @@ def lib() -> ctypes.CDLL:
         "qe_profile_step": (i32, [vp, u32, u64, vp, f32p, ctypes.POINTER(u32), ctypes.POINTER(ctypes.c_char_p),
                                   u32, ctypes.POINTER(u32)]),
         "qe_decode": (i32, [vp, u32, u64, u64, vp, ON_TOKEN, vp, f32p]),
+        "qe_prefill_batch": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, u32, f32p]),
+        "qe_verify": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, f32p]),
+        "qe_op_gemm_bf16": (i32, [vp, vp, vp, u64, u64, u64, vp]),
         "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
         "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
         "qe_op_matvec_bf16": (i32, [vp, vp, vp, u64, u64, vp]),
@@ -223,6 +226,22 @@ class Model:
         _check(lib().qe_profile_step(self._h, int(token), int(pos), cache._h, _fptr(us), launches, names, cap,
                                      ctypes.byref(n)))
         return [(names[i].decode(), float(us[i]), int(launches[i])) for i in range(min(n.value, cap))]
+
+    def prefill_batch(self, ids, start_pos: int, cache: "KVCache", chunk: int = 0, want_logits: bool = True):
+        """Chunked prefill on the matrix cores (qe_prefill_batch): the last token's logits or None."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(self.config().vocab_size, dtype=np.float32) if want_logits else None
+        _check(lib().qe_prefill_batch(self._h, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids),
+                                      int(start_pos), cache._h, int(chunk), _fptr(out) if want_logits else None))
+        return out
+
+    def verify(self, ids, start_pos: int, cache: "KVCache") -> np.ndarray:
+        """k tokens in one pass (qe_verify): logits [k, vocab]."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty((len(ids), self.config().vocab_size), dtype=np.float32)
+        _check(lib().qe_verify(self._h, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids),
+                               int(start_pos), cache._h, _fptr(out)))
+        return out
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",
                on_token: Optional[Callable[[int], None]] = None, want_logits: bool = False):
@@ -308,6 +327,13 @@ def op_matvec_bf16(w, x, out, stream=None) -> None:
     """out[r] = sum_c w[r, c] x[c]; w bf16 [rows, cols] (torch.bfloat16 or int16/uint16 view), x f32."""
     rows, cols = w.shape
     _check(lib().qe_op_matvec_bf16(_ptr(w), _ptr(x), _ptr(out), rows, cols, _stream_ptr(stream)))
+
+
+def op_gemm_bf16(a, w, c, stream=None) -> None:
+    """c [m, n] = a [m, k] (f32) @ w [n, k] (bf16)^T on the matrix cores."""
+    m, k = a.shape
+    n = w.shape[0]
+    _check(lib().qe_op_gemm_bf16(_ptr(a), _ptr(w), _ptr(c), m, n, k, _stream_ptr(stream)))
 
 
 def op_attention_work_bytes(n_heads: int, n_kv_heads: int, n_pos: int) -> int:

@@ -1,0 +1,126 @@
+"""Multi-token forward (chunked prefill, k-token verify) on the matrix cores, through the C ABI.
+
+The reference has only token-by-token prefill (bench.rs:174-176), so its own invariant is the
+oracle: chunked logits must equal sequential forward logits within the parity bar
+(tests/metal_parity.rs:14), and decoding must continue from a chunk-prefilled cache exactly as from
+a sequentially prefilled one.
+"""
+import numpy as np
+import pytest
+
+import oracle
+import qe
+from conftest import DECODE_STEPS, PROMPT_LEN, PROMPT_SEED, TINY
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS_DIFF = 1e-2  # tests/metal_parity.rs:14
+
+
+def bf16_round(a: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bits (round to nearest even), as uint16"""
+    u = a.astype(np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16
+    return u.astype(np.uint16)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 64, 32), (5, 128, 64), (64, 1024, 1024), (100, 4096, 1024),
+                                   (512, 1024, 3072), (37, 6144, 1024), (4, 32768, 1024), (3, 1000, 256)])
+def test_gemm_matches_float64(gpu, m, n, k):
+    import torch
+    rng = np.random.default_rng(m * 7 + n + k)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    w16 = bf16_round(rng.standard_normal((n, k)).astype(np.float32) * 0.05)
+    wf = (w16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    ref = a.astype(np.float64) @ wf.T
+    at, wt = torch.from_numpy(a).cuda(), torch.from_numpy(w16.view(np.int16)).cuda()
+    ct = torch.full((m, n), float("nan"), device="cuda")
+    qe.op_gemm_bf16(at, wt, ct)
+    torch.cuda.synchronize()
+    got = ct.cpu().numpy().astype(np.float64)
+    # a is split into two bf16 halves (|error| <= 2^-17 |a|); f32 accumulation over k terms
+    bound = (2.0 ** -16 + k * 2.0 ** -24) * (np.abs(a).astype(np.float64) @ np.abs(wf).T) + 1e-30
+    assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) / bound)}"
+
+
+@pytest.mark.parametrize("n_prompt,chunk", [(1, 0), (100, 32), (300, 0), (513, 512)])
+def test_tiny_prefill_batch_matches_oracle(gpu, tiny_ckpt, n_prompt, chunk):
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    prompt = qe.random_prompt(29, n_prompt, TINY.vocab_size)
+    cache = qe.KVCache(m, n_prompt + 24)
+    got = m.prefill_batch(prompt, 0, cache, chunk=chunk)
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        ref = om.forward(int(tok), pos, oc)
+    d = float(np.max(np.abs(got - ref)))
+    assert d < 1e-3, f"last-token logits diverge by {d}"
+    assert oracle.argmax(got) == oracle.argmax(ref)
+    assert len(cache) == n_prompt
+    # decoding continues from the chunk-filled cache like the oracle does
+    tok = oracle.argmax(ref)
+    toks, logits = m.decode(tok, n_prompt, 20, cache, want_logits=True)
+    for i in range(20):
+        ref = om.forward(tok, n_prompt + i, oc)
+        d = float(np.max(np.abs(logits[i] - ref)))
+        assert d < 1e-3, f"decode step {i} after chunked prefill: {d}"
+        tok = oracle.argmax(ref)
+        assert toks[i] == tok
+
+
+@pytest.mark.parametrize("k", [1, 4, 17])
+def test_tiny_verify_matches_oracle(gpu, tiny_ckpt, k):
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    prefix = qe.random_prompt(31, 40, TINY.vocab_size)
+    draft = qe.random_prompt(37, k, TINY.vocab_size)
+    cache = qe.KVCache(m, 40 + k)
+    m.prefill(prefix, 0, cache, want_logits=False)
+    rows = m.verify(draft, 40, cache)
+    oc = om.new_cache()
+    for pos, tok in enumerate(prefix):
+        om.forward(int(tok), pos, oc)
+    for i, tok in enumerate(draft):
+        ref = om.forward(int(tok), 40 + i, oc)
+        d = float(np.max(np.abs(rows[i] - ref)))
+        assert d < 1e-3, f"verify row {i}: {d}"
+        assert oracle.argmax(rows[i]) == oracle.argmax(ref)
+    assert len(cache) == 40 + k
+
+
+def test_batch_argument_errors(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    cache = qe.KVCache(m, 8)
+    with pytest.raises(qe.QeError) as e:
+        m.prefill_batch(np.arange(9, dtype=np.uint32), 0, cache)  # past max_seq
+    assert e.value.code == qe.QE_ERR_POS
+    with pytest.raises(qe.QeError) as e:
+        m.prefill_batch(np.arange(4, dtype=np.uint32), 0, cache, chunk=513)
+    assert e.value.code == qe.QE_ERR_ARG
+    with pytest.raises(qe.QeError) as e:
+        m.verify(np.zeros(65, dtype=np.uint32), 0, qe.KVCache(m, 80))
+    assert e.value.code == qe.QE_ERR_ARG
+    with pytest.raises(qe.QeError) as e:
+        m.verify(np.zeros(2, dtype=np.uint32), 3, cache)  # nothing cached at 0..2
+    assert e.value.code == qe.QE_ERR_POS
+
+
+@pytest.mark.slow
+def test_real_prefill_batch_then_decode_matches_fixture(gpu, real_ckpt):
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qwen3_0_6b_decode.npz"),
+                allow_pickle=False)
+    m = qe.Model.load_model(real_ckpt)
+    V = m.config().vocab_size
+    prompt = qe.random_prompt(PROMPT_SEED, PROMPT_LEN, V)
+    cache = qe.KVCache(m, PROMPT_LEN + DECODE_STEPS + 1)
+    logits = m.prefill_batch(prompt, 0, cache, chunk=64)  # three chunks, the last one partial
+    first = oracle.argmax(logits)
+    toks, step_logits = m.decode(first, PROMPT_LEN, DECODE_STEPS, cache, want_logits=True)
+    got = [first] + toks
+    ref = [int(t) for t in g["tokens"]]
+    assert got == ref, f"greedy tokens diverge at {next(i for i in range(len(ref)) if got[i] != ref[i])}"
+    idx = g["sample_idx"]
+    for i, lg in enumerate(np.concatenate([logits[None], step_logits])):
+        assert np.max(np.abs(lg[idx] - g["sample_val"][i])) < MAX_ABS_DIFF, f"step {i}"
+        assert np.max(np.abs(lg[g["top_idx"][i]] - g["top_val"][i])) < MAX_ABS_DIFF, f"step {i}"
