@@ -228,6 +228,78 @@ def sweep_attention(torch, qe, ceiling: float, repeats: int):
     return rows
 
 
+def prefill_bench(torch, qe, model, cfg, args):
+    """Config 5: a 2048-token random prompt prefilled in chunks of 512 on the matrix cores
+    (qe_prefill_batch), then k = 4 verify passes (qe_verify) against single decode steps.
+    GEMM work per chunk = 2 M x (all projection weights) FLOP; the kernels issue it twice (the
+    activations are split into two bf16 halves). Causal attention = 8192 x sum(p + 1) x L FLOP."""
+    n, chunk = args.prefill_tokens, args.chunk
+    ids = qe.random_prompt(11, n, cfg.vocab_size)
+    cache = qe.KVCache(model, n + 8)
+    model.prefill_batch(ids[:chunk], 0, cache, chunk=chunk, want_logits=False)  # warm-up, buffers
+    stream = torch.cuda.ExternalStream(model.stream_handle())
+    best = float("inf")
+    for _ in range(3):
+        cache = qe.KVCache(model, n + 8)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill_batch(ids, 0, cache, chunk=chunk, want_logits=False)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_hidden_layers
+    QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
+    proj = L * ((QD + 2 * KD) * H + H * QD + 2 * I * H + H * I)
+    gemm_flop = 2.0 * n * proj
+    attn_flop = 8192.0 * sum(p + 1 for p in range(n)) * L
+    # the engine's matrix-core work: both bf16 halves of every GEMM
+    mfma_flop = 2 * gemm_flop
+    # on-box bf16 GEMM ceiling: torch (hipBLASLt) at the largest projection shape of a chunk
+    a = torch.randn(chunk, H, device="cuda", dtype=torch.bfloat16)
+    w = torch.randn(2 * I, H, device="cuda", dtype=torch.bfloat16)
+    wt = w.t().contiguous()
+    for _ in range(3):
+        torch.matmul(a, wt)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(50):
+        torch.matmul(a, wt)
+    e1.record()
+    e1.synchronize()
+    lib_tflops = 2.0 * chunk * 2 * I * H * 50 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    # k = 4 verify vs one decode step, on a cache holding the prompt
+    draft = qe.random_prompt(13, 4, cfg.vocab_size)
+    vcache = qe.KVCache(model, n + 16)
+    model.prefill_batch(ids, 0, vcache, chunk=chunk, want_logits=False)
+    model.verify(draft, n, vcache)
+    t0 = time.perf_counter()
+    reps = 20
+    for _ in range(reps):
+        model.verify(draft, n, vcache)
+    verify_ms = (time.perf_counter() - t0) / reps * 1e3
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        model.forward(int(draft[0]), n, vcache)
+    forward_ms = (time.perf_counter() - t0) / reps * 1e3
+    return {
+        "metric": "prefill tok/s (2048-token prompt, chunks of 512, bf16 MFMA)",
+        "value": round(n / best, 1),
+        "unit": "tok/s",
+        "ms": round(best * 1e3, 3),
+        "prompt_tokens": n,
+        "chunk": chunk,
+        "gemm_flop": gemm_flop,
+        "attention_flop": attn_flop,
+        "achieved_tflops_algorithmic": round((gemm_flop + attn_flop) / best / 1e12, 2),
+        "mfma_tflops_issued": round(mfma_flop / best / 1e12, 2),
+        "mfma_peak_tflops": 2500.0,
+        "hipblaslt_bf16_tflops_same_shape": round(lib_tflops, 1),
+        "verify_k4_ms": round(verify_ms, 3),
+        "forward_1_ms": round(forward_ms, 3),
+        "verify_k4_tokens_per_s_if_all_accepted": round(4 / verify_ms * 1e3, 1),
+    }
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -240,7 +312,9 @@ def main():
     ap.add_argument("--no-profile", action="store_true",
                     help="skip the per-stage timing graphs (for counter-collection runs under QE_LAUNCH=eager)")
     ap.add_argument("--json-out", default=None, help="also write a detailed result JSON here")
-    ap.add_argument("--mode", choices=["decode", "matvec-sweep", "attention-sweep"], default="decode",
+    ap.add_argument("--prefill-tokens", type=int, default=2048)
+    ap.add_argument("--chunk", type=int, default=512)
+    ap.add_argument("--mode", choices=["decode", "matvec-sweep", "attention-sweep", "prefill"], default="decode",
                     help="decode: the batch-1 decode benchmark (one JSON line); the sweeps time the isolated "
                          "matvec at every model shape or the isolated attention at 128..32768 positions")
     ap.add_argument("--repeats", type=int, default=1000, help="launches per shape in the sweeps")
@@ -266,7 +340,7 @@ def main():
 
     ceiling = measured_read_ceiling(torch, qe)
     log(f"measured HBM read ceiling: {ceiling:.1f} GB/s")
-    if args.mode != "decode":
+    if args.mode in ("matvec-sweep", "attention-sweep"):
         sweep = sweep_matvec if args.mode == "matvec-sweep" else sweep_attention
         rows = sweep(torch, qe, ceiling, args.repeats)
         result = {"metric": f"isolated {args.mode.split('-')[0]} GB/s (algorithmic bytes / launch time)",
@@ -284,6 +358,14 @@ def main():
     model = qe.Model.load_model(ckpt)
     log(f"loaded model in {time.time() - t0:.1f}s")
     cfg = model.config()
+    if args.mode == "prefill":
+        result = dict(prefill_bench(torch, qe, model, cfg, args), n_gpus=1, data="synthetic",
+                      measured_ceiling_gbs=round(ceiling, 1))
+        if args.json_out:
+            with open(args.json_out, "w") as f:
+                json.dump(result, f, indent=1)
+        print(json.dumps(result), flush=True)
+        return
     kv_dtype = qe.QE_KV_BF16 if args.kv == "bf16" else qe.QE_KV_F32
     prompt = qe.random_prompt(PROMPT_SEED, args.prompt_len, cfg.vocab_size)
     K, W = args.steps, args.warmup

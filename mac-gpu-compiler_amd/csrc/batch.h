@@ -11,6 +11,9 @@ namespace qe {
 
 enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2 };
 
+// most key runs the causal attention of a chunk is split into (partials merged after)
+constexpr int kBatchMaxRuns = 32;
+
 // C[m][n] (=, +=) sum_k A'[m][k] W[n][k] for m < M, n < N; A' = A, or A x rowscale[m] x gain[k]
 // (an RMSNorm) when the launch asks for the norm. kGemmSiluPair: W rows 2i / 2i+1 are gate_i /
 // up_i and C[m][i] = silu(gate) * up. N even, K % 32 == 0, lda % 4 == 0.
@@ -29,12 +32,14 @@ struct BatchAttnParams {
   const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections
   float* q;                // [M][n_heads][128] normalized + rotated q
   float* att;              // [M][n_heads][128] attention output
+  float* part;             // [M][n_heads][runs][kPartStride] partials (several key runs)
   const uint16_t* q_norm;  // bf16 [128]
   const uint16_t* k_norm;
   const float* rope;       // [max_seq][64](cos, sin)
   void* k_cache;           // layer base [n_kv][max_seq][128]
   void* v_cache;
   uint32_t M, start, max_seq, n_heads, n_kv;
+  uint32_t key_run;        // positions per key run (set by launch_attn_causal)
   float eps, scale;
   int kv_bf16;
 };
@@ -42,7 +47,11 @@ struct BatchAttnParams {
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
 hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
-hipError_t launch_attn_causal(const BatchAttnParams& p, hipStream_t st);
+// causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
+hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);
+// key runs for a chunk of M tokens at positions start.. : enough workgroups to cover the chip,
+// at least two 32-position tiles per run
+uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv);
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
                              hipStream_t st);
 

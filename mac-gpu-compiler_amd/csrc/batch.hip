@@ -11,6 +11,7 @@
 //   k_attn_causal  token m attends positions 0..start+m               (cpu_inference.rs:144-162)
 #include "batch.h"
 
+#include <algorithm>
 #include <cmath>
 
 #include "device_common.h"
@@ -191,17 +192,20 @@ __global__ __launch_bounds__(256) void k_qk_rope(BatchAttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal attention of a chunk: workgroup (KV head g, block of QB = 16 / G tokens) serves its 16
-// query vectors (token mb + v / G, head g G + v % G) over positions 0 .. start + last token of
-// the block, in LDS tiles of T = 32 positions, with an online softmax per query vector (divide
-// by the sum at the end). Thread (v = tid / 16, kk = tid % 16): scores for keys kk and kk + 16
-// of the tile (K rows padded to 129 floats, so the 16 keys sit in 16 banks), then dims
-// kk + 16 i (i < 8) of the output. Out: att [M][n_heads][128].
+// Causal attention of a chunk: workgroup (KV head g, block of QB = 16 / G tokens, key run s)
+// serves its 16 query vectors (token mb + v / G, head g G + v % G) over the positions of run s,
+// [s key_run, (s+1) key_run) cut at start + the block's last token, in LDS tiles of T = 32
+// positions, with an online softmax per query vector. Thread (v = tid / 16, kk = tid % 16):
+// scores for keys kk and kk + 16 of the tile (K rows padded to 129 floats, so the 16 keys sit in
+// 16 banks), then dims kk + 16 i (i < 8) of the output. With one run the output is normalized
+// into att [M][n_heads][128]; with several, each writes its (m, l, acc) partial to
+// part [M][n_heads][runs][kPartStride] (a query vector with no visible key in the run writes
+// m = -inf, l = 0) and k_attn_merge_rows combines them.
 // ---------------------------------------------------------------------------------------------
 template <int G, bool KV_BF16>
 __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
   constexpr int D = kHeadDim, T = 32, NQ = 16, QB = NQ / G, KP = D + 1;
-  const uint32_t g = blockIdx.x, mb = blockIdx.y * QB;
+  const uint32_t g = blockIdx.x, mb = blockIdx.y * QB, run = blockIdx.z, runs = gridDim.z;
   const int tid = threadIdx.x, qv = tid >> 4, kk = tid & 15;
   __shared__ __align__(16) float qs[NQ][D];
   __shared__ float ks[T][KP];
@@ -220,17 +224,19 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
   const uint32_t my_m = mb + uint32_t(qv / G);
   const uint32_t my_pos = p.start + min(my_m, p.M - 1);
   const uint32_t last = p.start + min(mb + QB - 1, p.M - 1);  // positions 0..last are needed
+  const uint32_t k_begin = run * p.key_run;
+  const uint32_t k_end = min(last + 1, k_begin + p.key_run);  // this run: positions [k_begin, k_end)
   float m_run = -INFINITY, l_run = 0.f;
   float acc[8];
 #pragma unroll
   for (int i = 0; i < 8; i++) acc[i] = 0.f;
   const size_t head = size_t(g) * p.max_seq * D;
   const int lr = tid >> 5, ld = (tid & 31) * 4;  // tile loads: rows lr + 8 j, dims ld .. ld + 3
-  for (uint32_t t0 = 0; t0 <= last; t0 += T) {
+  for (uint32_t t0 = k_begin; t0 < k_end; t0 += T) {
     float4 kv4[T / 8], vv4[T / 8];
 #pragma unroll
     for (int j = 0; j < T / 8; j++) {
-      const size_t off = head + size_t(min(t0 + uint32_t(lr + 8 * j), last)) * D + ld;
+      const size_t off = head + size_t(min(t0 + uint32_t(lr + 8 * j), k_end - 1)) * D + ld;
       if constexpr (KV_BF16) {
         const uint2 kb = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.k_cache) + off);
         const uint2 vb = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + off);
@@ -258,11 +264,12 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
       float dot = 0.f;
 #pragma unroll 16
       for (int d = 0; d < D; d++) dot += qs[qv][d] * ks[key][d];
-      sc[j] = t0 + uint32_t(key) <= my_pos ? dot * p.scale : -INFINITY;
+      const uint32_t t = t0 + uint32_t(key);
+      sc[j] = t <= my_pos && t < k_end ? dot * p.scale : -INFINITY;
     }
     float tmax = fmaxf(sc[0], sc[1]);
     for (int o = 1; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o));
-    const float m_new = fmaxf(m_run, tmax);  // finite: key 0 of the first tile is always visible
+    const float m_new = fmaxf(m_run, tmax);  // -inf while no key of the run is visible to this vector
     const float corr = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
     const float e0 = sc[0] == -INFINITY ? 0.f : expf(sc[0] - m_new);
     const float e1 = sc[1] == -INFINITY ? 0.f : expf(sc[1] - m_new);
@@ -281,11 +288,49 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
       for (int i = 0; i < 8; i++) acc[i] += pe * vs[key][kk + 16 * i];
     }
   }
-  if (my_m < p.M) {
-    float* o = p.att + (size_t(my_m) * p.n_heads + g * G + qv % G) * D;
+  if (my_m >= p.M) return;
+  const size_t vec = size_t(my_m) * p.n_heads + g * G + qv % G;
+  if (runs == 1) {
+    float* o = p.att + vec * D;
 #pragma unroll
     for (int i = 0; i < 8; i++) o[kk + 16 * i] = acc[i] / l_run;
+  } else {
+    float* o = p.part + (vec * runs + run) * kPartStride;
+    if (kk == 0) { o[0] = m_run; o[1] = l_run; }
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[4 + kk + 16 * i] = acc[i];
   }
+}
+
+// att[v] = sum_s e_s acc_s / sum_s e_s l_s over the runs of query vector v = (token, head),
+// e_s = exp(m_s - max m); runs without a visible key (m = -inf) weigh 0. One workgroup of 128
+// threads (one per dim) per query vector; all of its run loads are issued at once.
+__global__ __launch_bounds__(kHeadDim) void k_attn_merge_rows(const float* __restrict__ part, uint32_t runs,
+                                                              float* __restrict__ att) {
+  constexpr int U = kBatchMaxRuns;
+  const size_t v = blockIdx.x;
+  const uint32_t d = threadIdx.x;
+  const float* base = part + v * runs * kPartStride;
+  float mv[U], lv[U], av[U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const float* q = base + size_t(min(uint32_t(u), runs - 1)) * kPartStride;
+    mv[u] = q[0];
+    lv[u] = q[1];
+    av[u] = q[4 + d];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float M = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < U; u++) M = uint32_t(u) < runs ? fmaxf(M, mv[u]) : M;
+  float L = 0.f, A = 0.f;
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const float e = (uint32_t(u) < runs && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
+    L += e * lv[u];
+    A += e * av[u];
+  }
+  att[v * kHeadDim + d] = A / L;
 }
 
 // x[m] = bf16 embedding row of ids[m] (cpu_inference.rs:109-111)
@@ -330,22 +375,38 @@ hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
-hipError_t launch_attn_causal(const BatchAttnParams& p, hipStream_t st) {
-  if (!p.n_kv || p.n_heads % p.n_kv) return hipErrorInvalidValue;
+hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st) {
+  if (!p.n_kv || p.n_heads % p.n_kv || runs == 0 || runs > uint32_t(kBatchMaxRuns) || (runs > 1 && !p.part))
+    return hipErrorInvalidValue;
   const uint32_t G = p.n_heads / p.n_kv;
-  const dim3 grid(p.n_kv, ceil_div(p.M, 16 / G));
+  BatchAttnParams q = p;
+  // runs of whole 32-position tiles covering positions 0 .. start + M - 1, none of them empty
+  const uint32_t tiles = ceil_div(p.start + p.M, 32), per_run = ceil_div(tiles, runs);
+  runs = ceil_div(tiles, per_run);
+  q.key_run = 32 * per_run;
+  const dim3 grid(p.n_kv, ceil_div(p.M, 16 / G), runs);
+  hipError_t e = hipErrorInvalidValue;
 #define QE_ATT(GG)                                                                                         \
   if (G == GG) {                                                                                           \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal<GG, true>), grid, dim3(256), 0, st, p);               \
-    else hipLaunchKernelGGL((k_attn_causal<GG, false>), grid, dim3(256), 0, st, p);                        \
-    return hipGetLastError();                                                                              \
+    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal<GG, true>), grid, dim3(256), 0, st, q);               \
+    else hipLaunchKernelGGL((k_attn_causal<GG, false>), grid, dim3(256), 0, st, q);                        \
+    e = hipGetLastError();                                                                                 \
   }
   QE_ATT(1)
   QE_ATT(2)
   QE_ATT(4)
   QE_ATT(8)
 #undef QE_ATT
-  return hipErrorInvalidValue;
+  if (e != hipSuccess || runs == 1) return e;
+  hipLaunchKernelGGL(k_attn_merge_rows, dim3(p.M * p.n_heads), dim3(kHeadDim), 0, st, p.part, runs, p.att);
+  return hipGetLastError();
+}
+
+uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv) {
+  if (!M || !n_kv || n_heads % n_kv || n_heads / n_kv > 16) return 1;
+  const uint32_t wgs = n_kv * ceil_div(M, 16 / (n_heads / n_kv));
+  uint32_t runs = std::min(ceil_div(1024, wgs), uint32_t(kBatchMaxRuns));
+  return std::max(1u, std::min(runs, ceil_div(start + M, 64)));
 }
 
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,

@@ -93,6 +93,7 @@ struct qe_model {
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
+  float* bpart = nullptr;  // causal attention partials
   float* blogits = nullptr;
   uint32_t* bids = nullptr;
 
@@ -419,6 +420,12 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   const size_t ox = take(cap * H * 4), os = take(cap * 4), oqkv = take(cap * (QD + 2 * KD) * 4),
                oq = take(cap * QD * 4), oatt = take(cap * QD * 4), oh = take(cap * I * 4),
                ologit = take(size_t(logit_rows) * c.vocab_size * 4), oids = take(cap * 4);
+  // attention partials: the most (tokens x key runs) any chunk of up to cap tokens asks for
+  size_t part_rows = 0;
+  for (uint32_t M = 1; M <= cap; M++)
+    part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
+                                                                     uint32_t(c.num_key_value_heads)));
+  const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
   HIP_TRY(hipStreamSynchronize(m->stream));
   if (m->batch_mem) HIP_TRY(hipFree(m->batch_mem));
   m->batch_mem = nullptr;
@@ -433,6 +440,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   m->bh = reinterpret_cast<float*>(m->batch_mem + oh);
   m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
   m->bids = reinterpret_cast<uint32_t*>(m->batch_mem + oids);
+  m->bpart = reinterpret_cast<float*>(m->batch_mem + opart);
   return QE_OK;
 }
 
@@ -469,7 +477,8 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.eps = eps; a.scale = 1.0f / sqrtf(float(D)); a.kv_bf16 = kv->dtype == QE_KV_BF16;
     HIP_TRY(qe::launch_qk_rope(a, s));
-    HIP_TRY(qe::launch_attn_causal(a, s));
+    a.part = m->bpart;
+    HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
     // o_proj + residual (cpu_inference.rs:163-164)
     if ((rc = gemm(m->batt, QD, nullptr, w.w_o, H, QD, m->bx, H, qe::kGemmResAdd))) return rc;
     // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)
