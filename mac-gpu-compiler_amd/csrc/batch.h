@@ -17,6 +17,8 @@ constexpr int kBatchMaxRuns = 32;
 // C[m][n] (=, +=) sum_k A'[m][k] W[n][k] for m < M, n < N; A' = A, or A x rowscale[m] x gain[k]
 // (an RMSNorm) when the launch asks for the norm. kGemmSiluPair: W rows 2i / 2i+1 are gate_i /
 // up_i and C[m][i] = silu(gate) * up. N even, K % 32 == 0, lda % 4 == 0.
+// Up to kGemmSkinnyMaxM rows run on the skinny kernel, which computes the norm's row scales
+// itself (rowscale unused, eps used); more rows need rowscale filled by launch_rownorm.
 struct GemmParams {
   const float* A;
   uint32_t lda;
@@ -26,7 +28,10 @@ struct GemmParams {
   uint32_t M, N, K;
   float* C;
   uint32_t ldc;
+  float eps;
 };
+
+constexpr uint32_t kGemmSkinnyMaxM = 32;
 
 struct BatchAttnParams {
   const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections

@@ -151,6 +151,126 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Skinny GEMM for M <= 16 MT rows (verify, the last chunk of a prefill): the weights are the
+// whole cost, so the work is spread over K as well as N. Workgroup = NW waves on 16 columns
+// n0 .. n0+15; wave w covers the k steps [w KPW, (w+1) KPW) with KPW = ceil(K / 32 / NW), two
+// per iteration (loads clamped to the last step, steps past the range masked by a zero W
+// fragment), MT m-tiles per W fragment, A split hi + lo as in k_gemm. The NW partial tiles are
+// summed in LDS in wave order. With the norm, each lane also sums x^2 of its row over the
+// steps it loads, so C = s[m] sum_k (x g)[m][k] W[n][k] with s[m] = 1 / sqrt(mean x^2 + eps)
+// (the scale applied after the sum, a reassociation of the reference's f32 product).
+// ---------------------------------------------------------------------------------------------
+template <bool NORM, int EPI, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmParams p) {
+  constexpr int KU = 2;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kg = lane >> 4;
+  const uint32_t n0 = blockIdx.x * 16;
+  const uint32_t KS = p.K / 32, KPW = (KS + NW - 1) / NW, s0 = uint32_t(wave) * KPW;
+  const uint16_t* Wr = p.W + size_t(min(n0 + uint32_t(li), p.N - 1)) * p.K;
+  const float* Ar[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) Ar[t] = p.A + size_t(min(uint32_t(16 * t + li), p.M - 1)) * p.lda;
+
+  f32x4 acc[MT];
+  float ss[MT];
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+    acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    ss[t] = 0.f;
+  }
+  float4 a0[KU][MT], a1[KU][MT];
+  uint4 g[KU], w[KU];
+  auto load = [&](uint32_t it) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const uint32_t k = 32 * min(s0 + it + uint32_t(u), KS - 1) + 8 * kg;
+      w[u] = *reinterpret_cast<const uint4*>(Wr + k);
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        a0[u][t] = *reinterpret_cast<const float4*>(Ar[t] + k);
+        a1[u][t] = *reinterpret_cast<const float4*>(Ar[t] + k + 4);
+      }
+      if constexpr (NORM) g[u] = *reinterpret_cast<const uint4*>(p.gain + k);
+    }
+  };
+  load(0);
+  for (uint32_t it = 0; it < KPW; it += KU) {
+    bf16x8 hi[KU][MT], lo[KU][MT];
+    uint4 wc[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const bool ok = it + u < KPW && s0 + it + u < KS;
+      wc[u] = make_uint4(ok ? w[u].x : 0u, ok ? w[u].y : 0u, ok ? w[u].z : 0u, ok ? w[u].w : 0u);
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        float v[8] = {a0[u][t].x, a0[u][t].y, a0[u][t].z, a0[u][t].w,
+                      a1[u][t].x, a1[u][t].y, a1[u][t].z, a1[u][t].w};
+        if constexpr (NORM) {
+          float q = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; e++) q += v[e] * v[e];
+          ss[t] += ok ? q : 0.f;
+          const uint32_t gg[4] = {g[u].x, g[u].y, g[u].z, g[u].w};
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            v[2 * e] *= __uint_as_float(gg[e] << 16);
+            v[2 * e + 1] *= __uint_as_float(gg[e] & 0xFFFF0000u);
+          }
+        }
+        split8(v, hi[u][t], lo[u][t]);
+      }
+    }
+    if (it + KU < KPW) load(it + KU);
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+      const bf16x8 b = __builtin_bit_cast(bf16x8, u32x4{wc[u].x, wc[u].y, wc[u].z, wc[u].w});
+#pragma unroll
+      for (int t = 0; t < MT; t++) {
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[u][t], b, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[u][t], b, acc[t], 0, 0, 0);
+      }
+    }
+  }
+
+  // partial tiles: lane holds rows 16 t + 4 kg + r, column li
+  __shared__ float part[NW][MT * 16][17];
+  __shared__ float ssp[NW][MT * 16];
+#pragma unroll
+  for (int t = 0; t < MT; t++) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) part[wave][16 * t + 4 * kg + r][li] = acc[t][r];
+    if constexpr (NORM) {
+      float q = ss[t];
+      q += __shfl_xor(q, 16);
+      q += __shfl_xor(q, 32);
+      if (kg == 0) ssp[wave][16 * t + li] = q;
+    }
+  }
+  __syncthreads();
+  if (tid >= MT * 256) return;  // whole waves
+  const uint32_t row = uint32_t(tid) >> 4, col = uint32_t(tid) & 15;
+  float c = 0.f;
+#pragma unroll
+  for (int v = 0; v < NW; v++) c += part[v][row][col];
+  if constexpr (NORM) {
+    float q = 0.f;
+#pragma unroll
+    for (int v = 0; v < NW; v++) q += ssp[v][row];
+    c *= 1.0f / sqrtf(q / float(p.K) + p.eps);
+  }
+  const uint32_t m = row, n = n0 + col;
+  if constexpr (EPI == kGemmSiluPair) {
+    const float up = __shfl_xor(c, 1);  // column n ^ 1 of the same row
+    if (m < p.M && n < p.N && (col & 1) == 0) p.C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
+  } else if constexpr (EPI == kGemmResAdd) {
+    if (m < p.M && n < p.N) p.C[size_t(m) * p.ldc + n] += c;
+  } else {
+    if (m < p.M && n < p.N) p.C[size_t(m) * p.ldc + n] = c;
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
 // Per token m and row r of [q heads, k heads, v heads]: q/k RMSNorm + RoPE with the table row of
 // position start + m; q goes to Q [M][n_heads][128], k and v to the cache slot (f32 or bf16).
 // One wave per (token, row); lane l holds dims l and l + 64.
@@ -352,7 +472,27 @@ hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, flo
 hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) {
   if (p.M == 0 || p.N == 0 || p.N % 2 || p.K % 32 || p.K == 0 || p.lda % 4 || !p.A || !p.W || !p.C)
     return hipErrorInvalidValue;
-  if (norm && (!p.rowscale || !p.gain)) return hipErrorInvalidValue;
+  if (norm && !p.gain) return hipErrorInvalidValue;
+  if (p.M <= kGemmSkinnyMaxM) {
+    // one m-tile: 16 waves per workgroup when there are few 16-column blocks, so the chip still
+    // fills; two m-tiles: 8 waves (their registers do not fit 16)
+    const uint32_t blocks = ceil_div(p.N, 16);
+    const bool wide = blocks < 256;
+#define QE_SKINNY_EPI(NRM, E)                                                                           \
+  do {                                                                                                  \
+    if (p.M > 16) hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 2, 8>), dim3(blocks), dim3(512), 0, st, p); \
+    else if (wide) hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 1, 16>), dim3(blocks), dim3(1024), 0, st, p); \
+    else hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 1, 8>), dim3(blocks), dim3(512), 0, st, p);          \
+  } while (0)
+    if (norm && epi == kGemmStore) QE_SKINNY_EPI(true, kGemmStore);
+    else if (norm && epi == kGemmSiluPair) QE_SKINNY_EPI(true, kGemmSiluPair);
+    else if (!norm && epi == kGemmStore) QE_SKINNY_EPI(false, kGemmStore);
+    else if (!norm && epi == kGemmResAdd) QE_SKINNY_EPI(false, kGemmResAdd);
+    else return hipErrorInvalidValue;
+#undef QE_SKINNY_EPI
+    return hipGetLastError();
+  }
+  if (norm && !p.rowscale) return hipErrorInvalidValue;
   const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64));
   // four 32-wide k steps per iteration when K allows, else one
 #define QE_GEMM(NRM, E)                                                                         \

@@ -457,8 +457,8 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
   const float eps = c.rms_norm_eps;
   auto gemm = [&](const float* A, uint32_t lda, const uint16_t* gain, const uint16_t* W, uint32_t N, uint32_t K,
                   float* C, uint32_t ldc, int epi) -> int {
-    if (gain) HIP_TRY(qe::launch_rownorm(A, M, K, eps, m->bs, s));
-    qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc};
+    if (gain && M > qe::kGemmSkinnyMaxM) HIP_TRY(qe::launch_rownorm(A, M, K, eps, m->bs, s));
+    qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc, eps};
     HIP_TRY(qe::launch_gemm(g, gain != nullptr, epi, s));
     return QE_OK;
   };
@@ -845,7 +845,7 @@ int qe_op_gemm_bf16(const float* a, const void* w, float* c, uint64_t m, uint64_
   if (reinterpret_cast<uintptr_t>(a) % 16 || reinterpret_cast<uintptr_t>(w) % 16)
     return fail(QE_ERR_ARG, "a and w must be 16-byte aligned");
   qe::GemmParams g{a, uint32_t(k), nullptr, nullptr, static_cast<const uint16_t*>(w), uint32_t(m), uint32_t(n),
-                   uint32_t(k), c, uint32_t(n)};
+                   uint32_t(k), c, uint32_t(n), 0.f};
   HIP_TRY(qe::launch_gemm(g, false, qe::kGemmStore, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }

@@ -24,8 +24,12 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
     return u.astype(np.uint16)
 
 
+# m <= 32 runs the skinny (split over k) kernel: one m-tile on 16 or 8 waves, or two m-tiles;
+# larger m the 64 x 64 tile kernel
 @pytest.mark.parametrize("m,n,k", [(1, 64, 32), (5, 128, 64), (64, 1024, 1024), (100, 4096, 1024),
-                                   (512, 1024, 3072), (37, 6144, 1024), (4, 32768, 1024), (3, 1000, 256)])
+                                   (512, 1024, 3072), (37, 6144, 1024), (4, 32768, 1024), (3, 1000, 256),
+                                   (16, 2048, 1024), (8, 4096, 3072), (17, 6144, 1024), (32, 1024, 3072),
+                                   (2, 4096, 160)])
 def test_gemm_matches_float64(gpu, m, n, k):
     import torch
     rng = np.random.default_rng(m * 7 + n + k)
@@ -124,3 +128,23 @@ def test_real_prefill_batch_then_decode_matches_fixture(gpu, real_ckpt):
     for i, lg in enumerate(np.concatenate([logits[None], step_logits])):
         assert np.max(np.abs(lg[idx] - g["sample_val"][i])) < MAX_ABS_DIFF, f"step {i}"
         assert np.max(np.abs(lg[g["top_idx"][i]] - g["top_val"][i])) < MAX_ABS_DIFF, f"step {i}"
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("k", [4, 20])
+def test_real_verify_matches_fixture(gpu, real_ckpt, k):
+    """verify of the greedy continuation: row i is the oracle's logits after token i + 1"""
+    import os
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qwen3_0_6b_decode.npz"),
+                allow_pickle=False)
+    m = qe.Model.load_model(real_ckpt)
+    prompt = qe.random_prompt(PROMPT_SEED, PROMPT_LEN, m.config().vocab_size)
+    cache = qe.KVCache(m, PROMPT_LEN + k)
+    m.prefill_batch(prompt, 0, cache, want_logits=False)
+    ref = [int(t) for t in g["tokens"]]
+    rows = m.verify(np.array(ref[:k], dtype=np.uint32), PROMPT_LEN, cache)
+    idx = g["sample_idx"]
+    for i in range(k):
+        assert oracle.argmax(rows[i]) == ref[i + 1], f"row {i}"
+        assert np.max(np.abs(rows[i][idx] - g["sample_val"][i + 1])) < MAX_ABS_DIFF, f"row {i}"
+        assert np.max(np.abs(rows[i][g["top_idx"][i + 1]] - g["top_val"][i + 1])) < MAX_ABS_DIFF, f"row {i}"
