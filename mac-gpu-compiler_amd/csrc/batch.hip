@@ -8,11 +8,12 @@
 //                  split into hi + lo bf16 so the products keep ~16 mantissa bits; epilogues
 //                  store / residual add / silu(gate)*up                 (cpu_inference.rs:225-257)
 //   k_qk_rope      per token and head: q/k RMSNorm + RoPE, K/V append   (cpu_inference.rs:134-141)
-//   k_attn_causal  token m attends positions 0..start+m               (cpu_inference.rs:144-162)
+//   k_attn_causal  token m attends positions 0..start+m on f32 MFMA     (cpu_inference.rs:144-162)
 #include "batch.h"
 
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "device_common.h"
 
@@ -312,113 +313,157 @@ __global__ __launch_bounds__(256) void k_qk_rope(BatchAttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal attention of a chunk: workgroup (KV head g, block of QB = 16 / G tokens, key run s)
-// serves its 16 query vectors (token mb + v / G, head g G + v % G) over the positions of run s,
-// [s key_run, (s+1) key_run) cut at start + the block's last token, in LDS tiles of T = 32
-// positions, with an online softmax per query vector. Thread (v = tid / 16, kk = tid % 16):
-// scores for keys kk and kk + 16 of the tile (K rows padded to 129 floats, so the 16 keys sit in
-// 16 banks), then dims kk + 16 i (i < 8) of the output. With one run the output is normalized
-// into att [M][n_heads][128]; with several, each writes its (m, l, acc) partial to
-// part [M][n_heads][runs][kPartStride] (a query vector with no visible key in the run writes
-// m = -inf, l = 0) and k_attn_merge_rows combines them.
+// Causal attention of a chunk on the f32 matrix cores (v_mfma_f32_16x16x4_f32, f32 products as
+// in the reference). Workgroup (KV head g, block of TOK = 64 / G tokens, key run s) serves 64
+// query rows, row r = token mb + r / G of head g G + r % G; wave w owns rows 16 w .. 16 w + 15
+// and lane l the row 16 w + l % 16. Keys come in LDS tiles of 64 positions (the next tile is
+// loaded into registers while this one is used). Per tile a wave computes the transposed
+// scores S^T[key][row] = sum_d K[key][d] Q[row][d] (the lane with kg = l / 16 takes dims
+// 32 kg .. 32 kg + 31 of its row, held in registers) and then O^T[d][row] += sum_key
+// V[key][d] P^T[key][row]. In the 16 x 16 output layout a lane holds keys 16 j + 4 kg + r
+// (j, r < 4) of its own row, which is exactly the operand layout P^T needs, and O^T's column is
+// again its row: the online softmax (max, rescale, sum) stays in the lane plus two shuffles
+// across kg, with no LDS round trip for P. Rows with no visible key in the run keep m = -inf,
+// l = 0. One run: normalized output to att [M][n_heads][128]; several: (m, l, acc) partials to
+// part [M][n_heads][runs][kPartStride], combined by k_attn_merge_rows.
 // ---------------------------------------------------------------------------------------------
 template <int G, bool KV_BF16>
 __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
-  constexpr int D = kHeadDim, T = 32, NQ = 16, QB = NQ / G, KP = D + 1;
-  const uint32_t g = blockIdx.x, mb = blockIdx.y * QB, run = blockIdx.z, runs = gridDim.z;
-  const int tid = threadIdx.x, qv = tid >> 4, kk = tid & 15;
-  __shared__ __align__(16) float qs[NQ][D];
-  __shared__ float ks[T][KP];
-  __shared__ __align__(16) float vs[T][D];
-  __shared__ float ps[NQ][T];
-  {
-    const int d4 = (tid & 31) * 4;  // 8 rows of 128 per pass, float4 each
-#pragma unroll
-    for (int pass = 0; pass < NQ / 8; pass++) {
-      const int v = pass * 8 + (tid >> 5);
-      const uint32_t m = min(mb + uint32_t(v / G), p.M - 1);
-      const float4 q4 = *reinterpret_cast<const float4*>(p.q + (size_t(m) * p.n_heads + g * G + v % G) * D + d4);
-      qs[v][d4] = q4.x; qs[v][d4 + 1] = q4.y; qs[v][d4 + 2] = q4.z; qs[v][d4 + 3] = q4.w;
-    }
-  }
-  const uint32_t my_m = mb + uint32_t(qv / G);
-  const uint32_t my_pos = p.start + min(my_m, p.M - 1);
-  const uint32_t last = p.start + min(mb + QB - 1, p.M - 1);  // positions 0..last are needed
+  constexpr int D = kHeadDim, BK = 64, TOK = 64 / G, KS = D + 4;  // row pad: 16 keys x 4 dims hit 64 banks
+  __shared__ __align__(16) float ks[BK][KS];
+  __shared__ __align__(16) float vs[BK][KS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const uint32_t g = blockIdx.x, mb = blockIdx.y * TOK, run = blockIdx.z, runs = gridDim.z;
+  const uint32_t row = uint32_t(wave) * 16 + uint32_t(li);
+  const uint32_t tok = mb + row / G, head = g * G + row % G;
+  const uint32_t tok_c = min(tok, p.M - 1);
+  const uint32_t my_pos = p.start + tok_c;
+  const uint32_t last = p.start + min(mb + TOK - 1, p.M - 1);  // positions 0..last are needed
   const uint32_t k_begin = run * p.key_run;
   const uint32_t k_end = min(last + 1, k_begin + p.key_run);  // this run: positions [k_begin, k_end)
-  float m_run = -INFINITY, l_run = 0.f;
-  float acc[8];
+
+  float q[32];
+  {
+    const float4* qp = reinterpret_cast<const float4*>(p.q + (size_t(tok_c) * p.n_heads + head) * D + 32 * kg);
 #pragma unroll
-  for (int i = 0; i < 8; i++) acc[i] = 0.f;
-  const size_t head = size_t(g) * p.max_seq * D;
-  const int lr = tid >> 5, ld = (tid & 31) * 4;  // tile loads: rows lr + 8 j, dims ld .. ld + 3
-  for (uint32_t t0 = k_begin; t0 < k_end; t0 += T) {
-    float4 kv4[T / 8], vv4[T / 8];
-#pragma unroll
-    for (int j = 0; j < T / 8; j++) {
-      const size_t off = head + size_t(min(t0 + uint32_t(lr + 8 * j), k_end - 1)) * D + ld;
-      if constexpr (KV_BF16) {
-        const uint2 kb = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.k_cache) + off);
-        const uint2 vb = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + off);
-        kv4[j] = make_float4(__uint_as_float(kb.x << 16), __uint_as_float(kb.x & 0xFFFF0000u),
-                             __uint_as_float(kb.y << 16), __uint_as_float(kb.y & 0xFFFF0000u));
-        vv4[j] = make_float4(__uint_as_float(vb.x << 16), __uint_as_float(vb.x & 0xFFFF0000u),
-                             __uint_as_float(vb.y << 16), __uint_as_float(vb.y & 0xFFFF0000u));
-      } else {
-        kv4[j] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k_cache) + off);
-        vv4[j] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v_cache) + off);
-      }
-    }
-    __syncthreads();  // the previous tile's LDS reads are done
-#pragma unroll
-    for (int j = 0; j < T / 8; j++) {
-      const int r = lr + 8 * j;
-      ks[r][ld] = kv4[j].x; ks[r][ld + 1] = kv4[j].y; ks[r][ld + 2] = kv4[j].z; ks[r][ld + 3] = kv4[j].w;
-      vs[r][ld] = vv4[j].x; vs[r][ld + 1] = vv4[j].y; vs[r][ld + 2] = vv4[j].z; vs[r][ld + 3] = vv4[j].w;
-    }
-    __syncthreads();
-    float sc[2];
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int key = kk + 16 * j;
-      float dot = 0.f;
-#pragma unroll 16
-      for (int d = 0; d < D; d++) dot += qs[qv][d] * ks[key][d];
-      const uint32_t t = t0 + uint32_t(key);
-      sc[j] = t <= my_pos && t < k_end ? dot * p.scale : -INFINITY;
-    }
-    float tmax = fmaxf(sc[0], sc[1]);
-    for (int o = 1; o < 16; o <<= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, o));
-    const float m_new = fmaxf(m_run, tmax);  // -inf while no key of the run is visible to this vector
-    const float corr = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-    const float e0 = sc[0] == -INFINITY ? 0.f : expf(sc[0] - m_new);
-    const float e1 = sc[1] == -INFINITY ? 0.f : expf(sc[1] - m_new);
-    ps[qv][kk] = e0;
-    ps[qv][kk + 16] = e1;
-    float tsum = e0 + e1;
-    for (int o = 1; o < 16; o <<= 1) tsum += __shfl_xor(tsum, o);
-    l_run = l_run * corr + tsum;
-    m_run = m_new;
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < 8; i++) acc[i] *= corr;
-    for (int key = 0; key < T; key++) {
-      const float pe = ps[qv][key];
-#pragma unroll
-      for (int i = 0; i < 8; i++) acc[i] += pe * vs[key][kk + 16 * i];
+    for (int i = 0; i < 8; i++) {
+      const float4 v = qp[i];
+      q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
     }
   }
-  if (my_m >= p.M) return;
-  const size_t vec = size_t(my_m) * p.n_heads + g * G + qv % G;
+  f32x4 o[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // tile staging: thread t moves rows t / 32 + 8 i (i < 8), dims 4 (t % 32) .. +3
+  const size_t hbase = size_t(g) * p.max_seq * D;
+  const int lr = tid >> 5, ld = (tid & 31) * 4;
+  using Pre = typename std::conditional<KV_BF16, uint2, float4>::type;
+  Pre kp[8], vp[8];
+  auto load_tile = [&](uint32_t t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const size_t off = hbase + size_t(min(t0 + uint32_t(lr + 8 * i), k_end - 1)) * D + ld;
+      if constexpr (KV_BF16) {
+        kp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.k_cache) + off);
+        vp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + off);
+      } else {
+        kp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k_cache) + off);
+        vp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v_cache) + off);
+      }
+    }
+  };
+  auto to_f4 = [](const Pre& v) __attribute__((always_inline)) {
+    if constexpr (KV_BF16)
+      return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
+                         __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
+    else
+      return v;
+  };
+  if (k_begin < k_end) load_tile(k_begin);
+  for (uint32_t t0 = k_begin; t0 < k_end; t0 += BK) {
+    __syncthreads();  // the previous tile's LDS reads are done
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      *reinterpret_cast<float4*>(&ks[lr + 8 * i][ld]) = to_f4(kp[i]);
+      *reinterpret_cast<float4*>(&vs[lr + 8 * i][ld]) = to_f4(vp[i]);
+    }
+    __syncthreads();
+    if (t0 + BK < k_end) load_tile(t0 + BK);
+
+    // S^T for 4 blocks of 16 keys
+    f32x4 s[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int t = 0; t < 8; t++) {
+        const float4 kv = *reinterpret_cast<const float4*>(&ks[16 * j + li][32 * kg + 4 * t]);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, q[4 * t], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, q[4 * t + 1], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, q[4 * t + 2], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, q[4 * t + 3], s[j], 0, 0, 0);
+      }
+    }
+    // online softmax over the lane's 16 keys and the three other kg lanes of its row
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t t = t0 + uint32_t(16 * j + 4 * kg + r);
+        const float v = t <= my_pos && t < k_end ? s[j][r] * p.scale : -INFINITY;
+        s[j][r] = v;
+        mx = fmaxf(mx, v);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 16));
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_run, mx);  // -inf while no key of the run is visible to this row
+    const float corr = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float e = s[j][r] == -INFINITY ? 0.f : expf(s[j][r] - m_new);
+        s[j][r] = e;
+        sum += e;
+      }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    l_run = l_run * corr + sum;
+    m_run = m_new;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] *= corr;
+    // O^T += V^T P^T, k index = key 16 j + 4 kg + r
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float* vr = &vs[16 * j + 4 * kg + r][li];
+#pragma unroll
+        for (int i = 0; i < 8; i++) o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * i], s[j][r], o[i], 0, 0, 0);
+      }
+    }
+  }
+  if (tok >= p.M) return;
+  // lane holds O^T[16 i + 4 kg + r][row], r < 4
+  const size_t vec = size_t(tok) * p.n_heads + head;
   if (runs == 1) {
-    float* o = p.att + vec * D;
+    const float inv = 1.0f / l_run;
+    float* out = p.att + vec * D + 4 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; i++) o[kk + 16 * i] = acc[i] / l_run;
+    for (int i = 0; i < 8; i++)
+      *reinterpret_cast<float4*>(out + 16 * i) = make_float4(o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv);
   } else {
-    float* o = p.part + (vec * runs + run) * kPartStride;
-    if (kk == 0) { o[0] = m_run; o[1] = l_run; }
+    float* out = p.part + (vec * runs + run) * kPartStride;
+    if (kg == 0) { out[0] = m_run; out[1] = l_run; }
 #pragma unroll
-    for (int i = 0; i < 8; i++) o[4 + kk + 16 * i] = acc[i];
+    for (int i = 0; i < 8; i++)
+      *reinterpret_cast<float4*>(out + 4 + 16 * i + 4 * kg) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
   }
 }
 
@@ -520,11 +565,11 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
     return hipErrorInvalidValue;
   const uint32_t G = p.n_heads / p.n_kv;
   BatchAttnParams q = p;
-  // runs of whole 32-position tiles covering positions 0 .. start + M - 1, none of them empty
-  const uint32_t tiles = ceil_div(p.start + p.M, 32), per_run = ceil_div(tiles, runs);
+  // runs of whole 64-position tiles covering positions 0 .. start + M - 1, none of them empty
+  const uint32_t tiles = ceil_div(p.start + p.M, 64), per_run = ceil_div(tiles, runs);
   runs = ceil_div(tiles, per_run);
-  q.key_run = 32 * per_run;
-  const dim3 grid(p.n_kv, ceil_div(p.M, 16 / G), runs);
+  q.key_run = 64 * per_run;
+  const dim3 grid(p.n_kv, ceil_div(p.M, 64 / G), runs);
   hipError_t e = hipErrorInvalidValue;
 #define QE_ATT(GG)                                                                                         \
   if (G == GG) {                                                                                           \
@@ -544,9 +589,9 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
 
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv) {
   if (!M || !n_kv || n_heads % n_kv || n_heads / n_kv > 16) return 1;
-  const uint32_t wgs = n_kv * ceil_div(M, 16 / (n_heads / n_kv));
+  const uint32_t wgs = n_kv * ceil_div(M, 64 / (n_heads / n_kv));
   uint32_t runs = std::min(ceil_div(1024, wgs), uint32_t(kBatchMaxRuns));
-  return std::max(1u, std::min(runs, ceil_div(start + M, 64)));
+  return std::max(1u, std::min(runs, ceil_div(start + M, 128)));
 }
 
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
