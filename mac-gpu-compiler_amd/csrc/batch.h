@@ -9,7 +9,8 @@
 
 namespace qe {
 
-enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2 };
+// kGemmPartial: split over K; split z writes its partial sums to C + z M ldc (launch_gemm_split)
+enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2, kGemmPartial = 3 };
 
 // most key runs the causal attention of a chunk is split into (partials merged after)
 constexpr int kBatchMaxRuns = 32;
@@ -51,6 +52,15 @@ struct BatchAttnParams {
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
 hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
+// K splits for a split GEMM of M > kGemmSkinnyMaxM rows: enough workgroups to fill the chip,
+// each split a multiple of 64 deep (1 when K does not split)
+uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K);
+// partial sums of `splits` K ranges (no norm): C[z][m][n], z < splits, ldc = N
+hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t st);
+// x[m][n] += sum_z part[z][m][n] (z in order), then s[m] = 1 / sqrt(mean_n x[m][n]^2 + eps):
+// the residual add of a split GEMM fused with the next RMSNorm's row scale. N % 4 == 0.
+hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, uint32_t M, uint32_t N, float eps,
+                                  float* s, hipStream_t st);
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
 // causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);

@@ -152,6 +152,138 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
+// Tiled GEMM, K % 64 == 0: workgroup tile 64 (m) x 64 (n), 4 waves; wave w owns rows
+// [16 w, 16 w + 16) and all four 16-column blocks. The W tile of each 64-deep stage is loaded
+// once per workgroup into LDS (double buffered, rows padded to 72 bf16 so that the 16 rows a
+// fragment read touches land in distinct banks) and shared by the four waves; each wave's A
+// rows go straight to registers, split hi + lo. The next stage's A and W loads are issued
+// before this stage's MFMAs. gridDim.z > 1 splits K: split z covers K / gridDim.z and writes
+// its partial sums (kGemmPartial) to C + z M ldc.
+// ---------------------------------------------------------------------------------------------
+template <bool NORM, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_lds(GemmParams p) {
+  constexpr int BK = 64, WP = BK + 8;
+  __shared__ __align__(16) uint16_t ws[2][64][WP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int li = lane & 15, kg = lane >> 4;
+  const uint32_t m0 = blockIdx.y * 64 + wave * 16, n0 = blockIdx.x * 64;
+  const uint32_t kz = p.K / gridDim.z, kbeg = blockIdx.z * kz, nst = kz / BK;
+  const uint32_t arow = min(m0 + uint32_t(li), p.M - 1);
+  const float* Ar = p.A + size_t(arow) * p.lda + kbeg;
+  const float rs = NORM ? p.rowscale[arow] : 1.0f;
+  const uint16_t* gp = NORM ? p.gain + kbeg : nullptr;
+  // W stage: 64 rows x 8 chunks of 16 B; thread t moves chunks t and t + 256
+  const uint16_t* Wsrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int c = tid + 256 * i;
+    Wsrc[i] = p.W + size_t(min(n0 + uint32_t(c >> 3), p.N - 1)) * p.K + kbeg + 8 * (c & 7);
+  }
+  u32x4 wn[2];
+  uint4 gn[2];
+  float4 an[2][2];
+  auto load = [&](uint32_t stg) __attribute__((always_inline)) {
+    const uint32_t k = stg * BK;
+#pragma unroll
+    for (int i = 0; i < 2; i++) wn[i] = *reinterpret_cast<const u32x4*>(Wsrc[i] + k);
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      an[u][0] = *reinterpret_cast<const float4*>(Ar + k + 32 * u + 8 * kg);
+      an[u][1] = *reinterpret_cast<const float4*>(Ar + k + 32 * u + 8 * kg + 4);
+      if constexpr (NORM) gn[u] = *reinterpret_cast<const uint4*>(gp + k + 32 * u + 8 * kg);
+    }
+  };
+  auto store_w = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(&ws[buf][c >> 3][8 * (c & 7)]) = wn[i];
+    }
+  };
+  f32x4 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  load(0);
+  store_w(0);
+  __syncthreads();
+  for (uint32_t stg = 0; stg < nst; stg++) {
+    bf16x8 hi[2], lo[2];
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      float v[8] = {an[u][0].x, an[u][0].y, an[u][0].z, an[u][0].w, an[u][1].x, an[u][1].y, an[u][1].z, an[u][1].w};
+      if constexpr (NORM) {
+        const uint32_t gg[4] = {gn[u].x, gn[u].y, gn[u].z, gn[u].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          v[2 * e] = (v[2 * e] * rs) * __uint_as_float(gg[e] << 16);
+          v[2 * e + 1] = (v[2 * e + 1] * rs) * __uint_as_float(gg[e] & 0xFFFF0000u);
+        }
+      }
+      split8(v, hi[u], lo[u]);
+    }
+    load(min(stg + 1, nst - 1));  // unconditional: the last stage reloads itself
+    const int buf = int(stg & 1);
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&ws[buf][16 * j + li][32 * u + 8 * kg]);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[u], b, acc[j], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[u], b, acc[j], 0, 0, 0);
+      }
+    }
+    store_w(buf ^ 1);  // that buffer's last reads were the previous stage's, before its barrier
+    __syncthreads();
+  }
+
+  // epilogue: lane holds C[m0 + 4 kg + r][n0 + 16 j + li]
+  float* C = p.C + (EPI == kGemmPartial ? size_t(blockIdx.z) * p.M * p.ldc : 0);
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const uint32_t n = n0 + 16 * j + li;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t m = m0 + 4 * kg + r;
+      const float c = acc[j][r];
+      if constexpr (EPI == kGemmSiluPair) {
+        const float up = __shfl_xor(c, 1);  // columns 2i (gate) and 2i+1 (up) in neighbouring lanes
+        if (m < p.M && n < p.N && (li & 1) == 0) C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
+      } else if constexpr (EPI == kGemmResAdd) {
+        if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] += c;
+      } else {
+        if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] = c;
+      }
+    }
+  }
+}
+
+// x[m] += sum_z part[z][m] (in z order), then s[m] = 1 / sqrt(mean x[m]^2 + eps); one workgroup
+// per row, float4 per thread per pass
+__global__ __launch_bounds__(256) void k_resadd_partials(float* __restrict__ x, const float* __restrict__ part,
+                                                         uint32_t splits, uint32_t M, uint32_t N, float eps,
+                                                         float* __restrict__ s) {
+  __shared__ float red[4];
+  const uint32_t m = blockIdx.x, tid = threadIdx.x;
+  float ss = 0.f;
+  for (uint32_t c = tid; c < N / 4; c += 256) {
+    float4 acc = reinterpret_cast<const float4*>(part + size_t(m) * N)[c];
+    for (uint32_t z = 1; z < splits; z++) {
+      const float4 v = reinterpret_cast<const float4*>(part + (size_t(z) * M + m) * N)[c];
+      acc.x += v.x; acc.y += v.y; acc.z += v.z; acc.w += v.w;
+    }
+    float4* xr = reinterpret_cast<float4*>(x + size_t(m) * N) + c;
+    float4 xv = *xr;
+    xv.x += acc.x; xv.y += acc.y; xv.z += acc.z; xv.w += acc.w;
+    *xr = xv;
+    ss += (xv.x * xv.x + xv.y * xv.y) + (xv.z * xv.z + xv.w * xv.w);
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  if (tid == 0) s[m] = 1.0f / sqrtf(((red[0] + red[1]) + (red[2] + red[3])) / float(N) + eps);
+}
+
+// ---------------------------------------------------------------------------------------------
 // Skinny GEMM for M <= 16 MT rows (verify, the last chunk of a prefill): the weights are the
 // whole cost, so the work is spread over K as well as N. Workgroup = NW waves on 16 columns
 // n0 .. n0+15; wave w covers the k steps [w KPW, (w+1) KPW) with KPW = ceil(K / 32 / NW), two
@@ -468,13 +600,13 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
 }
 
 // att[v] = sum_s e_s acc_s / sum_s e_s l_s over the runs of query vector v = (token, head),
-// e_s = exp(m_s - max m); runs without a visible key (m = -inf) weigh 0. One workgroup of 128
-// threads (one per dim) per query vector; all of its run loads are issued at once.
-__global__ __launch_bounds__(kHeadDim) void k_attn_merge_rows(const float* __restrict__ part, uint32_t runs,
-                                                              float* __restrict__ att) {
-  constexpr int U = kBatchMaxRuns;
-  const size_t v = blockIdx.x;
-  const uint32_t d = threadIdx.x;
+// e_s = exp(m_s - max m); runs without a visible key (m = -inf) weigh 0. Two query vectors per
+// workgroup of 256 threads (one per dim); all U >= runs run loads are issued at once.
+template <int U>
+__global__ __launch_bounds__(256) void k_attn_merge_rows(const float* __restrict__ part, uint32_t runs,
+                                                         uint32_t n_vec, float* __restrict__ att) {
+  const size_t v = min(blockIdx.x * 2 + (threadIdx.x >> 7), n_vec - 1);  // odd count: the last one twice
+  const uint32_t d = threadIdx.x & (kHeadDim - 1);
   const float* base = part + v * runs * kPartStride;
   float mv[U], lv[U], av[U];
 #pragma unroll
@@ -539,6 +671,14 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
   }
   if (norm && !p.rowscale) return hipErrorInvalidValue;
   const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64));
+  if (p.K % 64 == 0) {
+    if (norm && epi == kGemmStore) hipLaunchKernelGGL((k_gemm_lds<true, kGemmStore>), grid, dim3(256), 0, st, p);
+    else if (norm && epi == kGemmSiluPair) hipLaunchKernelGGL((k_gemm_lds<true, kGemmSiluPair>), grid, dim3(256), 0, st, p);
+    else if (!norm && epi == kGemmStore) hipLaunchKernelGGL((k_gemm_lds<false, kGemmStore>), grid, dim3(256), 0, st, p);
+    else if (!norm && epi == kGemmResAdd) hipLaunchKernelGGL((k_gemm_lds<false, kGemmResAdd>), grid, dim3(256), 0, st, p);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   // four 32-wide k steps per iteration when K allows, else one
 #define QE_GEMM(NRM, E)                                                                         \
   do {                                                                                          \
@@ -551,6 +691,28 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
   else if (!norm && epi == kGemmResAdd) QE_GEMM(false, kGemmResAdd);
   else return hipErrorInvalidValue;
 #undef QE_GEMM
+  return hipGetLastError();
+}
+
+uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K) {
+  const uint32_t tiles = ceil_div(N, 64) * ceil_div(M, 64);
+  uint32_t z = 1;
+  while (z < 8 && tiles * z < 256 && K % (128 * z) == 0) z *= 2;
+  return z;
+}
+
+hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t st) {
+  if (p.M == 0 || p.N == 0 || p.N % 2 || p.lda % 4 || !p.A || !p.W || !p.C || splits == 0 || p.K % (64 * splits))
+    return hipErrorInvalidValue;
+  const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), splits);
+  hipLaunchKernelGGL((k_gemm_lds<false, kGemmPartial>), grid, dim3(256), 0, st, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, uint32_t M, uint32_t N, float eps,
+                                  float* s, hipStream_t st) {
+  if (!M || N % 4 || !splits) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_resadd_partials, dim3(M), dim3(256), 0, st, x, part, splits, M, N, eps, s);
   return hipGetLastError();
 }
 
@@ -583,7 +745,12 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
   QE_ATT(8)
 #undef QE_ATT
   if (e != hipSuccess || runs == 1) return e;
-  hipLaunchKernelGGL(k_attn_merge_rows, dim3(p.M * p.n_heads), dim3(kHeadDim), 0, st, p.part, runs, p.att);
+  const uint32_t n_vec = p.M * p.n_heads;
+  const dim3 mg(ceil_div(n_vec, 2));
+  if (runs <= 4) hipLaunchKernelGGL((k_attn_merge_rows<4>), mg, dim3(256), 0, st, p.part, runs, n_vec, p.att);
+  else if (runs <= 8) hipLaunchKernelGGL((k_attn_merge_rows<8>), mg, dim3(256), 0, st, p.part, runs, n_vec, p.att);
+  else if (runs <= 16) hipLaunchKernelGGL((k_attn_merge_rows<16>), mg, dim3(256), 0, st, p.part, runs, n_vec, p.att);
+  else hipLaunchKernelGGL((k_attn_merge_rows<32>), mg, dim3(256), 0, st, p.part, runs, n_vec, p.att);
   return hipGetLastError();
 }
 

@@ -93,7 +93,8 @@ struct qe_model {
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
-  float* bpart = nullptr;  // causal attention partials
+  float* bpart = nullptr;   // causal attention partials
+  float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
   float* blogits = nullptr;
   uint32_t* bids = nullptr;
 
@@ -426,6 +427,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
     part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
                                                                      uint32_t(c.num_key_value_heads)));
   const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
+  const size_t osplit = take(size_t(8) * cap * H * 4);  // gemm_splits returns at most 8
   HIP_TRY(hipStreamSynchronize(m->stream));
   if (m->batch_mem) HIP_TRY(hipFree(m->batch_mem));
   m->batch_mem = nullptr;
@@ -441,6 +443,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
   m->bids = reinterpret_cast<uint32_t*>(m->batch_mem + oids);
   m->bpart = reinterpret_cast<float*>(m->batch_mem + opart);
+  m->bsplit = reinterpret_cast<float*>(m->batch_mem + osplit);
   return QE_OK;
 }
 
@@ -455,15 +458,34 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
   hipStream_t s = m->stream;
   const float eps = c.rms_norm_eps;
+  // Up to kGemmSkinnyMaxM rows the skinny GEMM computes each norm's row scales itself and adds
+  // residuals in its epilogue. Past that, m->bs holds the row scales of the current norm input:
+  // from a rownorm launch for layer 0, then from the reduction that finishes each split o_proj /
+  // down (residual add + the next norm's scales in one pass).
+  const bool skinny = M <= qe::kGemmSkinnyMaxM;
   auto gemm = [&](const float* A, uint32_t lda, const uint16_t* gain, const uint16_t* W, uint32_t N, uint32_t K,
                   float* C, uint32_t ldc, int epi) -> int {
-    if (gain && M > qe::kGemmSkinnyMaxM) HIP_TRY(qe::launch_rownorm(A, M, K, eps, m->bs, s));
     qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc, eps};
     HIP_TRY(qe::launch_gemm(g, gain != nullptr, epi, s));
     return QE_OK;
   };
+  // x += A W^T, then m->bs = the row scales of the updated x
+  auto gemm_resadd = [&](const float* A, uint32_t lda, const uint16_t* W, uint32_t K) -> int {
+    if (skinny) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
+    if (K % 64) {  // no split: residual epilogue, then the row scales
+      if (int rc2 = gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd)) return rc2;
+      HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
+      return QE_OK;
+    }
+    const uint32_t z = qe::gemm_splits(M, H, K);
+    qe::GemmParams g{A, lda, nullptr, nullptr, W, M, H, K, m->bsplit, H, eps};
+    HIP_TRY(qe::launch_gemm_split(g, z, s));
+    HIP_TRY(qe::launch_resadd_partials(m->bx, m->bsplit, z, M, H, eps, m->bs, s));
+    return QE_OK;
+  };
   int rc;
   HIP_TRY(qe::launch_embed_rows(m->embed, m->bids, M, H, m->bx, s));
+  if (!skinny) HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     // input_layernorm + q|k|v (cpu_inference.rs:129-132)
@@ -480,10 +502,10 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
     a.part = m->bpart;
     HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
     // o_proj + residual (cpu_inference.rs:163-164)
-    if ((rc = gemm(m->batt, QD, nullptr, w.w_o, H, QD, m->bx, H, qe::kGemmResAdd))) return rc;
+    if ((rc = gemm_resadd(m->batt, QD, w.w_o, QD))) return rc;
     // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)
     if ((rc = gemm(m->bx, H, w.w_post, w.w_gu, 2 * I, H, m->bh, I, qe::kGemmSiluPair))) return rc;
-    if ((rc = gemm(m->bh, I, nullptr, w.w_down, H, I, m->bx, H, qe::kGemmResAdd))) return rc;
+    if ((rc = gemm_resadd(m->bh, I, w.w_down, I))) return rc;
   }
   // final norm + lm_head (cpu_inference.rs:175-178)
   if (all_logits) {

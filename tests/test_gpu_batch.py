@@ -25,11 +25,11 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
 
 
 # m <= 32 runs the skinny (split over k) kernel: one m-tile on 16 or 8 waves, or two m-tiles;
-# larger m the 64 x 64 tile kernel
+# larger m the LDS-tiled 64 x 64 kernel (k % 64 == 0) or the register-only one (k = 96)
 @pytest.mark.parametrize("m,n,k", [(1, 64, 32), (5, 128, 64), (64, 1024, 1024), (100, 4096, 1024),
                                    (512, 1024, 3072), (37, 6144, 1024), (4, 32768, 1024), (3, 1000, 256),
                                    (16, 2048, 1024), (8, 4096, 3072), (17, 6144, 1024), (32, 1024, 3072),
-                                   (2, 4096, 160)])
+                                   (2, 4096, 160), (40, 512, 96)])
 def test_gemm_matches_float64(gpu, m, n, k):
     import torch
     rng = np.random.default_rng(m * 7 + n + k)
