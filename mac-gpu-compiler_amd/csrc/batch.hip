@@ -24,18 +24,18 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// f32 -> bf16 bits, round to nearest even (NaN kept quiet)
-__device__ __forceinline__ uint32_t bf16_bits(float f) { return f32_to_bf16(f); }
-
-// 8 floats -> (hi, lo) bf16x8 with hi = bf16(v), lo = bf16(v - hi)
+// 8 floats -> (hi, lo) bf16x8 with hi = bf16(v), lo = bf16(v - hi), both rounded to nearest
+// even by the hardware pair conversion (v_cvt_pk_bf16_f32); hi + lo keeps ~16 mantissa bits
 __device__ __forceinline__ void split8(const float (&v)[8], bf16x8& hi, bf16x8& lo) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
   u32x4 h, l;
 #pragma unroll
   for (int e = 0; e < 4; e++) {
-    const uint32_t h0 = bf16_bits(v[2 * e]), h1 = bf16_bits(v[2 * e + 1]);
-    const float r0 = v[2 * e] - __uint_as_float(h0 << 16), r1 = v[2 * e + 1] - __uint_as_float(h1 << 16);
-    h[e] = h0 | (h1 << 16);
-    l[e] = bf16_bits(r0) | (bf16_bits(r1) << 16);
+    const uint32_t hb = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{v[2 * e], v[2 * e + 1]}), bf16x2));
+    const float r0 = v[2 * e] - __uint_as_float(hb << 16), r1 = v[2 * e + 1] - __uint_as_float(hb & 0xFFFF0000u);
+    h[e] = hb;
+    l[e] = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{r0, r1}), bf16x2));
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);
@@ -154,24 +154,24 @@ __global__ __launch_bounds__(256) void k_gemm(GemmParams p) {
 // ---------------------------------------------------------------------------------------------
 // Tiled GEMM, K % 64 == 0: workgroup tile 64 (m) x 64 (n), 4 waves; wave w owns rows
 // [16 w, 16 w + 16) and all four 16-column blocks. The W tile of each 64-deep stage is loaded
-// once per workgroup into LDS (double buffered, rows padded to 72 bf16 so that the 16 rows a
+// once per workgroup into LDS (three buffers, rows padded to 72 bf16 so that the 16 rows a
 // fragment read touches land in distinct banks) and shared by the four waves; each wave's A
-// rows go straight to registers, split hi + lo. The next stage's A and W loads are issued
-// before this stage's MFMAs. gridDim.z > 1 splits K: split z covers K / gridDim.z and writes
+// rows go straight to registers, split hi + lo. Loads run two stages ahead of the MFMAs.
+// gridDim.z > 1 splits K: split z covers K / gridDim.z and writes
 // its partial sums (kGemmPartial) to C + z M ldc.
 // ---------------------------------------------------------------------------------------------
 template <bool NORM, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_lds(GemmParams p) {
   constexpr int BK = 64, WP = BK + 8;
-  __shared__ __align__(16) uint16_t ws[2][64][WP];
+  __shared__ __align__(16) uint16_t ws[3][64][WP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kg = lane >> 4;
   const uint32_t m0 = blockIdx.y * 64 + wave * 16, n0 = blockIdx.x * 64;
   const uint32_t kz = p.K / gridDim.z, kbeg = blockIdx.z * kz, nst = kz / BK;
   const uint32_t arow = min(m0 + uint32_t(li), p.M - 1);
-  const float* Ar = p.A + size_t(arow) * p.lda + kbeg;
+  const float* Ar = p.A + size_t(arow) * p.lda + kbeg + 8 * kg;
   const float rs = NORM ? p.rowscale[arow] : 1.0f;
-  const uint16_t* gp = NORM ? p.gain + kbeg : nullptr;
+  const uint16_t* gp = NORM ? p.gain + kbeg + 8 * kg : nullptr;
   // W stage: 64 rows x 8 chunks of 16 B; thread t moves chunks t and t + 256
   const uint16_t* Wsrc[2];
 #pragma unroll
@@ -179,61 +179,75 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmParams p) {
     const int c = tid + 256 * i;
     Wsrc[i] = p.W + size_t(min(n0 + uint32_t(c >> 3), p.N - 1)) * p.K + kbeg + 8 * (c & 7);
   }
-  u32x4 wn[2];
-  uint4 gn[2];
-  float4 an[2][2];
-  auto load = [&](uint32_t stg) __attribute__((always_inline)) {
+  // one stage in registers: its W chunks (bound for LDS), A fragments and gains
+  struct Stage {
+    u32x4 w[2];
+    f32x4 a[2][2];
+    u32x4 g[2];
+  };
+  auto load = [&](Stage& r, uint32_t stg) __attribute__((always_inline)) {
     const uint32_t k = stg * BK;
 #pragma unroll
-    for (int i = 0; i < 2; i++) wn[i] = *reinterpret_cast<const u32x4*>(Wsrc[i] + k);
+    for (int i = 0; i < 2; i++) r.w[i] = *reinterpret_cast<const u32x4*>(Wsrc[i] + k);
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-      an[u][0] = *reinterpret_cast<const float4*>(Ar + k + 32 * u + 8 * kg);
-      an[u][1] = *reinterpret_cast<const float4*>(Ar + k + 32 * u + 8 * kg + 4);
-      if constexpr (NORM) gn[u] = *reinterpret_cast<const uint4*>(gp + k + 32 * u + 8 * kg);
+      r.a[u][0] = *reinterpret_cast<const f32x4*>(Ar + k + 32 * u);
+      r.a[u][1] = *reinterpret_cast<const f32x4*>(Ar + k + 32 * u + 4);
+      if constexpr (NORM) r.g[u] = *reinterpret_cast<const u32x4*>(gp + k + 32 * u);
     }
   };
-  auto store_w = [&](int buf) __attribute__((always_inline)) {
+  auto store_w = [&](const Stage& r, uint32_t buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; i++) {
       const int c = tid + 256 * i;
-      *reinterpret_cast<u32x4*>(&ws[buf][c >> 3][8 * (c & 7)]) = wn[i];
+      *reinterpret_cast<u32x4*>(&ws[buf][c >> 3][8 * (c & 7)]) = r.w[i];
     }
   };
   f32x4 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-  load(0);
-  store_w(0);
-  __syncthreads();
-  for (uint32_t stg = 0; stg < nst; stg++) {
+  // Software pipeline over three LDS buffers: at step s the W tile of stage s is in buffer
+  // s % 3, stage s + 1's W (loaded one step earlier) goes to buffer (s + 1) % 3, whose last
+  // readers were at step s - 2, and stage s + 2 is loaded into the registers stage s vacates.
+  auto step = [&](Stage& cur, Stage& nxt, uint32_t s) __attribute__((always_inline)) {
+    store_w(nxt, (s + 1) % 3);
     bf16x8 hi[2], lo[2];
 #pragma unroll
     for (int u = 0; u < 2; u++) {
-      float v[8] = {an[u][0].x, an[u][0].y, an[u][0].z, an[u][0].w, an[u][1].x, an[u][1].y, an[u][1].z, an[u][1].w};
+      float v[8] = {cur.a[u][0][0], cur.a[u][0][1], cur.a[u][0][2], cur.a[u][0][3],
+                    cur.a[u][1][0], cur.a[u][1][1], cur.a[u][1][2], cur.a[u][1][3]};
       if constexpr (NORM) {
-        const uint32_t gg[4] = {gn[u].x, gn[u].y, gn[u].z, gn[u].w};
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          v[2 * e] = (v[2 * e] * rs) * __uint_as_float(gg[e] << 16);
-          v[2 * e + 1] = (v[2 * e + 1] * rs) * __uint_as_float(gg[e] & 0xFFFF0000u);
+          v[2 * e] = (v[2 * e] * rs) * __uint_as_float(cur.g[u][e] << 16);
+          v[2 * e + 1] = (v[2 * e + 1] * rs) * __uint_as_float(cur.g[u][e] & 0xFFFF0000u);
         }
       }
       split8(v, hi[u], lo[u]);
     }
-    load(min(stg + 1, nst - 1));  // unconditional: the last stage reloads itself
-    const int buf = int(stg & 1);
+    load(cur, min(s + 2, nst - 1));  // unconditional: the last stages reload the last one
+    if (s < nst) {                   // an odd stage count ends with one empty step
+      const uint32_t buf = s % 3;
 #pragma unroll
-    for (int u = 0; u < 2; u++) {
+      for (int u = 0; u < 2; u++) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const bf16x8 b = *reinterpret_cast<const bf16x8*>(&ws[buf][16 * j + li][32 * u + 8 * kg]);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[u], b, acc[j], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[u], b, acc[j], 0, 0, 0);
+        for (int j = 0; j < 4; j++) {
+          const bf16x8 b = *reinterpret_cast<const bf16x8*>(&ws[buf][16 * j + li][32 * u + 8 * kg]);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[u], b, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[u], b, acc[j], 0, 0, 0);
+        }
       }
     }
-    store_w(buf ^ 1);  // that buffer's last reads were the previous stage's, before its barrier
     __syncthreads();
+  };
+  Stage r0, r1;
+  load(r0, 0);
+  load(r1, min(1u, nst - 1));
+  store_w(r0, 0);
+  __syncthreads();
+  for (uint32_t s = 0; s < nst; s += 2) {
+    step(r0, r1, s);
+    step(r1, r0, s + 1);
   }
 
   // epilogue: lane holds C[m0 + 4 kg + r][n0 + 16 j + li]
