@@ -8,7 +8,7 @@
 //                  split into hi + lo bf16 so the products keep ~16 mantissa bits; epilogues
 //                  store / residual add / silu(gate)*up                 (cpu_inference.rs:225-257)
 //   k_qk_rope      per token and head: q/k RMSNorm + RoPE, K/V append   (cpu_inference.rs:134-141)
-//   k_attn_causal  token m attends positions 0..start+m on f32 MFMA     (cpu_inference.rs:144-162)
+//   k_attn_causal_bf  token m attends positions 0..start+m, split bf16 MFMA (cpu_inference.rs:144-162)
 #include "batch.h"
 
 #include <algorithm>
@@ -459,25 +459,30 @@ __global__ __launch_bounds__(256) void k_qk_rope(BatchAttnParams p) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Causal attention of a chunk on the f32 matrix cores (v_mfma_f32_16x16x4_f32, f32 products as
-// in the reference). Workgroup (KV head g, block of TOK = 64 / G tokens, key run s) serves 64
-// query rows, row r = token mb + r / G of head g G + r % G; wave w owns rows 16 w .. 16 w + 15
-// and lane l the row 16 w + l % 16. Keys come in LDS tiles of 64 positions (the next tile is
-// loaded into registers while this one is used). Per tile a wave computes the transposed
-// scores S^T[key][row] = sum_d K[key][d] Q[row][d] (the lane with kg = l / 16 takes dims
-// 32 kg .. 32 kg + 31 of its row, held in registers) and then O^T[d][row] += sum_key
-// V[key][d] P^T[key][row]. In the 16 x 16 output layout a lane holds keys 16 j + 4 kg + r
-// (j, r < 4) of its own row, which is exactly the operand layout P^T needs, and O^T's column is
-// again its row: the online softmax (max, rescale, sum) stays in the lane plus two shuffles
-// across kg, with no LDS round trip for P. Rows with no visible key in the run keep m = -inf,
+// Causal attention of a chunk on the bf16 matrix cores (v_mfma_f32_16x16x32_bf16) with split
+// operands: q, and f32 K / V, are split into hi + lo bf16 (K and V once, when a tile is staged
+// in LDS), and each product keeps the hi*hi, hi*lo and lo*hi terms (lo*lo is below 2^-16 of the
+// product); a bf16 cache is exact in hi, so its tiles take two terms.
+// Workgroup (KV head g, block of TOK = 64 / G tokens, key run s) serves 64 query rows, row
+// r = token mb + r / G of head g G + r % G; wave w owns rows 16 w .. 16 w + 15 and lane l the
+// row 16 w + l % 16. Keys come in LDS tiles of 64 positions (the next tile is loaded into
+// registers while this one is used). Per tile a wave computes the transposed scores
+// S^T[key][row] (A = K rows: lane has key 16 j + l % 16, dims 32 s + 8 kg .. +7 with
+// kg = l / 16; B = q of row l % 16, same dims). In the 16 x 16 output layout a lane then holds
+// keys 16 j + 4 kg + r (j, r < 4) of its own row, so the online softmax (max, rescale, sum)
+// stays in the lane plus two shuffles across kg, with no LDS round trip for P. Next
+// O^T[d][row] += V^T P^T, with the k index of a 32-key step mapped so that lane kg's eight B
+// values are its own probabilities for keys 4 kg + r and 16 + 4 kg + r (r < 4); the A side
+// reads those keys from a transposed V tile (Vt[d][key], written from key pairs when staging),
+// and O^T's column is again the lane's row. Rows with no visible key in the run keep m = -inf,
 // l = 0. One run: normalized output to att [M][n_heads][128]; several: (m, l, acc) partials to
 // part [M][n_heads][runs][kPartStride], combined by k_attn_merge_rows.
 // ---------------------------------------------------------------------------------------------
 template <int G, bool KV_BF16>
-__global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
-  constexpr int D = kHeadDim, BK = 64, TOK = 64 / G, KS = D + 4;  // row pad: 16 keys x 4 dims hit 64 banks
-  __shared__ __align__(16) float ks[BK][KS];
-  __shared__ __align__(16) float vs[BK][KS];
+__global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
+  constexpr int D = kHeadDim, BK = 64, TOK = 64 / G, KP = D + 8, VP = BK + 8, NL = KV_BF16 ? 1 : 2;
+  __shared__ __align__(16) uint16_t ks[NL][BK][KP];  // [hi, lo][key][dim]
+  __shared__ __align__(16) uint16_t vt[NL][D][VP];   // [hi, lo][dim][key]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
   const uint32_t g = blockIdx.x, mb = blockIdx.y * TOK, run = blockIdx.z, runs = gridDim.z;
   const uint32_t row = uint32_t(wave) * 16 + uint32_t(li);
@@ -488,13 +493,15 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
   const uint32_t k_begin = run * p.key_run;
   const uint32_t k_end = min(last + 1, k_begin + p.key_run);  // this run: positions [k_begin, k_end)
 
-  float q[32];
+  bf16x8 qh[4], ql[4];
   {
-    const float4* qp = reinterpret_cast<const float4*>(p.q + (size_t(tok_c) * p.n_heads + head) * D + 32 * kg);
+    const float* qp = p.q + (size_t(tok_c) * p.n_heads + head) * D + 8 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 v = qp[i];
-      q[4 * i] = v.x; q[4 * i + 1] = v.y; q[4 * i + 2] = v.z; q[4 * i + 3] = v.w;
+    for (int st = 0; st < 4; st++) {
+      const float4 a = *reinterpret_cast<const float4*>(qp + 32 * st);
+      const float4 b = *reinterpret_cast<const float4*>(qp + 32 * st + 4);
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      split8(v, qh[st], ql[st]);
     }
   }
   f32x4 o[8];
@@ -502,57 +509,89 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
   for (int i = 0; i < 8; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  // tile staging: thread t moves rows t / 32 + 8 i (i < 8), dims 4 (t % 32) .. +3
+  // staging: K rows lr + 8 i (i < 8) at dims ld .. ld + 3 (coalesced rows); V key pair
+  // 2 vk, 2 vk + 1 at dims 4 vb + 32 i .. +3 (i < 4), so that Vt gets (key, key + 1) words
   const size_t hbase = size_t(g) * p.max_seq * D;
-  const int lr = tid >> 5, ld = (tid & 31) * 4;
+  const int lr = tid >> 5, ld = (tid & 31) * 4, vk = tid & 31, vb = tid >> 5;
   using Pre = typename std::conditional<KV_BF16, uint2, float4>::type;
   Pre kp[8], vp[8];
   auto load_tile = [&](uint32_t t0) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-      const size_t off = hbase + size_t(min(t0 + uint32_t(lr + 8 * i), k_end - 1)) * D + ld;
+      const size_t ko = hbase + size_t(min(t0 + uint32_t(lr + 8 * i), k_end - 1)) * D + ld;
+      const size_t vo = hbase + size_t(min(t0 + uint32_t(2 * vk + (i & 1)), k_end - 1)) * D + 4 * vb + 32 * (i >> 1);
       if constexpr (KV_BF16) {
-        kp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.k_cache) + off);
-        vp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + off);
+        kp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.k_cache) + ko);
+        vp[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + vo);
       } else {
-        kp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k_cache) + off);
-        vp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v_cache) + off);
+        kp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.k_cache) + ko);
+        vp[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v_cache) + vo);
       }
     }
   };
-  auto to_f4 = [](const Pre& v) __attribute__((always_inline)) {
-    if constexpr (KV_BF16)
-      return make_float4(__uint_as_float(v.x << 16), __uint_as_float(v.x & 0xFFFF0000u),
-                         __uint_as_float(v.y << 16), __uint_as_float(v.y & 0xFFFF0000u));
-    else
-      return v;
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  auto pk = [](float a, float b) __attribute__((always_inline)) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+  };
+  auto store_tile = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      if constexpr (KV_BF16) {
+        *reinterpret_cast<uint2*>(&ks[0][lr + 8 * i][ld]) = kp[i];
+      } else {
+        const float4 v = kp[i];
+        const uint32_t h0 = pk(v.x, v.y), h1 = pk(v.z, v.w);
+        *reinterpret_cast<uint2*>(&ks[0][lr + 8 * i][ld]) = make_uint2(h0, h1);
+        *reinterpret_cast<uint2*>(&ks[NL - 1][lr + 8 * i][ld]) =
+            make_uint2(pk(v.x - __uint_as_float(h0 << 16), v.y - __uint_as_float(h0 & 0xFFFF0000u)),
+                       pk(v.z - __uint_as_float(h1 << 16), v.w - __uint_as_float(h1 & 0xFFFF0000u)));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {  // vp[i]: key 2 vk, vp[i + 1]: key 2 vk + 1, dims 4 vb + 16 i ..
+      const int d0 = 4 * vb + 16 * i;
+      if constexpr (KV_BF16) {
+        const uint2 a = vp[i], b = vp[i + 1];
+        const uint32_t w[4] = {(a.x & 0xFFFFu) | (b.x << 16), (a.x >> 16) | (b.x & 0xFFFF0000u),
+                               (a.y & 0xFFFFu) | (b.y << 16), (a.y >> 16) | (b.y & 0xFFFF0000u)};
+#pragma unroll
+        for (int c = 0; c < 4; c++) *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][2 * vk]) = w[c];
+      } else {
+        const float a[4] = {vp[i].x, vp[i].y, vp[i].z, vp[i].w};
+        const float b[4] = {vp[i + 1].x, vp[i + 1].y, vp[i + 1].z, vp[i + 1].w};
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const uint32_t h = pk(a[c], b[c]);
+          *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][2 * vk]) = h;
+          *reinterpret_cast<uint32_t*>(&vt[NL - 1][d0 + c][2 * vk]) =
+              pk(a[c] - __uint_as_float(h << 16), b[c] - __uint_as_float(h & 0xFFFF0000u));
+        }
+      }
+    }
   };
   if (k_begin < k_end) load_tile(k_begin);
   for (uint32_t t0 = k_begin; t0 < k_end; t0 += BK) {
     __syncthreads();  // the previous tile's LDS reads are done
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-      *reinterpret_cast<float4*>(&ks[lr + 8 * i][ld]) = to_f4(kp[i]);
-      *reinterpret_cast<float4*>(&vs[lr + 8 * i][ld]) = to_f4(vp[i]);
-    }
+    store_tile();
     __syncthreads();
     if (t0 + BK < k_end) load_tile(t0 + BK);
 
-    // S^T for 4 blocks of 16 keys
     f32x4 s[4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int t = 0; t < 8; t++) {
-        const float4 kv = *reinterpret_cast<const float4*>(&ks[16 * j + li][32 * kg + 4 * t]);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.x, q[4 * t], s[j], 0, 0, 0);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.y, q[4 * t + 1], s[j], 0, 0, 0);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.z, q[4 * t + 2], s[j], 0, 0, 0);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv.w, q[4 * t + 3], s[j], 0, 0, 0);
+      for (int st = 0; st < 4; st++) {
+        const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&ks[0][16 * j + li][32 * st + 8 * kg]);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[st], s[j], 0, 0, 0);
+        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[st], s[j], 0, 0, 0);
+        if constexpr (!KV_BF16) {
+          const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&ks[NL - 1][16 * j + li][32 * st + 8 * kg]);
+          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[st], s[j], 0, 0, 0);
+        }
       }
     }
-    // online softmax over the lane's 16 keys and the three other kg lanes of its row
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < 4; j++) {
@@ -584,14 +623,26 @@ __global__ __launch_bounds__(256) void k_attn_causal(BatchAttnParams p) {
     m_run = m_new;
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] *= corr;
-    // O^T += V^T P^T, k index = key 16 j + 4 kg + r
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int st = 0; st < 2; st++) {
+      const float pv[8] = {s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3],
+                           s[2 * st + 1][0], s[2 * st + 1][1], s[2 * st + 1][2], s[2 * st + 1][3]};
+      bf16x8 ph, pl;
+      split8(pv, ph, pl);
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float* vr = &vs[16 * j + 4 * kg + r][li];
-#pragma unroll
-        for (int i = 0; i < 8; i++) o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * i], s[j][r], o[i], 0, 0, 0);
+      for (int i = 0; i < 8; i++) {
+        const int d = 16 * i + li, k0 = 32 * st + 4 * kg;
+        const uint2 a = *reinterpret_cast<const uint2*>(&vt[0][d][k0]);
+        const uint2 b = *reinterpret_cast<const uint2*>(&vt[0][d][k0 + 16]);
+        const bf16x8 vh = __builtin_bit_cast(bf16x8, u32x4{a.x, a.y, b.x, b.y});
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[i], 0, 0, 0);
+        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[i], 0, 0, 0);
+        if constexpr (!KV_BF16) {
+          const uint2 c = *reinterpret_cast<const uint2*>(&vt[NL - 1][d][k0]);
+          const uint2 e = *reinterpret_cast<const uint2*>(&vt[NL - 1][d][k0 + 16]);
+          const bf16x8 vl = __builtin_bit_cast(bf16x8, u32x4{c.x, c.y, e.x, e.y});
+          o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[i], 0, 0, 0);
+        }
       }
     }
   }
@@ -749,8 +800,8 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
   hipError_t e = hipErrorInvalidValue;
 #define QE_ATT(GG)                                                                                         \
   if (G == GG) {                                                                                           \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal<GG, true>), grid, dim3(256), 0, st, q);               \
-    else hipLaunchKernelGGL((k_attn_causal<GG, false>), grid, dim3(256), 0, st, q);                        \
+    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal_bf<GG, true>), grid, dim3(256), 0, st, q);            \
+    else hipLaunchKernelGGL((k_attn_causal_bf<GG, false>), grid, dim3(256), 0, st, q);                     \
     e = hipGetLastError();                                                                                 \
   }
   QE_ATT(1)

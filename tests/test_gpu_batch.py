@@ -92,6 +92,25 @@ def test_tiny_verify_matches_oracle(gpu, tiny_ckpt, k):
     assert len(cache) == 40 + k
 
 
+@pytest.mark.parametrize("n_prompt,chunk", [(100, 32), (300, 0)])
+def test_tiny_prefill_batch_bf16_kv_matches_sequential(gpu, tiny_ckpt, n_prompt, chunk):
+    """bf16 cache: the chunked path stores the same rounded K/V as the token-by-token path (whose
+    drift from the f32 cache is bounded separately), so the two agree closely"""
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(41, n_prompt, TINY.vocab_size)
+    cb = qe.KVCache(m, n_prompt + 8, qe.QE_KV_BF16)
+    cs = qe.KVCache(m, n_prompt + 8, qe.QE_KV_BF16)
+    got = m.prefill_batch(prompt, 0, cb, chunk=chunk)
+    for pos, tok in enumerate(prompt):
+        ref = m.forward(int(tok), pos, cs)
+    assert float(np.max(np.abs(got - ref))) < 5e-3
+    draft = qe.random_prompt(43, 4, TINY.vocab_size)
+    rows = m.verify(draft, n_prompt, cb)
+    for i, tok in enumerate(draft):
+        ref = m.forward(int(tok), n_prompt + i, cs)
+        assert float(np.max(np.abs(rows[i] - ref))) < 5e-3, f"verify row {i}"
+
+
 def test_batch_argument_errors(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 8)
