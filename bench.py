@@ -236,23 +236,8 @@ def prefill_bench(torch, qe, model, cfg, args):
     n, chunk = args.prefill_tokens, args.chunk
     ids = qe.random_prompt(11, n, cfg.vocab_size)
     cache = qe.KVCache(model, n + 8)
-    model.prefill_batch(ids[:chunk], 0, cache, chunk=chunk, want_logits=False)  # warm-up, buffers
-    stream = torch.cuda.ExternalStream(model.stream_handle())
-    best = float("inf")
-    for _ in range(3):
-        cache = qe.KVCache(model, n + 8)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        model.prefill_batch(ids, 0, cache, chunk=chunk, want_logits=False)
-        torch.cuda.synchronize()
-        best = min(best, time.perf_counter() - t0)
-    H, I, V, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_hidden_layers
+    H, I, L = cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers
     QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
-    proj = L * ((QD + 2 * KD) * H + H * QD + 2 * I * H + H * I)
-    gemm_flop = 2.0 * n * proj
-    attn_flop = 8192.0 * sum(p + 1 for p in range(n)) * L
-    # the engine's matrix-core work: both bf16 halves of every GEMM
-    mfma_flop = 2 * gemm_flop
     # on-box bf16 GEMM ceiling: torch (hipBLASLt) at the largest projection shape of a chunk
     a = torch.randn(chunk, H, device="cuda", dtype=torch.bfloat16)
     w = torch.randn(2 * I, H, device="cuda", dtype=torch.bfloat16)
@@ -267,6 +252,20 @@ def prefill_bench(torch, qe, model, cfg, args):
     e1.record()
     e1.synchronize()
     lib_tflops = 2.0 * chunk * 2 * I * H * 50 / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    model.prefill_batch(ids[:chunk], 0, cache, chunk=chunk, want_logits=False)  # warm-up, buffers
+    best = float("inf")
+    for _ in range(3):
+        cache = qe.KVCache(model, n + 8)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        model.prefill_batch(ids, 0, cache, chunk=chunk, want_logits=False)
+        torch.cuda.synchronize()
+        best = min(best, time.perf_counter() - t0)
+    proj = L * ((QD + 2 * KD) * H + H * QD + 2 * I * H + H * I)
+    gemm_flop = 2.0 * n * proj
+    attn_flop = 8192.0 * sum(p + 1 for p in range(n)) * L
+    # the engine's matrix-core work: both bf16 halves of every GEMM
+    mfma_flop = 2 * gemm_flop
     # k = 4 verify vs one decode step, on a cache holding the prompt
     draft = qe.random_prompt(13, 4, cfg.vocab_size)
     vcache = qe.KVCache(model, n + 16)

@@ -300,24 +300,27 @@ __global__ __launch_bounds__(256) void k_resadd_partials(float* __restrict__ x, 
 // ---------------------------------------------------------------------------------------------
 // Skinny GEMM for M <= 16 MT rows (verify, the last chunk of a prefill): the weights are the
 // whole cost, so the work is spread over K as well as N. Workgroup = NW waves on 16 columns
-// n0 .. n0+15; wave w covers the k steps [w KPW, (w+1) KPW) with KPW = ceil(K / 32 / NW), two
-// per iteration (loads clamped to the last step, steps past the range masked by a zero W
-// fragment), MT m-tiles per W fragment, A split hi + lo as in k_gemm. The NW partial tiles are
-// summed in LDS in wave order. With the norm, each lane also sums x^2 of its row over the
-// steps it loads, so C = s[m] sum_k (x g)[m][k] W[n][k] with s[m] = 1 / sqrt(mean x^2 + eps)
-// (the scale applied after the sum, a reassociation of the reference's f32 product).
+// n0 .. n0+15 and the K range of split blockIdx.y (gridDim.y > 1: kGemmPartial sums to
+// C + split M ldc); wave w covers the k steps [w KPW, (w+1) KPW) with KPW = ceil(K / 32 / NW),
+// KMAX at a time with every load of the batch issued before any use (clamped to the last step;
+// steps past the range masked by a zero W fragment), MT m-tiles per W fragment, A split
+// hi + lo as in k_gemm. The NW partial tiles are summed in LDS in wave order. With the norm,
+// each lane also sums x^2 of its row over the steps it loads, so
+// C = s[m] sum_k (x g)[m][k] W[n][k] with s[m] = 1 / sqrt(mean x^2 + eps) (the scale applied
+// after the sum, a reassociation of the reference's f32 product).
 // ---------------------------------------------------------------------------------------------
-template <bool NORM, int EPI, int MT, int NW>
+template <bool NORM, int EPI, int MT, int NW, int KMAX>
 __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmParams p) {
-  constexpr int KU = 2;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int li = lane & 15, kg = lane >> 4;
   const uint32_t n0 = blockIdx.x * 16;
-  const uint32_t KS = p.K / 32, KPW = (KS + NW - 1) / NW, s0 = uint32_t(wave) * KPW;
-  const uint16_t* Wr = p.W + size_t(min(n0 + uint32_t(li), p.N - 1)) * p.K;
+  const uint32_t kz = p.K / gridDim.y, kbeg = blockIdx.y * kz;  // this split's k range
+  const uint32_t KS = kz / 32, KPW = (KS + NW - 1) / NW, s0 = uint32_t(wave) * KPW;
+  const uint16_t* Wr = p.W + size_t(min(n0 + uint32_t(li), p.N - 1)) * p.K + kbeg + 8 * kg;
   const float* Ar[MT];
 #pragma unroll
-  for (int t = 0; t < MT; t++) Ar[t] = p.A + size_t(min(uint32_t(16 * t + li), p.M - 1)) * p.lda;
+  for (int t = 0; t < MT; t++) Ar[t] = p.A + size_t(min(uint32_t(16 * t + li), p.M - 1)) * p.lda + kbeg + 8 * kg;
+  const uint16_t* gp = NORM ? p.gain + kbeg + 8 * kg : nullptr;
 
   f32x4 acc[MT];
   float ss[MT];
@@ -326,56 +329,45 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmParams p) {
     acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
     ss[t] = 0.f;
   }
-  float4 a0[KU][MT], a1[KU][MT];
-  uint4 g[KU], w[KU];
-  auto load = [&](uint32_t it) __attribute__((always_inline)) {
+  for (uint32_t base = 0; base < KPW; base += KMAX) {
+    u32x4 w[KMAX], g[KMAX];
+    f32x4 a0[KMAX][MT], a1[KMAX][MT];
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-      const uint32_t k = 32 * min(s0 + it + uint32_t(u), KS - 1) + 8 * kg;
-      w[u] = *reinterpret_cast<const uint4*>(Wr + k);
+    for (int u = 0; u < KMAX; u++) {
+      const uint32_t k = 32 * min(s0 + base + uint32_t(u), KS - 1);
+      w[u] = *reinterpret_cast<const u32x4*>(Wr + k);
 #pragma unroll
       for (int t = 0; t < MT; t++) {
-        a0[u][t] = *reinterpret_cast<const float4*>(Ar[t] + k);
-        a1[u][t] = *reinterpret_cast<const float4*>(Ar[t] + k + 4);
+        a0[u][t] = *reinterpret_cast<const f32x4*>(Ar[t] + k);
+        a1[u][t] = *reinterpret_cast<const f32x4*>(Ar[t] + k + 4);
       }
-      if constexpr (NORM) g[u] = *reinterpret_cast<const uint4*>(p.gain + k);
+      if constexpr (NORM) g[u] = *reinterpret_cast<const u32x4*>(gp + k);
     }
-  };
-  load(0);
-  for (uint32_t it = 0; it < KPW; it += KU) {
-    bf16x8 hi[KU][MT], lo[KU][MT];
-    uint4 wc[KU];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < KU; u++) {
-      const bool ok = it + u < KPW && s0 + it + u < KS;
-      wc[u] = make_uint4(ok ? w[u].x : 0u, ok ? w[u].y : 0u, ok ? w[u].z : 0u, ok ? w[u].w : 0u);
+    for (int u = 0; u < KMAX; u++) {
+      const bool ok = base + u < KPW && s0 + base + u < KS;
+      const u32x4 wc = ok ? w[u] : u32x4{0u, 0u, 0u, 0u};
+      const bf16x8 b = __builtin_bit_cast(bf16x8, wc);
 #pragma unroll
       for (int t = 0; t < MT; t++) {
-        float v[8] = {a0[u][t].x, a0[u][t].y, a0[u][t].z, a0[u][t].w,
-                      a1[u][t].x, a1[u][t].y, a1[u][t].z, a1[u][t].w};
+        float v[8] = {a0[u][t][0], a0[u][t][1], a0[u][t][2], a0[u][t][3],
+                      a1[u][t][0], a1[u][t][1], a1[u][t][2], a1[u][t][3]};
         if constexpr (NORM) {
           float q = 0.f;
 #pragma unroll
           for (int e = 0; e < 8; e++) q += v[e] * v[e];
           ss[t] += ok ? q : 0.f;
-          const uint32_t gg[4] = {g[u].x, g[u].y, g[u].z, g[u].w};
 #pragma unroll
           for (int e = 0; e < 4; e++) {
-            v[2 * e] *= __uint_as_float(gg[e] << 16);
-            v[2 * e + 1] *= __uint_as_float(gg[e] & 0xFFFF0000u);
+            v[2 * e] *= __uint_as_float(g[u][e] << 16);
+            v[2 * e + 1] *= __uint_as_float(g[u][e] & 0xFFFF0000u);
           }
         }
-        split8(v, hi[u][t], lo[u][t]);
-      }
-    }
-    if (it + KU < KPW) load(it + KU);
-#pragma unroll
-    for (int u = 0; u < KU; u++) {
-      const bf16x8 b = __builtin_bit_cast(bf16x8, u32x4{wc[u].x, wc[u].y, wc[u].z, wc[u].w});
-#pragma unroll
-      for (int t = 0; t < MT; t++) {
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[u][t], b, acc[t], 0, 0, 0);
-        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[u][t], b, acc[t], 0, 0, 0);
+        bf16x8 hi, lo;
+        split8(v, hi, lo);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b, acc[t], 0, 0, 0);
+        acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b, acc[t], 0, 0, 0);
       }
     }
   }
@@ -395,26 +387,50 @@ __global__ __launch_bounds__(64 * NW) void k_gemm_skinny(GemmParams p) {
     }
   }
   __syncthreads();
-  if (tid >= MT * 256) return;  // whole waves
-  const uint32_t row = uint32_t(tid) >> 4, col = uint32_t(tid) & 15;
-  float c = 0.f;
+  float* C = p.C + (EPI == kGemmPartial ? size_t(blockIdx.y) * p.M * p.ldc : 0);
+  // MT * 256 outputs over the workgroup's threads; each pass covers whole waves
+  for (uint32_t o = uint32_t(tid); o < uint32_t(MT * 256); o += uint32_t(64 * NW)) {
+    const uint32_t row = o >> 4, col = o & 15;
+    float c = 0.f;
 #pragma unroll
-  for (int v = 0; v < NW; v++) c += part[v][row][col];
-  if constexpr (NORM) {
-    float q = 0.f;
+    for (int v = 0; v < NW; v++) c += part[v][row][col];
+    if constexpr (NORM) {
+      float q = 0.f;
 #pragma unroll
-    for (int v = 0; v < NW; v++) q += ssp[v][row];
-    c *= 1.0f / sqrtf(q / float(p.K) + p.eps);
+      for (int v = 0; v < NW; v++) q += ssp[v][row];
+      c *= 1.0f / sqrtf(q / float(p.K) + p.eps);
+    }
+    const uint32_t m = row, n = n0 + col;
+    if constexpr (EPI == kGemmSiluPair) {
+      const float up = __shfl_xor(c, 1);  // column n ^ 1 of the same row
+      if (m < p.M && n < p.N && (col & 1) == 0) C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
+    } else if constexpr (EPI == kGemmResAdd) {
+      if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] += c;
+    } else {
+      if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] = c;
+    }
   }
-  const uint32_t m = row, n = n0 + col;
-  if constexpr (EPI == kGemmSiluPair) {
-    const float up = __shfl_xor(c, 1);  // column n ^ 1 of the same row
-    if (m < p.M && n < p.N && (col & 1) == 0) p.C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
-  } else if constexpr (EPI == kGemmResAdd) {
-    if (m < p.M && n < p.N) p.C[size_t(m) * p.ldc + n] += c;
+}
+
+// skinny launch: MT m-tiles, NW waves (4 when K is split over workgroups, else 8), and the
+// batch of k steps loaded at once sized to the steps per wave
+template <bool NORM, int EPI>
+void launch_skinny(const GemmParams& p, uint32_t splits, hipStream_t st) {
+  const uint32_t NW = splits > 1 ? 4 : 8, KPW = ceil_div(p.K / splits / 32, NW);
+  const dim3 grid(ceil_div(p.N, 16), splits);
+  const bool two = p.M > 16, wide_k = KPW > 4;
+#define QE_SK(MT, W, KM) hipLaunchKernelGGL((k_gemm_skinny<NORM, EPI, MT, W, KM>), grid, dim3(64 * W), 0, st, p)
+  // two m-tiles always load four steps at a time (eight do not fit their registers)
+  if (NW == 4) {
+    if (two) QE_SK(2, 4, 4);
+    else if (wide_k) QE_SK(1, 4, 8);
+    else QE_SK(1, 4, 4);
   } else {
-    if (m < p.M && n < p.N) p.C[size_t(m) * p.ldc + n] = c;
+    if (two) QE_SK(2, 8, 4);
+    else if (wide_k) QE_SK(1, 8, 8);
+    else QE_SK(1, 8, 4);
   }
+#undef QE_SK
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -716,22 +732,11 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
     return hipErrorInvalidValue;
   if (norm && !p.gain) return hipErrorInvalidValue;
   if (p.M <= kGemmSkinnyMaxM) {
-    // one m-tile: 16 waves per workgroup when there are few 16-column blocks, so the chip still
-    // fills; two m-tiles: 8 waves (their registers do not fit 16)
-    const uint32_t blocks = ceil_div(p.N, 16);
-    const bool wide = blocks < 256;
-#define QE_SKINNY_EPI(NRM, E)                                                                           \
-  do {                                                                                                  \
-    if (p.M > 16) hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 2, 8>), dim3(blocks), dim3(512), 0, st, p); \
-    else if (wide) hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 1, 16>), dim3(blocks), dim3(1024), 0, st, p); \
-    else hipLaunchKernelGGL((k_gemm_skinny<NRM, E, 1, 8>), dim3(blocks), dim3(512), 0, st, p);          \
-  } while (0)
-    if (norm && epi == kGemmStore) QE_SKINNY_EPI(true, kGemmStore);
-    else if (norm && epi == kGemmSiluPair) QE_SKINNY_EPI(true, kGemmSiluPair);
-    else if (!norm && epi == kGemmStore) QE_SKINNY_EPI(false, kGemmStore);
-    else if (!norm && epi == kGemmResAdd) QE_SKINNY_EPI(false, kGemmResAdd);
+    if (norm && epi == kGemmStore) launch_skinny<true, kGemmStore>(p, 1, st);
+    else if (norm && epi == kGemmSiluPair) launch_skinny<true, kGemmSiluPair>(p, 1, st);
+    else if (!norm && epi == kGemmStore) launch_skinny<false, kGemmStore>(p, 1, st);
+    else if (!norm && epi == kGemmResAdd) launch_skinny<false, kGemmResAdd>(p, 1, st);
     else return hipErrorInvalidValue;
-#undef QE_SKINNY_EPI
     return hipGetLastError();
   }
   if (norm && !p.rowscale) return hipErrorInvalidValue;
@@ -760,15 +765,23 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
 }
 
 uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K) {
-  const uint32_t tiles = ceil_div(N, 64) * ceil_div(M, 64);
+  // tiles of the kernel that runs M rows, and the depth one split must stay a multiple of
+  const bool skinny = M <= kGemmSkinnyMaxM;
+  const uint32_t tiles = skinny ? ceil_div(N, 16) : ceil_div(N, 64) * ceil_div(M, 64), unit = skinny ? 32 : 64;
   uint32_t z = 1;
-  while (z < 8 && tiles * z < 256 && K % (128 * z) == 0) z *= 2;
+  while (z < 8 && tiles * z < 256 && K % (2 * unit * z) == 0) z *= 2;
   return z;
 }
 
 hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t st) {
-  if (p.M == 0 || p.N == 0 || p.N % 2 || p.lda % 4 || !p.A || !p.W || !p.C || splits == 0 || p.K % (64 * splits))
+  if (p.M == 0 || p.N == 0 || p.N % 2 || p.lda % 4 || !p.A || !p.W || !p.C || splits == 0)
     return hipErrorInvalidValue;
+  if (p.M <= kGemmSkinnyMaxM) {
+    if (p.K % (32 * splits)) return hipErrorInvalidValue;
+    launch_skinny<false, kGemmPartial>(p, splits, st);
+    return hipGetLastError();
+  }
+  if (p.K % (64 * splits)) return hipErrorInvalidValue;
   const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), splits);
   hipLaunchKernelGGL((k_gemm_lds<false, kGemmPartial>), grid, dim3(256), 0, st, p);
   return hipGetLastError();

@@ -471,8 +471,8 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
   };
   // x += A W^T, then m->bs = the row scales of the updated x
   auto gemm_resadd = [&](const float* A, uint32_t lda, const uint16_t* W, uint32_t K) -> int {
-    if (skinny) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
-    if (K % 64) {  // no split: residual epilogue, then the row scales
+    if (skinny && qe::gemm_splits(M, H, K) == 1) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
+    if (!skinny && K % 64) {  // no split: residual epilogue, then the row scales
       if (int rc2 = gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd)) return rc2;
       HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
       return QE_OK;

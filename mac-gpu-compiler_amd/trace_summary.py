@@ -1,9 +1,13 @@
 """Markdown table of the kernels in a `rocprofv3 --kernel-trace --stats` database.
 
   python mac-gpu-compiler_amd/trace_summary.py RUN_results.db [--top N]
+      [--window MARKER FIRST LAST]
 
 Reads the `top_kernels` view of the rocprofv3 SQLite output: name, calls, average and total
 duration, share of GPU time. Kernel names are shortened (namespaces and parameter lists dropped).
+With --window, only the dispatches from the FIRST-th to just before the LAST-th dispatch of a
+kernel whose name contains MARKER (0-based, in start order) are counted, from the `kernels`
+view: e.g. one multi-chunk prefill between two of its embedding launches.
 """
 import argparse
 import re
@@ -20,8 +24,29 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("db")
     ap.add_argument("--top", type=int, default=16)
+    ap.add_argument("--window", nargs=3, metavar=("MARKER", "FIRST", "LAST"))
     a = ap.parse_args()
     db = sqlite3.connect(a.db)
+    if a.window:
+        marker, first, last = a.window[0], int(a.window[1]), int(a.window[2])
+        ks = db.execute("select name, start, duration from kernels order by start").fetchall()
+        marks = [i for i, k in enumerate(ks) if marker in k[0]]
+        sel = ks[marks[first]:marks[last]] if last < len(marks) else ks[marks[first]:]
+        agg = {}
+        for name, _, dur in sel:  # the kernels view reports nanoseconds
+            c = agg.setdefault(short(name), [0, 0.0])
+            c[0] += 1
+            c[1] += dur / 1e3
+        busy = sum(v[1] for v in agg.values())
+        span = (sel[-1][1] + sel[-1][2] - sel[0][1]) / 1e3
+        rows = sorted(((n, c, t / c, t, 100.0 * t / busy) for n, (c, t) in agg.items()), key=lambda r: -r[3])
+        print(f"Window: {len(sel)} dispatches, {busy / 1e3:.3f} ms of kernel time in a {span / 1e3:.3f} ms span.")
+        print()
+        print("| Kernel | Calls | Avg (us) | Total (ms) | % of window |")
+        print("|---|---|---|---|---|")
+        for name, calls, avg, total, pct in rows[: a.top]:
+            print(f"| `{name}` | {calls} | {avg:.3f} | {total / 1e3:.3f} | {pct:.1f} |")
+        return
     rows = db.execute("select name, total_calls, average, total_duration, percentage from top_kernels "
                       f"order by total_duration desc limit {int(a.top)}").fetchall()
     print("| Kernel | Calls | Avg (us) | Total (ms) | % of GPU time |")
