@@ -96,13 +96,15 @@ struct qe_model {
   float* bpart = nullptr;   // causal attention partials
   float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
   float* blogits = nullptr;
-  uint32_t* bids = nullptr;
+  uint32_t* ids_dev = nullptr;  // the token ids of one qe_prefill_batch / qe_verify call
+  uint64_t ids_cap = 0;
 
   ~qe_model() {  // teardown errors have nowhere to go; the handle is gone either way
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
     if (scratch) (void)hipFree(scratch);
     if (batch_mem) (void)hipFree(batch_mem);
+    if (ids_dev) (void)hipFree(ids_dev);
     if (h_logits) (void)hipHostFree(h_logits);
     if (h_small) (void)hipHostFree(h_small);
     if (stream) (void)hipStreamDestroy(stream);
@@ -420,7 +422,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
   const size_t ox = take(cap * H * 4), os = take(cap * 4), oqkv = take(cap * (QD + 2 * KD) * 4),
                oq = take(cap * QD * 4), oatt = take(cap * QD * 4), oh = take(cap * I * 4),
-               ologit = take(size_t(logit_rows) * c.vocab_size * 4), oids = take(cap * 4);
+               ologit = take(size_t(logit_rows) * c.vocab_size * 4);
   // attention partials: the most (tokens x key runs) any chunk of up to cap tokens asks for
   size_t part_rows = 0;
   for (uint32_t M = 1; M <= cap; M++)
@@ -441,16 +443,31 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   m->batt = reinterpret_cast<float*>(m->batch_mem + oatt);
   m->bh = reinterpret_cast<float*>(m->batch_mem + oh);
   m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
-  m->bids = reinterpret_cast<uint32_t*>(m->batch_mem + oids);
   m->bpart = reinterpret_cast<float*>(m->batch_mem + opart);
   m->bsplit = reinterpret_cast<float*>(m->batch_mem + osplit);
   return QE_OK;
 }
 
-// One chunk of M tokens (ids already in m->bids) at positions start..start+M-1 through every
-// layer, appending their K/V. all_logits: logits of every row to m->blogits [M][V]; otherwise
-// the last row's logits to m->logits (the decode step's buffer).
-int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_logits) {
+// Copies n token ids to the device (in stream order, before the kernels that read them).
+int upload_ids(qe_model* m, const uint32_t* ids, uint64_t n) {
+  if (n > m->ids_cap) {
+    HIP_TRY(hipStreamSynchronize(m->stream));
+    if (m->ids_dev) HIP_TRY(hipFree(m->ids_dev));
+    m->ids_dev = nullptr;
+    m->ids_cap = 0;
+    HIP_TRY(hipMalloc(&m->ids_dev, n * 4));
+    m->ids_cap = n;
+  }
+  HIP_TRY(hipMemcpyAsync(m->ids_dev, ids, n * 4, hipMemcpyHostToDevice, m->stream));
+  return QE_OK;
+}
+
+enum BatchLogits { kNoLogits, kLastLogits, kAllLogits };
+
+// One chunk of M tokens (device ids) at positions start..start+M-1 through every layer,
+// appending their K/V. kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the
+// last row's logits to m->logits (the decode step's buffer); kNoLogits: none (an inner chunk).
+int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint32_t* ids, BatchLogits logits) {
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -484,7 +501,7 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
     return QE_OK;
   };
   int rc;
-  HIP_TRY(qe::launch_embed_rows(m->embed, m->bids, M, H, m->bx, s));
+  HIP_TRY(qe::launch_embed_rows(m->embed, ids, M, H, m->bx, s));
   if (!skinny) HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
@@ -508,9 +525,9 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, bool all_l
     if ((rc = gemm_resadd(m->bh, I, w.w_down, I))) return rc;
   }
   // final norm + lm_head (cpu_inference.rs:175-178)
-  if (all_logits) {
+  if (logits == kAllLogits) {
     if ((rc = gemm(m->bx, H, m->final_norm, m->lm_head, V, H, m->blogits, V, qe::kGemmStore))) return rc;
-  } else {
+  } else if (logits == kLastLogits) {
     MatvecParams p{};
     p.eps = eps; p.w = m->lm_head; p.x = m->bx + size_t(M - 1) * H; p.nw = m->final_norm;
     p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
@@ -755,13 +772,11 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
     if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
   int rc = ensure_batch(model, chunk, 0);
   if (rc) return rc;
-  HIP_TRY(hipStreamSynchronize(model->stream));
+  if ((rc = upload_ids(model, ids, n))) return rc;
   for (uint64_t done = 0; done < n;) {
     const uint32_t M = uint32_t(std::min<uint64_t>(chunk, n - done));
-    // the previous chunk's kernels read bids: its copy waits for them on the same stream
-    HIP_TRY(hipMemcpyAsync(model->bids, ids + done, size_t(M) * 4, hipMemcpyHostToDevice, model->stream));
-    HIP_TRY(hipStreamSynchronize(model->stream));
-    if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), false))) return rc;
+    const BatchLogits lg = done + M == n && last_logits ? kLastLogits : kNoLogits;
+    if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), model->ids_dev + done, lg))) return rc;
     done += M;
   }
   if (last_logits) {
@@ -783,10 +798,8 @@ int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_p
     if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
   int rc = ensure_batch(model, uint32_t(k), uint32_t(k));
   if (rc) return rc;
-  HIP_TRY(hipStreamSynchronize(model->stream));
-  HIP_TRY(hipMemcpyAsync(model->bids, ids, size_t(k) * 4, hipMemcpyHostToDevice, model->stream));
-  HIP_TRY(hipStreamSynchronize(model->stream));
-  if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), true))) return rc;
+  if ((rc = upload_ids(model, ids, k))) return rc;
+  if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), model->ids_dev, kAllLogits))) return rc;
   HIP_TRY(hipMemcpyAsync(logits_out, model->blogits, size_t(k) * model->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
                          model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
