@@ -299,6 +299,35 @@ def prefill_bench(torch, qe, model, cfg, args):
     }
 
 
+def lookup_bench(qe, model, cfg, args):
+    """Prompt-lookup speculative decode (qe_decode_lookup) against plain greedy decode on the
+    decode workload: the 130-token prompt, then `steps` greedy tokens. Both must give the same
+    tokens; reports tok/s of each, verify passes and tokens per pass for k_max = 4 and 8."""
+    import numpy as np
+    P, K = args.prompt_len, args.steps
+    prompt = qe.random_prompt(PROMPT_SEED, P, cfg.vocab_size)
+
+    def run(fn):
+        best, out = float("inf"), None
+        for _ in range(3):
+            c = qe.KVCache(model, P + K + 1)
+            first = int(np.argmax(model.prefill(prompt, 0, c)))
+            t0 = time.perf_counter()
+            out = fn(first, c)
+            best = min(best, time.perf_counter() - t0)
+        return best, first, out
+
+    t_plain, first, (plain, _) = run(lambda f, c: model.decode(f, P, K, c))
+    res = {"metric": f"greedy decode tok/s with prompt-lookup drafts ({P}-token prompt, {K} steps)", "unit": "tok/s",
+           "plain_tok_s": round(K / t_plain, 1)}
+    for k_max in (4, 8):
+        t, _, (toks, st) = run(lambda f, c: model.decode_lookup(f, P, K, c, context=prompt, k_max=k_max, ngram=3))
+        passes = st["passes"] + st["single_steps"]
+        res[f"k{k_max}"] = {"tok_s": round(K / t, 1), "speedup": round(t_plain / t, 3), "same_tokens": toks == plain,
+                            "tokens_per_pass": round(K / passes, 3), **st}
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -313,10 +342,16 @@ def main():
     ap.add_argument("--json-out", default=None, help="also write a detailed result JSON here")
     ap.add_argument("--prefill-tokens", type=int, default=2048)
     ap.add_argument("--chunk", type=int, default=512)
-    ap.add_argument("--mode", choices=["decode", "matvec-sweep", "attention-sweep", "prefill"], default="decode",
+    ap.add_argument("--mode", choices=["decode", "matvec-sweep", "attention-sweep", "prefill", "lookup"],
+                    default="decode",
                     help="decode: the batch-1 decode benchmark (one JSON line); the sweeps time the isolated "
                          "matvec at every model shape or the isolated attention at 128..32768 positions")
     ap.add_argument("--repeats", type=int, default=1000, help="launches per shape in the sweeps")
+    ap.add_argument("--results", default=None,
+                    help="decode mode: also write engine_hip_<chip>_<prompt>.json and append to "
+                         "history_<chip>_<prompt>.jsonl here, in the reference harness's format")
+    ap.add_argument("--label", default="", help="label stored in the --results record")
+    ap.add_argument("--prompt-name", default="random130", help="prompt name in the --results file names")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -355,11 +390,15 @@ def main():
 
     t0 = time.time()
     model = qe.Model.load_model(ckpt)
-    log(f"loaded model in {time.time() - t0:.1f}s")
+    load_ms = (time.time() - t0) * 1e3
+    log(f"loaded model in {load_ms / 1e3:.1f}s")
     cfg = model.config()
-    if args.mode == "prefill":
-        result = dict(prefill_bench(torch, qe, model, cfg, args), n_gpus=1, data="synthetic",
-                      measured_ceiling_gbs=round(ceiling, 1))
+    if args.mode in ("prefill", "lookup"):
+        if args.mode == "prefill":
+            result = dict(prefill_bench(torch, qe, model, cfg, args), measured_ceiling_gbs=round(ceiling, 1))
+        else:
+            result = lookup_bench(qe, model, cfg, args)
+        result.update(n_gpus=1, data="synthetic")
         if args.json_out:
             with open(args.json_out, "w") as f:
                 json.dump(result, f, indent=1)
@@ -436,6 +475,7 @@ def main():
 
     # token parity against the oracle's committed run of the same workload
     parity = None
+    ref = []
     fx = os.path.join(ROOT, "tests", "golden", "qwen3_0_6b_decode.npz")
     if os.path.exists(fx) and P == PROMPT_LEN and kv_dtype == qe.QE_KV_F32:
         g = np.load(fx, allow_pickle=False)
@@ -500,6 +540,14 @@ def main():
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(ckpt, prompt)
+    if args.results:
+        import harness
+        rec = harness.engine_record(
+            engine="hip", label=args.label, chip=torch.cuda.get_device_name(0), prompt_name=args.prompt_name,
+            prompt_tokens=P, load_ms=load_ms, step_ms=[g * 1e3 for g in gaps], tokens=[first] + tokens,
+            weight_bytes_per_token=weight_bytes, total_bytes=bytes_total, peak_bw_gbs=SPEC_HBM_GBS,
+            ref_tokens=ref, repo_dir=ROOT)
+        log(f"wrote {harness.write_records(args.results, rec)}")
     if args.json_out:
         detail = dict(result, tokens=[first] + tokens, samples_ms=[round(g * 1e3, 4) for g in gaps])
         with open(args.json_out, "w") as f:

@@ -118,6 +118,32 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
  * decoding): appends their K/V and writes all k logit rows, logits_out [k][vocab_size]. */
 int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv,
               float* logits_out);
+/* qe_verify with each row's greedy token taken on the device (the decode step's argmax rule):
+ * tokens_out[i] = the token after ids[i]. */
+int qe_verify_greedy(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv,
+                     uint32_t* tokens_out);
+
+/* ---- speculative greedy decode by prompt lookup (no reference counterpart: README.md:109-111
+ *      names it as the next step). Same contract and same greedy tokens as qe_decode(first,
+ *      start_pos, steps): each pass drafts up to k_max tokens that followed an earlier
+ *      occurrence of the history's last g tokens (g = ngram .. 1; history = context[0..n_context)
+ *      + first + the tokens emitted so far; the most recent occurrence with k_max followers, else
+ *      the earliest) and checks them with one verify pass; drafts are
+ *      accepted while they equal the greedy token of the row before, and that pass adds one
+ *      greedy token of its own. With no draft a pass is one decode step. on_token gets every
+ *      token in order. k_max 1..63, ngram >= 1. ---- */
+typedef struct {
+  uint64_t passes;        /* verify passes */
+  uint64_t drafted;       /* draft tokens checked */
+  uint64_t accepted;      /* draft tokens accepted */
+  uint64_t single_steps;  /* decode steps taken when no draft was found */
+} qe_lookup_stats;
+int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                     uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
+                     qe_lookup_stats* stats);
+/* The draft rule alone (host code, no device): writes the draft qe_decode_lookup would check
+ * after history[0..n) (at most k_max tokens) to draft_out and returns its length. */
+uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, uint32_t k_max, uint32_t* draft_out);
 
 /* ---- per-stage kernel timing: runs `token` at `pos` like qe_forward, then times each stage
  *      of the step (qkv, attention, o_proj, gate_up, down, lm_head, argmax) as a graph of that

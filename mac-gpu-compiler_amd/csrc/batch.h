@@ -67,6 +67,8 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
 // key runs for a chunk of M tokens at positions start.. : enough workgroups to cover the chip,
 // at least two 32-position tiles per run
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv);
+// tokens[r] = greedy token of row r of logits [rows][V] (the decode step's argmax rule)
+hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, hipStream_t st);
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
                              hipStream_t st);
 

@@ -711,6 +711,43 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float* __restrict
   att[v * kHeadDim + d] = A / L;
 }
 
+// tokens[r] = the greedy token of logits row r by the reference's scan (bench.rs:98-103,
+// main.rs:37-42): the largest non-NaN value, lowest index on ties, and 0 when the row starts
+// with NaN. One workgroup per row; each thread's loads of a pass are issued together.
+__global__ __launch_bounds__(1024) void k_row_argmax(const float* __restrict__ logits, uint32_t V,
+                                                     uint32_t* __restrict__ tokens) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const float* x = logits + size_t(blockIdx.x) * V;
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  constexpr int U = 8;
+  for (uint32_t base = 0; base < V; base += 1024u * U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) v[u] = x[min(base + uint32_t(tid) + 1024u * u, V - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const uint32_t i = base + uint32_t(tid) + 1024u * u;
+      if (i < V && cand_better(v[u], i, bv, bi)) { bv = v[u]; bi = i; }  // NaN never wins
+    }
+  }
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    if (cand_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; w++)
+      if (cand_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    tokens[blockIdx.x] = (isnan(x[0]) || bi == 0xFFFFFFFFu) ? 0u : bi;
+  }
+}
+
 // x[m] = bf16 embedding row of ids[m] (cpu_inference.rs:109-111)
 __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__ table, const uint32_t* __restrict__ ids,
                                                     uint32_t M, uint32_t H, float* __restrict__ x) {
@@ -837,6 +874,12 @@ uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t
   const uint32_t wgs = n_kv * ceil_div(M, 64 / (n_heads / n_kv));
   uint32_t runs = std::min(ceil_div(1024, wgs), uint32_t(kBatchMaxRuns));
   return std::max(1u, std::min(runs, ceil_div(start + M, 128)));
+}
+
+hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, hipStream_t st) {
+  if (!rows || !V) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_row_argmax, dim3(rows), dim3(1024), 0, st, logits, V, tokens);
+  return hipGetLastError();
 }
 
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,

@@ -95,6 +95,7 @@ struct qe_model {
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
   float* bpart = nullptr;   // causal attention partials
   float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
+  uint32_t* btok = nullptr;  // greedy tokens of verify rows [kVerifyMaxTokens]
   float* blogits = nullptr;
   uint32_t* ids_dev = nullptr;  // the token ids of one qe_prefill_batch / qe_verify call
   uint64_t ids_cap = 0;
@@ -430,6 +431,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
                                                                      uint32_t(c.num_key_value_heads)));
   const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
   const size_t osplit = take(size_t(8) * cap * H * 4);  // gemm_splits returns at most 8
+  const size_t otok = take(size_t(kVerifyMaxTokens) * 4);
   HIP_TRY(hipStreamSynchronize(m->stream));
   if (m->batch_mem) HIP_TRY(hipFree(m->batch_mem));
   m->batch_mem = nullptr;
@@ -445,6 +447,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
   m->bpart = reinterpret_cast<float*>(m->batch_mem + opart);
   m->bsplit = reinterpret_cast<float*>(m->batch_mem + osplit);
+  m->btok = reinterpret_cast<uint32_t*>(m->batch_mem + otok);
   return QE_OK;
 }
 
@@ -788,14 +791,62 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
   return QE_OK;
 }
 
-int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv, float* logits_out) {
-  if (!model || !kv || !ids || !logits_out) return fail(QE_ERR_ARG, "null argument");
+namespace {
+
+int check_verify_args(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv) {
+  if (!model || !kv || !ids) return fail(QE_ERR_ARG, "null argument");
   if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
   if (k == 0 || k > kVerifyMaxTokens) return fail(QE_ERR_ARG, "k must be 1..%u", kVerifyMaxTokens);
   if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
   if (start_pos + k > kv->max_seq) return fail(QE_ERR_POS, "verify end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + k), (unsigned long long)kv->max_seq);
   for (uint64_t i = 0; i < k; i++)
     if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
+  return QE_OK;
+}
+
+// verify pass with the argmax on the device: tokens[i] = greedy token of row i
+int verify_greedy(qe_model* model, const uint32_t* ids, uint32_t k, uint64_t start_pos, qe_kv* kv, uint32_t* tokens) {
+  int rc = ensure_batch(model, k, k);
+  if (rc) return rc;
+  if ((rc = upload_ids(model, ids, k))) return rc;
+  if ((rc = enqueue_batch(model, kv, k, uint32_t(start_pos), model->ids_dev, kAllLogits))) return rc;
+  HIP_TRY(qe::launch_row_argmax(model->blogits, k, uint32_t(model->cfg.vocab_size), model->btok, model->stream));
+  // h_logits is pinned and idle here (no decode step is in flight on this stream)
+  HIP_TRY(hipMemcpyAsync(model->h_logits, model->btok, size_t(k) * 4, hipMemcpyDeviceToHost, model->stream));
+  HIP_TRY(hipStreamSynchronize(model->stream));
+  memcpy(tokens, model->h_logits, size_t(k) * 4);
+  kv->len = std::max<uint64_t>(kv->len, start_pos + k);
+  return QE_OK;
+}
+
+// Prompt lookup (Saxena, "Prompt Lookup Decoding", 2023): the draft is what followed an earlier
+// occurrence of the history's last g tokens, g from ngram down to 1, at most kd tokens: the most
+// recent occurrence followed by kd tokens, else the earliest (whose continuation is the longest);
+// empty when no suffix recurs.
+void lookup_draft(const std::vector<uint32_t>& h, uint32_t ngram, uint32_t kd, std::vector<uint32_t>& draft) {
+  draft.clear();
+  const size_t n = h.size();
+  if (kd == 0 || n < 2) return;
+  for (size_t g = std::min<size_t>(ngram, n - 1); g >= 1; g--) {
+    size_t earliest = n;
+    for (size_t i = n - g; i-- > 0;) {  // candidate starts, most recent first; i + g <= n - 1
+      if (!std::equal(h.begin() + i, h.begin() + i + g, h.end() - g)) continue;
+      earliest = i;
+      if (i + g + kd <= n) break;  // a full-length continuation
+    }
+    if (earliest < n) {
+      const size_t from = earliest + g, to = std::min(n, from + kd);
+      draft.assign(h.begin() + from, h.begin() + to);
+      return;
+    }
+  }
+}
+
+}  // namespace
+
+int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv, float* logits_out) {
+  if (!logits_out) return fail(QE_ERR_ARG, "null argument");
+  if (int rc = check_verify_args(model, ids, k, start_pos, kv)) return rc;
   int rc = ensure_batch(model, uint32_t(k), uint32_t(k));
   if (rc) return rc;
   if ((rc = upload_ids(model, ids, k))) return rc;
@@ -804,6 +855,78 @@ int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_p
                          model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
   kv->len = std::max<uint64_t>(kv->len, start_pos + k);
+  return QE_OK;
+}
+
+uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, uint32_t k_max, uint32_t* draft_out) {
+  if (!history || !draft_out) return 0;
+  std::vector<uint32_t> h(history, history + n), d;
+  lookup_draft(h, ngram, k_max, d);
+  std::copy(d.begin(), d.end(), draft_out);
+  return d.size();
+}
+
+int qe_verify_greedy(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_pos, qe_kv* kv,
+                     uint32_t* tokens_out) {
+  if (!tokens_out) return fail(QE_ERR_ARG, "null argument");
+  if (int rc = check_verify_args(model, ids, k, start_pos, kv)) return rc;
+  return verify_greedy(model, ids, uint32_t(k), start_pos, kv, tokens_out);
+}
+
+int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                     uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
+                     qe_lookup_stats* stats) {
+  if (!model || !kv || (!context && n_context)) return fail(QE_ERR_ARG, "null argument");
+  if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
+  if (k_max == 0 || k_max >= kVerifyMaxTokens) return fail(QE_ERR_ARG, "k_max must be 1..%u", kVerifyMaxTokens - 1);
+  if (ngram == 0) return fail(QE_ERR_ARG, "ngram must be >= 1");
+  if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
+  if (start_pos + steps > kv->max_seq) return fail(QE_ERR_POS, "decode end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + steps), (unsigned long long)kv->max_seq);
+  if (first >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab", first);
+  for (uint64_t i = 0; i < n_context; i++)
+    if (context[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "context token %u at %llu >= vocab", context[i], (unsigned long long)i);
+  qe_lookup_stats st{};
+  std::vector<uint32_t> h(context, context + n_context), draft, ids, got(kVerifyMaxTokens);
+  h.push_back(first);
+  uint32_t cur = first;
+  uint64_t pos = start_pos, emitted = 0;
+  int rc;
+  while (emitted < steps) {
+    // a pass emits accepted drafts + 1 token, so it never runs past `steps`
+    lookup_draft(h, ngram, uint32_t(std::min<uint64_t>(k_max, steps - emitted - 1)), draft);
+    if (draft.empty()) {  // nothing to verify: one decode step
+      uint32_t tok = 0;
+      auto keep = [](void* u, uint32_t t) { *static_cast<uint32_t*>(u) = t; };
+      if ((rc = qe_decode(model, cur, pos, 1, kv, keep, &tok, nullptr))) return rc;
+      st.single_steps++;
+      h.push_back(tok);
+      if (on_token) on_token(user, tok);
+      cur = tok;
+      pos++;
+      emitted++;
+      continue;
+    }
+    ids.assign(1, cur);
+    ids.insert(ids.end(), draft.begin(), draft.end());
+    if ((rc = verify_greedy(model, ids.data(), uint32_t(ids.size()), pos, kv, got.data()))) return rc;
+    // row i is the greedy token after ids[i]: drafts are accepted while they equal it, and the
+    // row after the last accepted one adds a token of its own
+    size_t j = 0;
+    while (j < draft.size() && got[j] == draft[j]) j++;
+    st.passes++;
+    st.drafted += draft.size();
+    st.accepted += j;
+    for (size_t i = 0; i <= j; i++) {
+      const uint32_t tok = i < j ? draft[i] : got[j];
+      h.push_back(tok);
+      if (on_token) on_token(user, tok);
+    }
+    cur = got[j];
+    pos += j + 1;
+    emitted += j + 1;
+  }
+  kv->len = start_pos + steps;  // positions past the accepted tokens hold rejected drafts
+  if (stats) *stats = st;
   return QE_OK;
 }
 

@@ -93,6 +93,20 @@ QWEN3_0_6B = Config(1024, 3072, 28, 16, 8, 128, 151936, 1e-6, 1e6, 151645)
 
 ON_TOKEN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32)
 
+
+def lookup_draft(history, ngram: int = 3, k_max: int = 4) -> list:
+    """The prompt-lookup draft after `history` (qe_lookup_draft; host code, no device)."""
+    h = np.ascontiguousarray(history, dtype=np.uint32)
+    out = np.zeros(max(int(k_max), 1), dtype=np.uint32)
+    u32p = ctypes.POINTER(ctypes.c_uint32)
+    n = lib().qe_lookup_draft(h.ctypes.data_as(u32p), len(h), int(ngram), int(k_max), out.ctypes.data_as(u32p))
+    return [int(t) for t in out[:n]]
+
+
+class _LookupStats(ctypes.Structure):
+    _fields_ = [("passes", ctypes.c_uint64), ("drafted", ctypes.c_uint64), ("accepted", ctypes.c_uint64),
+                ("single_steps", ctypes.c_uint64)]
+
 _lib = None
 
 
@@ -149,6 +163,10 @@ def lib() -> ctypes.CDLL:
         "qe_decode": (i32, [vp, u32, u64, u64, vp, ON_TOKEN, vp, f32p]),
         "qe_prefill_batch": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, u32, f32p]),
         "qe_verify": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, f32p]),
+        "qe_verify_greedy": (i32, [vp, ctypes.POINTER(u32), u64, u64, vp, ctypes.POINTER(u32)]),
+        "qe_lookup_draft": (u64, [ctypes.POINTER(u32), u64, u32, u32, ctypes.POINTER(u32)]),
+        "qe_decode_lookup": (i32, [vp, ctypes.POINTER(u32), u64, u32, u64, u64, vp, u32, u32, ON_TOKEN, vp,
+                                   ctypes.POINTER(_LookupStats)]),
         "qe_op_gemm_bf16": (i32, [vp, vp, vp, u64, u64, u64, vp]),
         "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
         "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
@@ -242,6 +260,36 @@ class Model:
         _check(lib().qe_verify(self._h, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids),
                                int(start_pos), cache._h, _fptr(out)))
         return out
+
+    def verify_greedy(self, ids, start_pos: int, cache: "KVCache") -> np.ndarray:
+        """k tokens in one pass with the argmax on the device (qe_verify_greedy): the greedy token
+        after each of them, uint32 [k]."""
+        ids = np.ascontiguousarray(ids, dtype=np.uint32)
+        out = np.empty(len(ids), dtype=np.uint32)
+        u32p = ctypes.POINTER(ctypes.c_uint32)
+        _check(lib().qe_verify_greedy(self._h, ids.ctypes.data_as(u32p), len(ids), int(start_pos), cache._h,
+                                      out.ctypes.data_as(u32p)))
+        return out
+
+    def decode_lookup(self, first: int, start_pos: int, steps: int, cache: "KVCache", context=(),
+                      k_max: int = 4, ngram: int = 3, on_token: Optional[Callable[[int], None]] = None):
+        """Greedy decode with prompt-lookup drafts checked by verify passes (qe_decode_lookup): the
+        same tokens as decode(). context: the ids before `first` (the prompt). Returns (tokens,
+        stats) with stats = {passes, drafted, accepted, single_steps}."""
+        toks = []
+
+        def cb(_user, tok):
+            toks.append(int(tok))
+            if on_token is not None:
+                on_token(int(tok))
+
+        ccb = ON_TOKEN(cb)
+        ctx = np.ascontiguousarray(context, dtype=np.uint32)
+        st = _LookupStats()
+        _check(lib().qe_decode_lookup(self._h, ctx.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ctx),
+                                      int(first), int(start_pos), int(steps), cache._h, int(k_max), int(ngram), ccb,
+                                      None, ctypes.byref(st)))
+        return toks, {f: int(getattr(st, f)) for f, _ in _LookupStats._fields_}
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",
                on_token: Optional[Callable[[int], None]] = None, want_logits: bool = False):

@@ -1,0 +1,70 @@
+"""Speculative greedy decode by prompt lookup (qe_decode_lookup) through the C ABI: it must emit
+exactly the greedy tokens of token-by-token decoding (the oracle's on the tiny model, the
+committed decode fixture on the real one) and leave the cache as qe_decode would."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import qe
+from conftest import DECODE_STEPS, PROMPT_LEN, PROMPT_SEED, TINY
+
+pytestmark = pytest.mark.gpu
+
+
+def test_verify_greedy_is_the_argmax_of_verify(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    prefix = qe.random_prompt(51, 30, TINY.vocab_size)
+    draft = qe.random_prompt(53, 9, TINY.vocab_size)
+    c = qe.KVCache(m, 48)
+    m.prefill(prefix, 0, c, want_logits=False)
+    rows = m.verify(draft, 30, c)
+    toks = m.verify_greedy(draft, 30, c)
+    assert [int(t) for t in toks] == [oracle.argmax(r) for r in rows]
+
+
+@pytest.mark.parametrize("k_max,ngram", [(1, 1), (4, 3), (8, 2)])
+def test_tiny_lookup_decode_matches_oracle(gpu, tiny_ckpt, k_max, ngram):
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    # a prompt that repeats, so drafts exist and some are rejected
+    base = [int(t) for t in qe.random_prompt(57, 12, TINY.vocab_size)]
+    prompt = np.array(base * 3 + base[:5], dtype=np.uint32)
+    P, steps = len(prompt), 40
+    c = qe.KVCache(m, P + steps + 8)
+    logits = m.prefill(prompt, 0, c)
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        ref = om.forward(int(tok), pos, oc)
+    first = oracle.argmax(ref)
+    assert oracle.argmax(logits) == first
+    got, st = m.decode_lookup(first, P, steps, c, context=prompt, k_max=k_max, ngram=ngram)
+    want, tok = [], first
+    for i in range(steps):
+        tok = oracle.argmax(om.forward(tok, P + i, oc))
+        want.append(tok)
+    assert got == want
+    assert st["accepted"] <= st["drafted"] and st["passes"] + st["single_steps"] >= 1
+    assert st["passes"] + st["single_steps"] + st["accepted"] == steps
+    assert len(c) == P + steps
+    # the cache continues like the oracle's after the rejected drafts
+    more, _ = m.decode(got[-1], P + steps, 5, c)
+    for i in range(5):
+        tok = oracle.argmax(om.forward(tok, P + steps + i, oc))
+        assert more[i] == tok
+
+
+@pytest.mark.slow
+def test_real_lookup_decode_matches_fixture(gpu, real_ckpt):
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qwen3_0_6b_decode.npz"),
+                allow_pickle=False)
+    m = qe.Model.load_model(real_ckpt)
+    prompt = qe.random_prompt(PROMPT_SEED, PROMPT_LEN, m.config().vocab_size)
+    c = qe.KVCache(m, PROMPT_LEN + DECODE_STEPS + 1)
+    first = oracle.argmax(m.prefill(prompt, 0, c))
+    toks, st = m.decode_lookup(first, PROMPT_LEN, DECODE_STEPS, c, context=prompt, k_max=4, ngram=3)
+    ref = [int(t) for t in g["tokens"]]
+    got = [first] + toks
+    assert got == ref, f"diverges at {next(i for i in range(len(ref)) if got[i] != ref[i])}"
+    print(f"lookup decode: {st}, {DECODE_STEPS / (st['passes'] + st['single_steps']):.2f} tokens per pass")
