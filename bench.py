@@ -178,7 +178,10 @@ def sweep_matvec(torch, qe, ceiling: float, repeats: int):
     every launch streams its weights from HBM (bench.rs-style bytes: out*in*2 + in*4 + out*4)."""
     rows = []
     shapes = [(1024, 2048), (1024, 1024), (2048, 1024), (1024, 3072), (3072, 1024), (1024, 4096), (1024, 6144), (1024, 151936)]
-    for cin, cout in shapes:
+    # one GPU's share of each projection under 8-way tensor parallelism by KV head: q 2 heads,
+    # k / v 1 head, o 2 heads in, gate|up 384 + 384 rows, down 384 in, lm_head 18,992 rows
+    shard = [(1024, 256), (1024, 128), (256, 1024), (1024, 768), (384, 1024), (1024, 18992)]
+    for cin, cout in shapes + shard:
         wbytes = cout * cin * 2
         copies = max(2, -(-2 * MALL_BYTES // wbytes))
         W = (torch.randn(copies, cout, cin, device="cuda") * 0.02).to(torch.bfloat16)
@@ -188,7 +191,8 @@ def sweep_matvec(torch, qe, ceiling: float, repeats: int):
                                                               stream=torch.cuda.current_stream()), repeats)
         b = wbytes + cin * 4 + cout * 4
         gbs = b / (us * 1e-6) / 1e9
-        rows.append({"in": cin, "out": cout, "us": round(us, 3), "bytes": b, "gb_s": round(gbs, 1),
+        rows.append({"in": cin, "out": cout, "tp8_shard": (cin, cout) in shard, "us": round(us, 3), "bytes": b,
+                     "gb_s": round(gbs, 1),
                      "frac_of_measured": round(gbs / ceiling, 4), "frac_of_spec": round(gbs / SPEC_HBM_GBS, 4),
                      "w_copies": copies})
         log(f"matvec {cin:5d} -> {cout:6d}: {us:8.3f} us  {gbs:7.1f} GB/s ({gbs / ceiling:.1%} of measured)")

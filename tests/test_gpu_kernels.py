@@ -10,7 +10,9 @@ pytestmark = pytest.mark.gpu
 
 # (rows, cols) = (out, in): q, k/v, o, gate/up, down, lm_head, fused q|k|v, fused gate|up
 SHAPES = [(2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072), (151936, 1024),
-          (4096, 1024), (6144, 1024), (7, 8), (65, 520), (33, 4104)]
+          (4096, 1024), (6144, 1024), (7, 8), (65, 520), (33, 4104),
+          # one GPU's share under 8-way tensor parallelism (q, k/v, o, gate|up, down, lm_head)
+          (256, 1024), (128, 1024), (1024, 256), (768, 1024), (1024, 384), (18992, 1024)]
 
 
 def bf16_rne(x: np.ndarray) -> np.ndarray:
