@@ -112,8 +112,56 @@ __device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16>& X, int i) {
   }
 }
 
+__device__ __forceinline__ uint32_t xcc_id() {
+  uint32_t v;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(v));
+  return v & 0xf;
+}
+
+// Prefetch workgroup q (slot q / 8 of the XCD it runs on; consecutive q land on consecutive
+// XCDs) loads the chunks of the consumer workgroups j = x + 8 (slot + slots k) of each target,
+// x = this XCD, so they sit in the L2 those workgroups will read. All of a thread's loads are
+// issued before any is used; the values only feed a never-taken store.
+__device__ void l2_prefetch(const AttnParams& p, uint32_t q) {
+  constexpr int KMAX = 16;
+  const uint32_t x = xcc_id(), slot = q / 8, ns = p.pf_slots, tid = threadIdx.x;
+  uint32_t cnt[kMaxPrefetch], tot = 0;
+#pragma unroll
+  for (int t = 0; t < kMaxPrefetch; t++) {
+    const uint32_t j0 = x + 8 * slot;
+    cnt[t] = p.pf[t].w && j0 < p.pf[t].n_cwg ? ceil_div(p.pf[t].n_cwg - j0, 8 * ns) : 0;
+    tot += cnt[t] * p.pf[t].cw_chunks;
+  }
+  if (tot == 0) return;
+  uint4 v[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) {
+    uint32_t i = min(tid + 256u * k, tot - 1), t = 0;
+    if (i >= cnt[0] * p.pf[0].cw_chunks) {
+      i -= cnt[0] * p.pf[0].cw_chunks;
+      t = 1;
+    }
+    const L2Prefetch& f = p.pf[t];
+    const uint32_t jj = i / f.cw_chunks, c = i - jj * f.cw_chunks;
+    const uint32_t j = x + 8 * (slot + ns * jj);
+    v[k] = reinterpret_cast<const uint4*>(f.w)[min(j * f.cw_chunks + c, f.n_chunks - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint32_t h = 0;
+#pragma unroll
+  for (int k = 0; k < KMAX; k++) h ^= v[k].x ^ v[k].w;
+  if (ns == 0xFFFFFFFFu && h == 0x5A5A5A5Au) *p.err = h;  // never: keeps the loads
+}
+
 template <int G, bool KV_BF16, bool DECODE>
 __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk) {
+  if constexpr (DECODE) {
+    if (blockIdx.y >= p.splits) {  // a prefetch workgroup (whole workgroup, before any load)
+      const uint32_t q = (blockIdx.y - p.splits) * gridDim.x + blockIdx.x;
+      if (q < 8 * p.pf_slots) l2_prefetch(p, q);
+      return;
+    }
+  }
   // DECODE: q/k RMSNorm + RoPE on the raw q|k|v rows, append of the new K/V row, positions
   // 0..state->pos; otherwise (the isolated op) q is final and positions are 0..n_pos_fixed-1
   constexpr int D = kHeadDim, T = 64, NR = DECODE ? G + 2 : G, RPW = (NR + 3) / 4;
@@ -166,8 +214,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     const bool bad = pos >= p.max_seq;
     if (bad && g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
     n = bad ? 0u : pos + 1;
-    // the n positions in gridDim.y runs of a whole number of tiles
-    run = T * ceil_div(max(n, 1u), T * gridDim.y);
+    // the n positions in p.splits runs of a whole number of tiles
+    run = T * ceil_div(max(n, 1u), T * p.splits);
     t0 = s * run;
     owns_new = !bad && pos >= t0 && pos < t0 + run;
     if (run != T) load_tile<KV_BF16>(A, p, head_base, t0, tid);  // longer runs start elsewhere
@@ -178,7 +226,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     t0 = t0_first;
   }
   const uint32_t t1 = min(n, t0 + run);
-  float* part = p.partial + (size_t(g) * gridDim.y + s) * G * kPartStride;
+  float* part = p.partial + (size_t(g) * p.splits + s) * G * kPartStride;
 
   // ---- q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215) ----
 #pragma unroll
@@ -371,9 +419,14 @@ bool attn_args_ok(const AttnParams& p, uint32_t splits, uint32_t chunk, uint32_t
 }
 
 template <bool DECODE>
-hipError_t launch_split(const AttnParams& p, uint32_t splits, uint32_t chunk, hipStream_t s) {
-  const uint32_t G = p.n_heads / p.n_kv;
-  dim3 grid(p.n_kv, splits);
+hipError_t launch_split(const AttnParams& pin, uint32_t splits, uint32_t chunk, hipStream_t s) {
+  const uint32_t G = pin.n_heads / pin.n_kv;
+  AttnParams p = pin;
+  p.splits = splits;
+  if (!DECODE) p.pf_slots = 0;
+  // prefetch workgroups: whole rows of n_kv after the attention's `splits` rows (dispatched
+  // after them: ahead of them, they delay the attention more than they gain)
+  const dim3 grid(p.n_kv, splits + ceil_div(8 * p.pf_slots, p.n_kv));
 #define QE_ATT(GG)                                                                                          \
   if (G == GG) {                                                                                            \
     if (p.kv_bf16) hipLaunchKernelGGL((k_attn_split<GG, true, DECODE>), grid, dim3(256), 0, s, p, chunk);   \

@@ -89,6 +89,8 @@ struct qe_model {
   float* h_logits = nullptr;
   uint32_t* h_small = nullptr;  // [0..3] state staging, [4] error word
   uint64_t weight_bytes = 0;
+  // decode attention launches also load the next weights into L2 (QE_L2_PREFETCH=0 turns it off)
+  bool l2_prefetch = true;
   // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
@@ -183,6 +185,7 @@ int qe_model_load(const char* path, qe_model** out) {
   int rc = m->ckpt.open(path, err);
   if (rc != QE_OK) return fail(rc, "%s", err.c_str());
   m->cfg = m->ckpt.config();
+  if (const char* pf = getenv("QE_L2_PREFETCH")) m->l2_prefetch = strcmp(pf, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
   const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
@@ -382,6 +385,13 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.max_seq = uint32_t(kv->max_seq); a.eps = c.rms_norm_eps; a.scale = 1.0f / sqrtf(float(D));
     a.kv_bf16 = kv->dtype == QE_KV_BF16;
+    if (m->l2_prefetch) {
+      // the attention is latency-bound: extra workgroups of its launch pull this layer's o_proj
+      // and gate/up weights into the L2 of the XCDs whose workgroups will read them
+      a.pf[0] = qe::l2_prefetch_target(w.w_o, H, QD, qe::kAttnMerge, qe::kResAdd);
+      a.pf[1] = qe::l2_prefetch_target(w.w_gu, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
+    }
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
     if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, s));

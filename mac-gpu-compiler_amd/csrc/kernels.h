@@ -56,6 +56,18 @@ struct MatvecParams {
 enum Prologue { kCopy = 0, kNorm = 1, kEmbedNorm = 2, kAttnMerge = 3 };
 enum Epilogue { kStore = 0, kResAdd = 1, kSiluPair = 2, kLogits = 3 };
 
+// Weight chunks that a later kernel of the step reads, loaded ahead into the L2 of the XCD that
+// will read them. Consumer workgroup j of launch_matvec_wide reads the 16-byte chunks
+// [j * cw_chunks, (j + 1) * cw_chunks) of its matrix and runs on XCD j % 8 (workgroups are
+// dispatched round-robin over the 8 XCDs).
+struct L2Prefetch {
+  const uint16_t* w;   // bf16 matrix
+  uint32_t n_chunks;   // 16-byte chunks in the matrix
+  uint32_t cw_chunks;  // chunks one consumer workgroup reads
+  uint32_t n_cwg;      // consumer workgroups
+};
+constexpr int kMaxPrefetch = 2;
+
 struct AttnParams {
   const float* qkv;        // raw projections [n_heads*D | n_kv*D | n_kv*D]
   const uint16_t* q_norm;  // bf16 [D]
@@ -71,6 +83,11 @@ struct AttnParams {
   float eps, scale;
   int kv_bf16;
   uint32_t n_pos_fixed;    // isolated op: attend positions 0..n_pos_fixed-1 with a final q
+  uint32_t splits;         // runs per KV head (set by the launchers)
+  // decode only: 8 * pf_slots extra workgroups load these matrices into L2 while the attention
+  // runs (pf_slots = 0: none)
+  L2Prefetch pf[kMaxPrefetch];
+  uint32_t pf_slots;
 };
 
 // --- launch wrappers (kernels.hip) ---
@@ -86,6 +103,10 @@ constexpr int kAttnMaxMergeSplits = 16;
 // one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
 constexpr int kPartStride = 4 + kHeadDim;
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, hipStream_t s);
+// The L2 prefetch of a matrix that launch_matvec_wide(rows x cols, prologue, epilogue) will read.
+L2Prefetch l2_prefetch_target(const uint16_t* w, uint32_t rows, uint32_t cols, int prologue, int epilogue);
+// Prefetch workgroups per XCD for these targets (each loads at most 16 chunks per thread).
+uint32_t l2_prefetch_slots(const L2Prefetch* pf, int n);
 // The isolated op: final q [n_heads][D], complete K/V [n_kv][max_seq][D] (f32), positions
 // 0..n_pos_fixed-1 in `splits` runs (<= kAttnMaxSplits), partials merged into out [n_heads][D].
 hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);

@@ -12,6 +12,7 @@
 // All arithmetic is f32 with bf16 weights widened exactly (u16 << 16).
 #include "kernels.h"
 
+#include <algorithm>
 #include <cmath>
 
 #include "device_common.h"
@@ -527,6 +528,32 @@ hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipS
   if (prologue == kNorm && epilogue == kSiluPair) return launch_mv_cpl<kNorm, kSiluPair>(p, s);
   if (prologue == kNorm && epilogue == kLogits) return launch_mv_cpl<kNorm, kLogits>(p, s);
   return hipErrorInvalidValue;
+}
+
+// rows one workgroup of launch_matvec_wide covers: (256 / TPR) row groups of RR rows, with the
+// TPR / CPT / RR that launch_wide_cols and launch_merge_cols pick for this shape
+uint32_t matvec_wide_rows_per_block(uint32_t cols, int prologue, int epilogue) {
+  const uint32_t nch = cols / 8;
+  if (prologue == kAttnMerge) return nch <= 128 ? 8 : 4;  // RR 4 with TPR 128, else TPR 256
+  const bool silu = epilogue == kSiluPair;
+  if (nch <= 64) return 4 * 2;                // TPR 64, CPT 1: RR 2
+  if (nch <= 128) return 2 * 2;               // TPR 128, CPT 1: RR 2
+  if (nch <= 256) return silu ? 2 : 1;        // TPR 256
+  if (nch == 384) return 2 * (silu ? 2 : 1);  // TPR 128, CPT 3
+  return silu ? 2 : 1;                        // TPR 256, CPT 2
+}
+
+L2Prefetch l2_prefetch_target(const uint16_t* w, uint32_t rows, uint32_t cols, int prologue, int epilogue) {
+  const uint32_t rpb = matvec_wide_rows_per_block(cols, prologue, epilogue);
+  return L2Prefetch{w, rows * (cols / 8), rpb * (cols / 8), ceil_div(rows, rpb)};
+}
+
+uint32_t l2_prefetch_slots(const L2Prefetch* pf, int n) {
+  uint64_t chunks = 0;
+  for (int i = 0; i < n; i++) chunks += pf[i].w ? pf[i].n_chunks : 0;
+  if (!chunks) return 0;
+  // 8 XCDs x slots workgroups x 256 threads x 16 chunks, with headroom for uneven splits
+  return uint32_t(std::min<uint64_t>(64, ceil_div(uint32_t(chunks), 8u * 256u * 12u)));
 }
 
 hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue, hipStream_t s) {
