@@ -265,6 +265,17 @@ def prefill_bench(torch, qe, model, cfg, args):
         model.prefill_batch(ids, 0, cache, chunk=chunk, want_logits=False)
         torch.cuda.synchronize()
         best = min(best, time.perf_counter() - t0)
+    # the same prompt in one chunk of n tokens (the largest chunk qe_prefill_batch takes)
+    best_one = float("inf")
+    if n <= 2048:
+        model.prefill_batch(ids, 0, qe.KVCache(model, n + 8), chunk=n, want_logits=False)
+        for _ in range(3):
+            cache = qe.KVCache(model, n + 8)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            model.prefill_batch(ids, 0, cache, chunk=n, want_logits=False)
+            torch.cuda.synchronize()
+            best_one = min(best_one, time.perf_counter() - t0)
     proj = L * ((QD + 2 * KD) * H + H * QD + 2 * I * H + H * I)
     gemm_flop = 2.0 * n * proj
     attn_flop = 8192.0 * sum(p + 1 for p in range(n)) * L
@@ -297,6 +308,8 @@ def prefill_bench(torch, qe, model, cfg, args):
         "mfma_tflops_issued": round(mfma_flop / best / 1e12, 2),
         "mfma_peak_tflops": 2500.0,
         "hipblaslt_bf16_tflops_same_shape": round(lib_tflops, 1),
+        "one_chunk_ms": round(best_one * 1e3, 3) if best_one < float("inf") else None,
+        "one_chunk_tok_s": round(n / best_one, 1) if best_one < float("inf") else None,
         "verify_k4_ms": round(verify_ms, 3),
         "forward_1_ms": round(forward_ms, 3),
         "verify_k4_tokens_per_s_if_all_accepted": round(4 / verify_ms * 1e3, 1),

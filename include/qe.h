@@ -107,7 +107,7 @@ int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t step
 /* ---- multi-token forward on the matrix cores (no reference counterpart: the reference's
  *      prompt loop calls forward once per token, bench.rs:174-176) ---- */
 /* Chunked prefill: runs ids[0..n) at positions start_pos.. through the model in chunks of up to
- * `chunk` tokens (0 = 512, at most 512): one bf16 MFMA GEMM per projection and chunk, f32
+ * `chunk` tokens (0 = 512, at most 2048): one bf16 MFMA GEMM per projection and chunk, f32
  * activations split into two bf16 halves (about 16 mantissa bits), causal attention over the
  * cache and the chunk. Appends the K/V of every position and writes the last token's logits
  * (nullable). Same position contract as qe_prefill; logits agree with it within 1e-2, not bit for

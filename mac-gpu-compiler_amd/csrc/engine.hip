@@ -58,7 +58,8 @@ struct Layer {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-constexpr uint32_t kBatchMaxChunk = 512;   // tokens per chunk of qe_prefill_batch
+constexpr uint32_t kBatchDefaultChunk = 512;  // tokens per chunk of qe_prefill_batch (chunk = 0)
+constexpr uint32_t kBatchMaxChunk = 2048;
 constexpr uint32_t kVerifyMaxTokens = 64;  // tokens of one qe_verify call
 
 }  // namespace
@@ -777,7 +778,7 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
   if (!model || !kv || (!ids && n)) return fail(QE_ERR_ARG, "null argument");
   if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
   if (n == 0) return QE_OK;
-  if (chunk == 0) chunk = kBatchMaxChunk;
+  if (chunk == 0) chunk = kBatchDefaultChunk;
   if (chunk > kBatchMaxChunk) return fail(QE_ERR_ARG, "chunk %u above %u", chunk, kBatchMaxChunk);
   if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
   if (start_pos + n > kv->max_seq) return fail(QE_ERR_POS, "prompt end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + n), (unsigned long long)kv->max_seq);

@@ -47,7 +47,7 @@ def test_gemm_matches_float64(gpu, m, n, k):
     assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) / bound)}"
 
 
-@pytest.mark.parametrize("n_prompt,chunk", [(1, 0), (100, 32), (300, 0), (513, 512)])
+@pytest.mark.parametrize("n_prompt,chunk", [(1, 0), (100, 32), (300, 0), (513, 512), (700, 2048)])
 def test_tiny_prefill_batch_matches_oracle(gpu, tiny_ckpt, n_prompt, chunk):
     m = qe.Model.load_model(tiny_ckpt)
     om = oracle.Model(tiny_ckpt)
@@ -118,7 +118,7 @@ def test_batch_argument_errors(gpu, tiny_ckpt):
         m.prefill_batch(np.arange(9, dtype=np.uint32), 0, cache)  # past max_seq
     assert e.value.code == qe.QE_ERR_POS
     with pytest.raises(qe.QeError) as e:
-        m.prefill_batch(np.arange(4, dtype=np.uint32), 0, cache, chunk=513)
+        m.prefill_batch(np.arange(4, dtype=np.uint32), 0, cache, chunk=2049)
     assert e.value.code == qe.QE_ERR_ARG
     with pytest.raises(qe.QeError) as e:
         m.verify(np.zeros(65, dtype=np.uint32), 0, qe.KVCache(m, 80))
