@@ -111,6 +111,21 @@ def test_tiny_prefill_batch_bf16_kv_matches_sequential(gpu, tiny_ckpt, n_prompt,
         assert float(np.max(np.abs(rows[i] - ref))) < 5e-3, f"verify row {i}"
 
 
+def test_tiny_prefill_batch_continues_a_cache(gpu, tiny_ckpt):
+    """chunked prefill from start_pos > 0 onto a cache filled token by token"""
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    prompt = qe.random_prompt(61, 150, TINY.vocab_size)
+    cache = qe.KVCache(m, 160)
+    m.prefill(prompt[:50], 0, cache, want_logits=False)
+    got = m.prefill_batch(prompt[50:], 50, cache, chunk=64)
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        ref = om.forward(int(tok), pos, oc)
+    assert float(np.max(np.abs(got - ref))) < 1e-3
+    assert len(cache) == 150
+
+
 def test_batch_argument_errors(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 8)

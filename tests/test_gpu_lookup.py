@@ -68,3 +68,25 @@ def test_real_lookup_decode_matches_fixture(gpu, real_ckpt):
     got = [first] + toks
     assert got == ref, f"diverges at {next(i for i in range(len(ref)) if got[i] != ref[i])}"
     print(f"lookup decode: {st}, {DECODE_STEPS / (st['passes'] + st['single_steps']):.2f} tokens per pass")
+
+
+def test_lookup_argument_errors(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    c = qe.KVCache(m, 16)
+    m.prefill(np.arange(4, dtype=np.uint32), 0, c, want_logits=False)
+    for kw, code in (({"k_max": 0}, qe.QE_ERR_ARG), ({"k_max": 64}, qe.QE_ERR_ARG), ({"ngram": 0}, qe.QE_ERR_ARG)):
+        with pytest.raises(qe.QeError) as e:
+            m.decode_lookup(1, 4, 4, c, context=[0, 1, 2, 3], **kw)
+        assert e.value.code == code
+    with pytest.raises(qe.QeError) as e:
+        m.decode_lookup(1, 5, 4, c)  # nothing cached at position 4
+    assert e.value.code == qe.QE_ERR_POS
+    with pytest.raises(qe.QeError) as e:
+        m.decode_lookup(1, 4, 13, c)  # runs past max_seq
+    assert e.value.code == qe.QE_ERR_POS
+    with pytest.raises(qe.QeError) as e:
+        m.decode_lookup(TINY.vocab_size, 4, 2, c)
+    assert e.value.code == qe.QE_ERR_ARG
+    with pytest.raises(qe.QeError) as e:
+        m.verify_greedy(np.zeros(65, dtype=np.uint32), 0, qe.KVCache(m, 80))
+    assert e.value.code == qe.QE_ERR_ARG
