@@ -475,7 +475,7 @@ def main():
     del wc
     el = 2 if kv_dtype == qe.QE_KV_BF16 else 4
     mean_pos = sum(prof_positions) / n_prof
-    stage_bytes = qe.stage_bytes(cfg, mean_pos, el)
+    stage_bytes = qe.stage_bytes(cfg, mean_pos, el, prefetch=qe.l2_prefetch_enabled())
     kernel_table = {}
     for name, (durs, per_step) in stages.items():
         mean_us = sum(durs) / len(durs)

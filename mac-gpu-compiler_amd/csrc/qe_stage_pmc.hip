@@ -2,9 +2,10 @@
 // eight times per stage with the weights rotating over four copies (past the 4 MB L2), after a
 // 1 GiB device copy of known traffic. Meant to run under `rocprofv3 --pmc FETCH_SIZE` and
 // `--pmc WRITE_SIZE`: the counters per dispatch, scaled by the copy's, give each stage's HBM
-// bytes per launch. Stage order and kernels are those of the engine's decode step.
+// bytes per launch. Stage order and kernels are those of the engine's decode step, including
+// the attention launch's L2 prefetch of the layer's o_proj and gate/up weights.
 //
-//   qe_stage_pmc [--pos P]     (attention attends positions 0..P, default 193)
+//   qe_stage_pmc [--pos P] [--no-prefetch]   (attention attends positions 0..P, default 193)
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -51,8 +52,10 @@ T* dalloc(size_t n) {
 
 int main(int argc, char** argv) {
   uint32_t pos = 193;
+  bool prefetch = true;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
+    else if (!strcmp(argv[i], "--no-prefetch")) prefetch = false;
   }
   const uint32_t H = 1024, I = 3072, V = 151936, NH = 16, NKV = 8, D = qe::kHeadDim, G = NH / NKV;
   const uint32_t QD = NH * D, KD = NKV * D, max_seq = 258;
@@ -123,6 +126,11 @@ int main(int argc, char** argv) {
     a.qkv = qkv; a.q_norm = gains; a.k_norm = gains; a.rope = rope; a.rope_cur = rope_cur;
     a.k_cache = kc; a.v_cache = vc; a.partial = part; a.state = st; a.err = err;
     a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f;
+    if (prefetch) {
+      a.pf[0] = qe::l2_prefetch_target(Wc + n_qkv, H, QD, qe::kAttnMerge, qe::kResAdd);
+      a.pf[1] = qe::l2_prefetch_target(Wc + n_qkv + n_o, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
+    }
     CK(qe::launch_attention_split(a, splits, s));
     // merge + o_proj + residual
     p = qe::MatvecParams{};
@@ -148,7 +156,7 @@ int main(int argc, char** argv) {
   }
   uint32_t e = 0;
   CK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
-  std::printf("qe_stage_pmc: 8 x (qkv, attention at pos %u, o_proj, gate_up, down), 2 x (lm_head, argmax); error bits 0x%x\n",
-              pos, e);
+  std::printf("qe_stage_pmc: 8 x (qkv, attention at pos %u%s, o_proj, gate_up, down), 2 x (lm_head, argmax); error bits 0x%x\n",
+              pos, prefetch ? " with the L2 prefetch" : "", e);
   return 0;
 }

@@ -58,6 +58,8 @@ def main():
     ap.add_argument("--out-json", required=True)
     ap.add_argument("--out-md", required=True)
     ap.add_argument("--command", default="")
+    ap.add_argument("--no-prefetch", action="store_true",
+                    help="the counter runs used qe_stage_pmc --no-prefetch (attention without the L2 prefetch)")
     a = ap.parse_args()
 
     fetch, write = read(a.fetch, "FETCH_SIZE"), read(a.write, "WRITE_SIZE")
@@ -73,7 +75,7 @@ def main():
     ff, fw = copy_kib / cf, copy_kib / cw
 
     mean_pos = float(a.attn_pos)
-    algo = qe.stage_bytes(qe.QWEN3_0_6B, mean_pos, 4)
+    algo = qe.stage_bytes(qe.QWEN3_0_6B, mean_pos, 4, prefetch=not a.no_prefetch)
     stages = {}
     for rows, key in ((fetch, "fetch_kib"), (write, "write_kib")):
         for kernel, v in rows:
@@ -114,7 +116,8 @@ def main():
         f"{a.copy_mib} MiB copy kernel (read {a.copy_mib} MiB, write {a.copy_mib} MiB): FETCH_SIZE x {ff:.4f},",
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
-        "for attention (the figures `bench.py` divides by the launch time).",
+        "for attention" + ("" if a.no_prefetch else ", plus the o_proj and gate/up weights its launch streams into L2") +
+        " (the figures `bench.py` divides by the launch time).",
         "",
         "Commands (MI355X, one GPU; committed files only):",
         "",
