@@ -136,15 +136,23 @@ __device__ void l2_prefetch(const AttnParams& p, uint32_t q) {
   uint4 v[KMAX];
 #pragma unroll
   for (int k = 0; k < KMAX; k++) {
-    uint32_t i = min(tid + 256u * k, tot - 1), t = 0;
-    if (i >= cnt[0] * p.pf[0].cw_chunks) {
-      i -= cnt[0] * p.pf[0].cw_chunks;
-      t = 1;
+    // chunk i of this workgroup's share: target t, its consumer workgroup jj, chunk c in it
+    uint32_t i = min(tid + 256u * k, tot - 1);
+    const uint16_t* w = p.pf[0].w;
+    uint32_t cw = p.pf[0].cw_chunks, nc = p.pf[0].n_chunks, span = cnt[0] * cw;
+#pragma unroll
+    for (int t = 1; t < kMaxPrefetch; t++) {
+      if (i >= span) {
+        i -= span;
+        w = p.pf[t].w;
+        cw = p.pf[t].cw_chunks;
+        nc = p.pf[t].n_chunks;
+        span = cnt[t] * cw;
+      }
     }
-    const L2Prefetch& f = p.pf[t];
-    const uint32_t jj = i / f.cw_chunks, c = i - jj * f.cw_chunks;
+    const uint32_t jj = i / cw, c = i - jj * cw;
     const uint32_t j = x + 8 * (slot + ns * jj);
-    v[k] = reinterpret_cast<const uint4*>(f.w)[min(j * f.cw_chunks + c, f.n_chunks - 1)];
+    v[k] = reinterpret_cast<const uint4*>(w)[min(j * cw + c, nc - 1)];
   }
   __builtin_amdgcn_sched_barrier(0);
   uint32_t h = 0;

@@ -387,10 +387,12 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     a.max_seq = uint32_t(kv->max_seq); a.eps = c.rms_norm_eps; a.scale = 1.0f / sqrtf(float(D));
     a.kv_bf16 = kv->dtype == QE_KV_BF16;
     if (m->l2_prefetch) {
-      // the attention is latency-bound: extra workgroups of its launch pull this layer's o_proj
-      // and gate/up weights into the L2 of the XCDs whose workgroups will read them
-      a.pf[0] = qe::l2_prefetch_target(w.w_o, H, QD, qe::kAttnMerge, qe::kResAdd);
-      a.pf[1] = qe::l2_prefetch_target(w.w_gu, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      // the attention is latency-bound: extra workgroups of its launch pull this layer's gate/up
+      // and down weights into the L2 of the XCDs whose workgroups will read them (measured
+      // against o_proj + gate/up, down alone and adding the next layer's q|k|v: this pair is
+      // fastest)
+      a.pf[0] = qe::l2_prefetch_target(w.w_gu, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      a.pf[1] = qe::l2_prefetch_target(w.w_down, H, I, qe::kCopy, qe::kResAdd);
       a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
     }
     p = MatvecParams{};

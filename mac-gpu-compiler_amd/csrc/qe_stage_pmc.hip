@@ -3,7 +3,7 @@
 // 1 GiB device copy of known traffic. Meant to run under `rocprofv3 --pmc FETCH_SIZE` and
 // `--pmc WRITE_SIZE`: the counters per dispatch, scaled by the copy's, give each stage's HBM
 // bytes per launch. Stage order and kernels are those of the engine's decode step, including
-// the attention launch's L2 prefetch of the layer's o_proj and gate/up weights.
+// the attention launch's L2 prefetch of the layer's gate/up and down weights.
 //
 //   qe_stage_pmc [--pos P] [--no-prefetch]   (attention attends positions 0..P, default 193)
 #include <cstdio>
@@ -127,8 +127,8 @@ int main(int argc, char** argv) {
     a.k_cache = kc; a.v_cache = vc; a.partial = part; a.state = st; a.err = err;
     a.n_heads = NH; a.n_kv = NKV; a.max_seq = max_seq; a.eps = 1e-6f; a.scale = 0.08838834764f;
     if (prefetch) {
-      a.pf[0] = qe::l2_prefetch_target(Wc + n_qkv, H, QD, qe::kAttnMerge, qe::kResAdd);
-      a.pf[1] = qe::l2_prefetch_target(Wc + n_qkv + n_o, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      a.pf[0] = qe::l2_prefetch_target(Wc + n_qkv + n_o, 2 * I, H, qe::kNorm, qe::kSiluPair);
+      a.pf[1] = qe::l2_prefetch_target(Wc + n_qkv + n_o + n_gu, H, I, qe::kCopy, qe::kResAdd);
       a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
     }
     CK(qe::launch_attention_split(a, splits, s));

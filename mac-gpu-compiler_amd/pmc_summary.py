@@ -116,7 +116,7 @@ def main():
         f"{a.copy_mib} MiB copy kernel (read {a.copy_mib} MiB, write {a.copy_mib} MiB): FETCH_SIZE x {ff:.4f},",
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
-        "for attention" + ("" if a.no_prefetch else ", plus the o_proj and gate/up weights its launch streams into L2") +
+        "for attention" + ("" if a.no_prefetch else ", plus the gate/up and down weights its launch streams into L2") +
         " (the figures `bench.py` divides by the launch time).",
         "",
         "Commands (MI355X, one GPU; committed files only):",
