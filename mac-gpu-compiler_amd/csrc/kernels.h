@@ -33,6 +33,18 @@ struct ArgCand {
   uint32_t i;
 };
 
+// Weight chunks that a later kernel of the step reads, loaded ahead into the L2 of the XCD that
+// will read them. Consumer workgroup j of launch_matvec_wide reads the 16-byte chunks
+// [j * cw_chunks, (j + 1) * cw_chunks) of its matrix and runs on XCD j % 8 (workgroups are
+// dispatched round-robin over the 8 XCDs).
+struct L2Prefetch {
+  const uint16_t* w;   // bf16 matrix
+  uint32_t n_chunks;   // 16-byte chunks in the matrix
+  uint32_t cw_chunks;  // chunks one consumer workgroup reads
+  uint32_t n_cwg;      // consumer workgroups
+};
+constexpr int kMaxPrefetch = 2;
+
 struct MatvecParams {
   const uint16_t* w;     // bf16 [rows][cols] row-major
   const float* x;        // [cols] input
@@ -55,18 +67,6 @@ struct MatvecParams {
 
 enum Prologue { kCopy = 0, kNorm = 1, kEmbedNorm = 2, kAttnMerge = 3 };
 enum Epilogue { kStore = 0, kResAdd = 1, kSiluPair = 2, kLogits = 3 };
-
-// Weight chunks that a later kernel of the step reads, loaded ahead into the L2 of the XCD that
-// will read them. Consumer workgroup j of launch_matvec_wide reads the 16-byte chunks
-// [j * cw_chunks, (j + 1) * cw_chunks) of its matrix and runs on XCD j % 8 (workgroups are
-// dispatched round-robin over the 8 XCDs).
-struct L2Prefetch {
-  const uint16_t* w;   // bf16 matrix
-  uint32_t n_chunks;   // 16-byte chunks in the matrix
-  uint32_t cw_chunks;  // chunks one consumer workgroup reads
-  uint32_t n_cwg;      // consumer workgroups
-};
-constexpr int kMaxPrefetch = 2;
 
 struct AttnParams {
   const float* qkv;        // raw projections [n_heads*D | n_kv*D | n_kv*D]
