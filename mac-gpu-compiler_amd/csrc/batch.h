@@ -33,6 +33,8 @@ struct GemmParams {
 };
 
 constexpr uint32_t kGemmSkinnyMaxM = 32;
+// More than kGemmTileMinM rows run on the 128-row tile kernel; between the two, 64 x 64 tiles.
+constexpr uint32_t kGemmTileMinM = 64;
 
 struct BatchAttnParams {
   const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections
@@ -52,8 +54,8 @@ struct BatchAttnParams {
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
 hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
-// K splits for a split GEMM of M > kGemmSkinnyMaxM rows: enough workgroups to fill the chip,
-// each split a multiple of 64 deep (1 when K does not split)
+// K splits for a split GEMM: enough workgroups to fill the chip, each split a multiple of the
+// kernel's k step deep (1 when K does not split)
 uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K);
 // partial sums of `splits` K ranges (no norm): C[z][m][n], z < splits, ldc = N
 hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t st);

@@ -271,6 +271,149 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Tiled GEMM for M > 64: workgroup tile 128 (m) x BN (n), BN = 128 or 64, k stages of 32. Four
+// waves as 2 x 2: wave (wm, wn) owns rows 64 wm .. 64 wm + 63 and columns (BN / 2) wn .. + BN / 2
+// - 1, i.e. 4 x BN / 32 MFMA tiles of 16 x 16, so each fragment read from LDS feeds BN / 32 (A)
+// or 8 (W) MFMAs. Both operands are staged in LDS: the thread that loads an f32 A element
+// applies the norm scale and splits it into hi + lo bf16 once for the whole workgroup; W rows go
+// in as they are. Two LDS buffers, two register stages: while stage s is computed, stage s + 1
+// (already in registers) is written to the other buffer and stage s + 2 is loaded from memory.
+// gridDim.z > 1 splits K as in k_gemm_lds.
+// ---------------------------------------------------------------------------------------------
+template <bool NORM, int EPI, int BN>
+__global__ __launch_bounds__(256) void k_gemm_tile(GemmParams p) {
+  constexpr int BM = 128, BK = 32, NT = BN / 32, KP = BK + 8;
+  constexpr int WCH = BN * BK / 8 / 256;  // 16-byte W chunks per thread per stage
+  static_assert(WCH >= 1 && NT >= 2, "tile");
+  __shared__ __align__(16) uint16_t as[2][2][BM][KP];  // [buffer][hi, lo][m][k]
+  __shared__ __align__(16) uint16_t bs[2][BN][KP];     // [buffer][n][k]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int wm = wave & 1, wn = wave >> 1;
+  const uint32_t m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+  const uint32_t kz = p.K / gridDim.z, kbeg = blockIdx.z * kz, nst = kz / BK;
+  // A staging: float4 f = tid + 256 i (i < 4) is row tid / 8 + 32 i, k (tid % 8) * 4
+  const int ar = tid >> 3, ak = (tid & 7) * 4;
+  const float* Asrc[4];
+  float rs[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const uint32_t row = min(m0 + uint32_t(ar + 32 * i), p.M - 1);
+    Asrc[i] = p.A + size_t(row) * p.lda + kbeg + ak;
+    rs[i] = NORM ? p.rowscale[row] : 1.0f;
+  }
+  const uint16_t* gsrc = NORM ? p.gain + kbeg + ak : nullptr;
+  // W staging: chunk c = tid + 256 i is row c / 4, k (c % 4) * 8
+  const uint16_t* Wsrc[WCH];
+#pragma unroll
+  for (int i = 0; i < WCH; i++) {
+    const int c = tid + 256 * i;
+    Wsrc[i] = p.W + size_t(min(n0 + uint32_t(c >> 2), p.N - 1)) * p.K + kbeg + 8 * (c & 3);
+  }
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+  struct Stage {
+    f32x4 a[4];
+    u32x4 w[WCH];
+    u32x2 g;
+  };
+  auto load = [&](Stage& r, uint32_t stg) __attribute__((always_inline)) {
+    const uint32_t k = stg * BK;
+#pragma unroll
+    for (int i = 0; i < 4; i++) r.a[i] = *reinterpret_cast<const f32x4*>(Asrc[i] + k);
+#pragma unroll
+    for (int i = 0; i < WCH; i++) r.w[i] = *reinterpret_cast<const u32x4*>(Wsrc[i] + k);
+    if constexpr (NORM) r.g = *reinterpret_cast<const u32x2*>(gsrc + k);
+  };
+  auto pk = [](float a, float b) __attribute__((always_inline)) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+  };
+  auto store = [&](const Stage& r, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      float v[4] = {r.a[i][0], r.a[i][1], r.a[i][2], r.a[i][3]};
+      if constexpr (NORM) {
+        v[0] = (v[0] * rs[i]) * __uint_as_float(r.g[0] << 16);
+        v[1] = (v[1] * rs[i]) * __uint_as_float(r.g[0] & 0xFFFF0000u);
+        v[2] = (v[2] * rs[i]) * __uint_as_float(r.g[1] << 16);
+        v[3] = (v[3] * rs[i]) * __uint_as_float(r.g[1] & 0xFFFF0000u);
+      }
+      const uint32_t h0 = pk(v[0], v[1]), h1 = pk(v[2], v[3]);
+      const uint32_t l0 = pk(v[0] - __uint_as_float(h0 << 16), v[1] - __uint_as_float(h0 & 0xFFFF0000u));
+      const uint32_t l1 = pk(v[2] - __uint_as_float(h1 << 16), v[3] - __uint_as_float(h1 & 0xFFFF0000u));
+      *reinterpret_cast<u32x2*>(&as[buf][0][ar + 32 * i][ak]) = u32x2{h0, h1};
+      *reinterpret_cast<u32x2*>(&as[buf][1][ar + 32 * i][ak]) = u32x2{l0, l1};
+    }
+#pragma unroll
+    for (int i = 0; i < WCH; i++) {
+      const int c = tid + 256 * i;
+      *reinterpret_cast<u32x4*>(&bs[buf][c >> 2][8 * (c & 3)]) = r.w[i];
+    }
+  };
+  f32x4 acc[4][NT];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](int buf) __attribute__((always_inline)) {
+    bf16x8 b[NT];
+#pragma unroll
+    for (int j = 0; j < NT; j++)
+      b[j] = *reinterpret_cast<const bf16x8*>(&bs[buf][wn * (BN / 2) + 16 * j + li][8 * kg]);
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const int row = wm * 64 + 16 * i + li;
+      const bf16x8 hi = *reinterpret_cast<const bf16x8*>(&as[buf][0][row][8 * kg]);
+      const bf16x8 lo = *reinterpret_cast<const bf16x8*>(&as[buf][1][row][8 * kg]);
+#pragma unroll
+      for (int j = 0; j < NT; j++) {
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b[j], acc[i][j], 0, 0, 0);
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b[j], acc[i][j], 0, 0, 0);
+      }
+    }
+  };
+  // step s: x is free (its stage is in LDS), y holds stage s + 1
+  auto step = [&](Stage& x, Stage& y, uint32_t s) __attribute__((always_inline)) {
+    load(x, min(s + 2, nst - 1));  // unconditional: the last steps reload the last stage
+    if (s < nst) compute(int(s & 1));
+    if (s + 1 < nst) store(y, int((s + 1) & 1));
+    __syncthreads();
+  };
+  Stage r0, r1;
+  load(r0, 0);
+  load(r1, min(1u, nst - 1));
+  store(r0, 0);
+  __syncthreads();
+  for (uint32_t s = 0; s < nst; s += 2) {
+    step(r0, r1, s);
+    step(r1, r0, s + 1);
+  }
+
+  // epilogue: lane holds C[m0 + 64 wm + 16 i + 4 kg + r][n0 + (BN / 2) wn + 16 j + li]
+  float* C = p.C + (EPI == kGemmPartial ? size_t(blockIdx.z) * p.M * p.ldc : 0);
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+      const uint32_t n = n0 + uint32_t(wn * (BN / 2) + 16 * j + li);
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const uint32_t m = m0 + uint32_t(wm * 64 + 16 * i + 4 * kg + r);
+        const float c = acc[i][j][r];
+        if constexpr (EPI == kGemmSiluPair) {
+          const float up = __shfl_xor(c, 1);  // columns 2i (gate) and 2i+1 (up) in neighbouring lanes
+          if (m < p.M && n < p.N && (li & 1) == 0) C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
+        } else if constexpr (EPI == kGemmResAdd) {
+          if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] += c;
+        } else {
+          if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] = c;
+        }
+      }
+    }
+  }
+}
+
 // x[m] += sum_z part[z][m] (in z order), then s[m] = 1 / sqrt(mean x[m]^2 + eps); one workgroup
 // per row, float4 per thread per pass
 __global__ __launch_bounds__(256) void k_resadd_partials(float* __restrict__ x, const float* __restrict__ part,
@@ -756,6 +899,9 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
     x[size_t(m) * H + i] = bf16f(table[size_t(ids[m]) * H + i]);
 }
 
+// column tile of k_gemm_tile: 128 when that alone gives a tile per CU, else 64
+uint32_t tile_bn(uint32_t M, uint32_t N) { return ceil_div(M, 128) * ceil_div(N, 128) >= 256 ? 128 : 64; }
+
 }  // namespace
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st) {
@@ -777,6 +923,21 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
     return hipGetLastError();
   }
   if (norm && !p.rowscale) return hipErrorInvalidValue;
+  if (p.M > kGemmTileMinM) {
+    const uint32_t bn = tile_bn(p.M, p.N);
+    const dim3 tg(ceil_div(p.N, bn), ceil_div(p.M, 128));
+#define QE_TILE(NRM, E)                                                                          \
+  do {                                                                                           \
+    if (bn == 128) hipLaunchKernelGGL((k_gemm_tile<NRM, E, 128>), tg, dim3(256), 0, st, p);      \
+    else hipLaunchKernelGGL((k_gemm_tile<NRM, E, 64>), tg, dim3(256), 0, st, p);                 \
+  } while (0)
+    if (norm && epi == kGemmStore) QE_TILE(true, kGemmStore);
+    else if (norm && epi == kGemmSiluPair) QE_TILE(true, kGemmSiluPair);
+    else if (!norm && epi == kGemmStore) QE_TILE(false, kGemmStore);
+    else if (!norm && epi == kGemmResAdd) QE_TILE(false, kGemmResAdd);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64));
   if (p.K % 64 == 0) {
     if (norm && epi == kGemmStore) hipLaunchKernelGGL((k_gemm_lds<true, kGemmStore>), grid, dim3(256), 0, st, p);
@@ -803,8 +964,17 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
 
 uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K) {
   // tiles of the kernel that runs M rows, and the depth one split must stay a multiple of
-  const bool skinny = M <= kGemmSkinnyMaxM;
-  const uint32_t tiles = skinny ? ceil_div(N, 16) : ceil_div(N, 64) * ceil_div(M, 64), unit = skinny ? 32 : 64;
+  uint32_t tiles, unit;
+  if (M <= kGemmSkinnyMaxM) {
+    tiles = ceil_div(N, 16);
+    unit = 32;
+  } else if (M <= kGemmTileMinM) {
+    tiles = ceil_div(N, 64) * ceil_div(M, 64);
+    unit = 64;
+  } else {
+    tiles = ceil_div(N, tile_bn(M, N)) * ceil_div(M, 128);
+    unit = 32;
+  }
   uint32_t z = 1;
   while (z < 8 && tiles * z < 256 && K % (2 * unit * z) == 0) z *= 2;
   return z;
@@ -816,6 +986,14 @@ hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t s
   if (p.M <= kGemmSkinnyMaxM) {
     if (p.K % (32 * splits)) return hipErrorInvalidValue;
     launch_skinny<false, kGemmPartial>(p, splits, st);
+    return hipGetLastError();
+  }
+  if (p.M > kGemmTileMinM) {
+    if (p.K % (32 * splits)) return hipErrorInvalidValue;
+    const uint32_t bn = tile_bn(p.M, p.N);
+    const dim3 tg(ceil_div(p.N, bn), ceil_div(p.M, 128), splits);
+    if (bn == 128) hipLaunchKernelGGL((k_gemm_tile<false, kGemmPartial, 128>), tg, dim3(256), 0, st, p);
+    else hipLaunchKernelGGL((k_gemm_tile<false, kGemmPartial, 64>), tg, dim3(256), 0, st, p);
     return hipGetLastError();
   }
   if (p.K % (64 * splits)) return hipErrorInvalidValue;
