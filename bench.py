@@ -373,7 +373,7 @@ def main():
 
     if args.gpus != 1:
         print(f"bench.py: this engine runs batch-1 decode on one GPU; --gpus {args.gpus} is not supported "
-              "(the multi-GPU layout is a design note, see DESIGN.md)", file=sys.stderr)
+              "(how the path would shard across GPUs is a design note, not code)", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np

@@ -2,7 +2,7 @@
  * CPU oracle for the Qwen3 batch-1 decode path -- TEST INFRASTRUCTURE ONLY.
  *
  * A plain-C restatement of metal_infrence_engine/src/cpu_inference.rs (the reference's CPU
- * engine), used by tests/ as the parity checker for the HIP engine and by bench.py as the
+ * engine), used by tests/ as the parity reference for the HIP engine and by bench.py as the
  * timed CPU baseline. The product (the HIP engine library) never links or calls this file.
  *
  * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, no fast-math), so every f32 multiply and

@@ -2,8 +2,8 @@
  * CPU oracle for the Qwen3 batch-1 decode path.
  *
  * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's CPU engine
- * (metal_infrence_engine/src/cpu_inference.rs), used as the checker that the HIP engine is
- * compared against, and timed as the CPU baseline. Only tests/, __graft_entry__.smoke() and
+ * (metal_infrence_engine/src/cpu_inference.rs): the HIP engine's results are compared against
+ * it, and it is timed as the CPU baseline. Only tests/, __graft_entry__.smoke() and
  * bench.py's cpu_baseline leg may load it. The product path never calls it.
  *
  * Every function cites the reference line it restates. Op order is kept exactly: separate

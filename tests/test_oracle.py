@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity checker.
+"""Pins the CPU oracle (oracle/oracle.c) before the HIP engine's results are compared against it.
 
 Each check is chosen so that a plausible restatement mistake fails it: closed forms, float64
 brute force, invariants, and an independent implementation (transformers' Qwen3, built from a
