@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   if constexpr (DECODE) {
     if (blockIdx.y >= p.splits) {  // a prefetch workgroup (whole workgroup, before any load)
       const uint32_t q = (blockIdx.y - p.splits) * gridDim.x + blockIdx.x;
-      if (q < 8 * p.pf_slots) l2_prefetch(p.pf, p.pf_slots, q, p.err);
+      if (q < 8 * p.pf_slots && p.state->pos < p.pf_max_pos) l2_prefetch(p.pf, p.pf_slots, q, p.err);
       return;
     }
   }

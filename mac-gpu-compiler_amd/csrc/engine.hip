@@ -394,6 +394,11 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
       a.pf[0] = qe::l2_prefetch_target(w.w_gu, 2 * I, H, qe::kNorm, qe::kSiluPair);
       a.pf[1] = qe::l2_prefetch_target(w.w_down, H, I, qe::kCopy, qe::kResAdd);
       a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
+      // once the layer's own K/V stream reaches half the prefetched bytes the attention is no
+      // longer idle on HBM and the prefetch costs more than it saves (measured crossover:
+      // ~1150 positions with an f32 cache, ~2300-2700 with bf16)
+      const double pf_bytes = double(3 * I * H) * 2.0, kv_bytes_per_pos = double(2 * c.num_key_value_heads * D * el);
+      a.pf_max_pos = uint32_t(std::min(0.5 * pf_bytes / kv_bytes_per_pos, double(kv->max_seq)));
     }
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;

@@ -85,9 +85,10 @@ struct AttnParams {
   uint32_t n_pos_fixed;    // isolated op: attend positions 0..n_pos_fixed-1 with a final q
   uint32_t splits;         // runs per KV head (set by the launchers)
   // decode only: 8 * pf_slots extra workgroups load these matrices into L2 while the attention
-  // runs (pf_slots = 0: none)
+  // runs (pf_slots = 0: none), at positions below pf_max_pos
   L2Prefetch pf[kMaxPrefetch];
   uint32_t pf_slots;
+  uint32_t pf_max_pos;
 };
 
 // --- launch wrappers (kernels.hip) ---

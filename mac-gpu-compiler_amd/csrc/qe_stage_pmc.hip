@@ -130,6 +130,8 @@ int main(int argc, char** argv) {
       a.pf[0] = qe::l2_prefetch_target(Wc + n_qkv + n_o, 2 * I, H, qe::kNorm, qe::kSiluPair);
       a.pf[1] = qe::l2_prefetch_target(Wc + n_qkv + n_o + n_gu, H, I, qe::kCopy, qe::kResAdd);
       a.pf_slots = qe::l2_prefetch_slots(a.pf, qe::kMaxPrefetch);
+      // the engine's rule: prefetch while one layer's K/V (f32 here) is below half its bytes
+      a.pf_max_pos = uint32_t(0.5 * (3.0 * I * H * 2) / (2.0 * NKV * D * 4));
     }
     CK(qe::launch_attention_split(a, splits, s));
     // merge + o_proj + residual

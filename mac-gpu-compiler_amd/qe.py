@@ -116,15 +116,23 @@ def l2_prefetch_enabled() -> bool:
     return os.environ.get("QE_L2_PREFETCH", "1") != "0"
 
 
+def l2_prefetch_max_pos(cfg: Config, kv_el: int = 4) -> int:
+    """First position at which the attention launch no longer prefetches: where one layer's K/V
+    history reaches half the prefetched gate/up + down bytes (the engine's rule)."""
+    pf_bytes = 3 * cfg.intermediate_size * cfg.hidden_size * 2
+    return int(0.5 * pf_bytes / (2 * cfg.num_key_value_heads * cfg.head_dim * kv_el))
+
+
 def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4, prefetch: bool = False) -> dict:
     """Algorithmic bytes per launch of each decode-step stage: a matvec moves its bf16 weights
     plus its f32 input and output once (out*in*2 + in*4 + out*4, bench.rs:106-119 counts the
     weights), attention its K/V history at mean_pos plus q/k/v in and the output out. With
-    `prefetch`, the attention launch also streams the layer's gate/up and down weights (the
-    bytes it moves from HBM; the per-token total still counts each weight once)."""
+    `prefetch` (and mean_pos below l2_prefetch_max_pos), the attention launch also streams the
+    layer's gate/up and down weights (the bytes it moves from HBM; the per-token total still
+    counts each weight once)."""
     H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
-    pf = (2 * I * H * 2 + H * I * 2) if prefetch else 0
+    pf = (2 * I * H * 2 + H * I * 2) if prefetch and mean_pos < l2_prefetch_max_pos(cfg, kv_el) else 0
     return {
         "embed": H * 2 + H * 4,
         "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
