@@ -66,8 +66,8 @@ hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, 
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
 // causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);
-// key runs for a chunk of M tokens at positions start.. : enough workgroups to cover the chip,
-// at least two 32-position tiles per run
+// key runs for a chunk of M tokens at positions start.. : at least 4, more while the chunk has
+// under 512 workgroups, and at most one per 128 keys
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv);
 // tokens[r] = greedy token of row r of logits [rows][V] (the decode step's argmax rule)
 hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, hipStream_t st);
