@@ -132,7 +132,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   const size_t head_base = size_t(g) * p.max_seq * D;
   // Decode sizes the runs from the current length (below); the first tile is loaded up front
   // for runs of a single tile, which is what every step up to 64 * splits positions has.
-  const uint32_t t0_first = DECODE ? s * T : s * chunk;
+  // the first run start: known at launch unless the decode step has no run length from the host
+  const uint32_t t0_first = DECODE ? s * (p.run ? p.run : uint32_t(T)) : s * chunk;
 
   __shared__ __align__(16) float qs[G][D];
   __shared__ __align__(16) float knew[D];
@@ -174,11 +175,20 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     const bool bad = pos >= p.max_seq;
     if (bad && g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
     n = bad ? 0u : pos + 1;
-    // the n positions in p.splits runs of a whole number of tiles
-    run = T * ceil_div(max(n, 1u), T * p.splits);
+    if (p.run) {
+      // runs of the host's length; positions they do not cover would be skipped: flag that
+      run = p.run;
+      if (n > p.splits * run) {
+        if (g == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrShape);
+        n = 0;
+      }
+    } else {
+      // the n positions in p.splits runs of a whole number of tiles
+      run = T * ceil_div(max(n, 1u), T * p.splits);
+    }
     t0 = s * run;
-    owns_new = !bad && pos >= t0 && pos < t0 + run;
-    if (run != T) load_tile<KV_BF16>(A, p, head_base, t0, tid);  // longer runs start elsewhere
+    owns_new = n != 0 && pos >= t0 && pos < t0 + run;
+    if (!p.run && run != T) load_tile<KV_BF16>(A, p, head_base, t0, tid);  // longer runs start elsewhere
   } else {
     n = p.n_pos_fixed;
     pos = n - 1;

@@ -128,17 +128,26 @@ struct qe_kv {
   uint32_t* tokens = nullptr;       // device token ring [tok_cap]
   uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
   uint32_t tok_cap = 0;
-  uint32_t attn_splits = 1;
-  bool eager = false;           // launch the step kernel by kernel instead of replaying the graph
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
+  uint32_t attn_splits = 1;     // the most attention runs per KV head a step uses
+  // the attention shape enqueue_step records: runs per KV head and positions per run
+  uint32_t step_splits = 1, step_run = 64;
+  bool eager = false;           // launch the step kernel by kernel instead of replaying a graph
+  // one captured step per attention shape (splits, run); launch_step picks it by position
+  struct StepGraph {
+    uint32_t splits, run;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+  };
+  std::vector<StepGraph> graphs;
   std::vector<hipEvent_t> events;
   uint64_t len = 0;
 
   ~qe_kv() {
     if (model && model->stream) (void)hipStreamSynchronize(model->stream);
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
+    for (auto& g : graphs) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
     for (auto e : events) (void)hipEventDestroy(e);
     if (mem) (void)hipFree(mem);
     if (host_tokens) (void)hipHostFree(host_tokens);
@@ -402,9 +411,10 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     }
     p = MatvecParams{};
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
-    if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->attn_splits, s));
+    a.run = kv->step_run;
+    if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->step_splits, s));
     // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
-    p.attn_part = m->attn_part; p.attn_splits = kv->attn_splits;
+    p.attn_part = m->attn_part; p.attn_splits = kv->step_splits;
     p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
     if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
@@ -571,10 +581,63 @@ int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
   return QE_OK;
 }
 
-// one decode step on the model stream: a replay of the captured graph, or eager launches
-int launch_step(qe_model* m, qe_kv* kv) {
-  if (kv->eager) return enqueue_step(m, kv);
-  HIP_TRY(hipGraphLaunch(kv->exec, m->stream));
+// The attention shape of a decode step at position pos: runs of `run` positions (a multiple of
+// 64, the least that covers pos + 1 positions in kv->attn_splits runs) and `splits` runs per KV
+// head. Runs of 64 come in 4, 8 or attn_splits, so that a short context in a large cache does
+// not launch (and o_proj does not merge) empty runs; longer runs always use attn_splits. The
+// host knows every step's position, so each step replays the graph of its shape and the
+// attention kernel starts its first K/V tile load at launch instead of after reading pos.
+void step_shape(const qe_kv* kv, uint64_t pos, uint32_t& splits, uint32_t& run) {
+  const uint64_t n = pos + 1, S = kv->attn_splits;
+  run = uint32_t(64 * ((n + 64 * S - 1) / (64 * S)));
+  const uint64_t active = (n + run - 1) / run;
+  splits = uint32_t(run == 64 ? (active <= 4 ? std::min<uint64_t>(4, S) : active <= 8 ? std::min<uint64_t>(8, S) : S) : S);
+}
+
+// capture one decode step with attention shape (splits, run)
+int capture_step(qe_model* m, qe_kv* kv, uint32_t splits, uint32_t run) {
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  kv->step_splits = splits;
+  kv->step_run = run;
+  HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+  int rc = enqueue_step(m, kv);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(m->stream, &g);
+  if (rc != QE_OK) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return fail(QE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
+  hipGraphExec_t ex = nullptr;
+  e = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return fail(QE_ERR_HIP, "graph instantiation failed: %s", hipGetErrorString(e));
+  }
+  kv->graphs.push_back({splits, run, g, ex});
+  return QE_OK;
+}
+
+// one decode step at position pos on the model stream: a replay of the graph of its attention
+// shape (captured here the first time a shape is needed), or eager launches
+int launch_step(qe_model* m, qe_kv* kv, uint64_t pos) {
+  uint32_t splits, run;
+  step_shape(kv, pos, splits, run);
+  if (kv->eager) {
+    kv->step_splits = splits;
+    kv->step_run = run;
+    return enqueue_step(m, kv);
+  }
+  for (const auto& g : kv->graphs)
+    if (g.splits == splits && g.run == run) {
+      kv->step_splits = splits;
+      kv->step_run = run;
+      HIP_TRY(hipGraphLaunch(g.exec, m->stream));
+      return QE_OK;
+    }
+  int rc = capture_step(m, kv, splits, run);
+  if (rc) return rc;
+  HIP_TRY(hipGraphLaunch(kv->graphs.back().exec, m->stream));
   return QE_OK;
 }
 
@@ -656,17 +719,23 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
     *out = kv.release();
     return QE_OK;
   }
-  HIP_TRY(hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal));
-  int rc = enqueue_step(model, kv.get());
-  hipGraph_t g = nullptr;
-  hipError_t e = hipStreamEndCapture(model->stream, &g);
-  if (rc != QE_OK) {
-    if (g) (void)hipGraphDestroy(g);
-    return rc;
+  // capture every attention shape up front when there are few (caches up to ~60 K positions);
+  // larger caches capture the rest as decoding first reaches them
+  std::vector<std::pair<uint32_t, uint32_t>> shapes;
+  for (uint64_t pos = 0; pos < max_seq && shapes.size() <= 64;) {
+    uint32_t splits, run;
+    step_shape(kv.get(), pos, splits, run);
+    if (shapes.empty() || shapes.back() != std::make_pair(splits, run)) shapes.push_back({splits, run});
+    // the next position whose shape can differ: the end of this run length's range, or for runs
+    // of 64 the next multiple of 64
+    pos = run == 64 ? (pos / 64 + 1) * 64 : uint64_t(run) * kv->attn_splits;
   }
-  if (e != hipSuccess) return fail(QE_ERR_HIP, "graph capture failed: %s", hipGetErrorString(e));
-  kv->graph = g;
-  HIP_TRY(hipGraphInstantiate(&kv->exec, g, nullptr, nullptr, 0));
+  if (shapes.size() <= 64) {
+    for (const auto& sh : shapes) {
+      int rc = capture_step(model, kv.get(), sh.first, sh.second);
+      if (rc) return rc;
+    }
+  }
   *out = kv.release();
   return QE_OK;
 }
@@ -683,7 +752,7 @@ int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* 
   if (token >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab %llu", token, (unsigned long long)model->cfg.vocab_size);
   int rc = set_state(model, kv, token, pos);
   if (rc) return rc;
-  if ((rc = launch_step(model, kv))) return rc;
+  if ((rc = launch_step(model, kv, pos))) return rc;
   const size_t V = model->cfg.vocab_size;
   HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
   if ((rc = check_err(model))) return rc;
@@ -702,7 +771,7 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   // the full step first, so that every stage reads the activations of a real step
   int rc = set_state(model, kv, token, pos);
   if (rc) return rc;
-  if ((rc = launch_step(model, kv))) return rc;
+  if ((rc = launch_step(model, kv, pos))) return rc;
   if ((rc = check_err(model))) return rc;
   kv->len = pos + 1;
   // then each stage alone: a graph of its launches (28 per-layer launches, or the one lm_head /
@@ -769,7 +838,7 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
       // overwrite the slot the previous step's argmax wrote with the next prompt id
       HIP_TRY(hipMemcpyAsync(kv->tokens + i, ids + i, 4, hipMemcpyHostToDevice, model->stream));
     }
-    if ((rc = launch_step(model, kv))) return rc;
+    if ((rc = launch_step(model, kv, start_pos + i))) return rc;
   }
   if (last_logits) {
     HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost, model->stream));
@@ -964,7 +1033,7 @@ int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t step
   for (uint64_t i = 0; i <= steps; i++) {
     if (i < steps) {
       if (i >= nev) HIP_TRY(hipEventSynchronize(kv->events[i % nev]));  // ring slot free
-      if ((rc = launch_step(model, kv))) return rc;
+      if ((rc = launch_step(model, kv, start_pos + i))) return rc;
       if (logits_per_step) {
         HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, V * 4, hipMemcpyDeviceToHost, model->stream));
       }

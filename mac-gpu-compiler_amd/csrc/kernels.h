@@ -25,6 +25,7 @@ enum : uint32_t {
   kErrPos = 1u,       // pos >= max_seq seen on the device
   kErrToken = 2u,     // input token >= vocab
   kErrRing = 4u,      // token ring full
+  kErrShape = 8u,     // the decode step's attention runs do not cover pos (a host-side mistake)
 };
 
 // Per-workgroup greedy candidate (value, index); NaN is never a candidate.
@@ -84,6 +85,8 @@ struct AttnParams {
   int kv_bf16;
   uint32_t n_pos_fixed;    // isolated op: attend positions 0..n_pos_fixed-1 with a final q
   uint32_t splits;         // runs per KV head (set by the launchers)
+  uint32_t run;            // decode: positions per run (a multiple of 64) chosen by the host for
+                           // the step's position; 0: derived from pos on the device
   // decode only: 8 * pf_slots extra workgroups load these matrices into L2 while the attention
   // runs (pf_slots = 0: none), at positions below pf_max_pos
   L2Prefetch pf[kMaxPrefetch];
