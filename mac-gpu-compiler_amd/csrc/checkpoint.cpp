@@ -370,6 +370,12 @@ const uint16_t* Checkpoint::bf16(const std::string& name, uint64_t numel, std::s
     err = name + ": data offsets run past the end of the file";
     return nullptr;
   }
+  // the reference views the bytes in place as u16 (cpu_inference.rs:95), which needs an even
+  // offset into the (2-byte aligned) data section
+  if (t.off0 % 2) {
+    err = name + ": data offset " + std::to_string(t.off0) + " is not 2-byte aligned";
+    return nullptr;
+  }
   return reinterpret_cast<const uint16_t*>(data_ + t.off0);
 }
 

@@ -115,6 +115,11 @@ def test_missing_tensor_wrong_dtype_wrong_shape(tmp_path):
     h3 = json.loads(json.dumps(header))
     h3["model.layers.0.self_attn.q_norm.weight"]["shape"] = [64]
     cases["shape"] = h3
+    # an odd data offset: the reference views the bytes in place as u16 (cpu_inference.rs:95)
+    h4 = json.loads(json.dumps(header))
+    t = h4["model.layers.0.self_attn.q_norm.weight"]
+    t["data_offsets"] = [t["data_offsets"][0] + 1, t["data_offsets"][1] + 1]
+    cases["odd_offset"] = h4
     for name, h in cases.items():
         d = tmp_path / name
         d.mkdir()
