@@ -163,10 +163,18 @@ static int jparse_value(jparser* p, jval* out, int depth) {
       }
       if (out->n == cap) {
         cap = cap ? cap * 2 : 8;
-        out->items = realloc(out->items, cap * sizeof(jval));
-        if (obj) out->keys = realloc(out->keys, cap * sizeof(char*));
+        jval* items = realloc(out->items, cap * sizeof(jval));
+        if (items) out->items = items;
+        char** keys = obj ? realloc(out->keys, cap * sizeof(char*)) : NULL;
+        if (keys) out->keys = keys;
+        if (!items || (obj && !keys)) { free(key); p->err = 1; return -1; }
       }
-      if (jparse_value(p, &out->items[out->n], depth + 1) != 0) { free(key); return -1; }
+      /* a failed child is freed here; the caller frees this value's first n items */
+      if (jparse_value(p, &out->items[out->n], depth + 1) != 0) {
+        jfree(&out->items[out->n]);
+        free(key);
+        return -1;
+      }
       if (obj) out->keys[out->n] = key;
       out->n++;
       jws(p);
@@ -223,12 +231,19 @@ static int jparse_value(jparser* p, jval* out, int depth) {
   return -1;
 }
 
+/* On failure *out is freed and left as an empty null value. */
 static int jparse(const char* s, size_t n, jval* out) {
   jparser p = {s, 0, n, 0};
-  if (jparse_value(&p, out, 0) != 0) { jfree(out); return -1; }
-  jws(&p);
-  if (p.i != p.n) { jfree(out); return -1; }
-  return 0;
+  int rc = jparse_value(&p, out, 0);
+  if (rc == 0) {
+    jws(&p);
+    if (p.i != p.n) rc = -1;
+  }
+  if (rc != 0) {
+    jfree(out);
+    memset(out, 0, sizeof(*out));
+  }
+  return rc;
 }
 
 static const jval* jget(const jval* obj, const char* key) {
