@@ -77,9 +77,10 @@ def test_tiny_decode_matches_oracle(gpu, tiny_ckpt):
 
 @pytest.mark.parametrize("max_seq,n_pos", [(300, 290), (2100, 2050)])
 def test_tiny_long_cache_matches_oracle(gpu, tiny_ckpt, max_seq, n_pos):
-    # A cache of 300 positions is split into 5 runs of 60 (one tile each, runs past pos empty);
-    # 2100 positions give 16 runs of 132, i.e. three 64-position tiles per run, so the
-    # double-buffered tile loop and the 16-way merge in o_proj are both exercised.
+    # Every position replays the step graph of its attention shape. A cache of 300 positions
+    # allows 5 runs per KV head: steps use 4 or 5 runs of 64 positions. 2100 positions allow 16:
+    # runs of 64 in groups of 4, 8 and 16, then runs of 128 and 192 positions (two and three
+    # tiles, so the double-buffered tile loop runs), with o_proj merging 4, 8 and 16 partials.
     m = qe.Model.load_model(tiny_ckpt)
     om = oracle.Model(tiny_ckpt)
     cache = qe.KVCache(m, max_seq)
