@@ -704,9 +704,9 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   HIP_TRY(hipMemcpyAsync(kv->rope, table.data(), rope_bytes, hipMemcpyHostToDevice, model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
 
-  // attention workgroups per KV head: one per 64 cached positions, at most kAttnMaxMergeSplits
-  // (the o_proj prologue merges that many partials per q head); each step cuts its positions
-  // into that many runs of whole 64-position tiles
+  // the most attention runs (workgroups) per KV head a step uses: one per 64 cached positions,
+  // at most kAttnMaxMergeSplits (the o_proj prologue merges that many partials per q head);
+  // step_shape picks each step's runs within this
   kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
 
   // QE_LAUNCH=eager launches each step kernel by kernel (for tools that do not follow graph
