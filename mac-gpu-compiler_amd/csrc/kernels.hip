@@ -468,7 +468,8 @@ hipError_t launch_wide(const MatvecParams& p, hipStream_t s) {
 // rows per row group: silu needs the (gate, up) pair; one-chunk rows of <= 128 threads take two
 template <int TPR, int CPT, int PRO, int EPI>
 hipError_t launch_wide_rr(const MatvecParams& p, hipStream_t s) {
-  constexpr int RR = (EPI == kSiluPair || (TPR <= 128 && CPT == 1)) ? 2 : 1;
+  // two rows per row group also for the 3-chunk rows of down (measured +0.8% per decode step)
+  constexpr int RR = (EPI == kSiluPair || (TPR <= 128 && CPT == 1) || (TPR == 128 && CPT == 3)) ? 2 : 1;
   return launch_wide<TPR, CPT, RR, PRO, EPI>(p, s);
 }
 
@@ -477,7 +478,10 @@ template <int PRO, int EPI>
 hipError_t launch_wide_cols(const MatvecParams& p, hipStream_t s) {
   const uint32_t nch = p.cols / 8;
   if (nch <= 64) return launch_wide_rr<64, 1, PRO, EPI>(p, s);
-  if (nch <= 128) return launch_wide_rr<128, 1, PRO, EPI>(p, s);
+  // gate|up (the silu pair, usually on weights the attention launch prefetched into L2) runs
+  // faster on twice the rows per workgroup: 64 threads x 2 chunks per row group (measured +1.3%
+  // per decode step)
+  if (nch <= 128) return EPI == kSiluPair ? launch_wide_rr<64, 2, PRO, EPI>(p, s) : launch_wide_rr<128, 1, PRO, EPI>(p, s);
   if (nch <= 256) return launch_wide_rr<256, 1, PRO, EPI>(p, s);
   if (nch == 384) return launch_wide_rr<128, 3, PRO, EPI>(p, s);
   if (nch <= 512) return launch_wide_rr<256, 2, PRO, EPI>(p, s);
@@ -537,9 +541,9 @@ uint32_t matvec_wide_rows_per_block(uint32_t cols, int prologue, int epilogue) {
   if (prologue == kAttnMerge) return nch <= 128 ? 8 : 4;  // RR 4 with TPR 128, else TPR 256
   const bool silu = epilogue == kSiluPair;
   if (nch <= 64) return 4 * 2;                // TPR 64, CPT 1: RR 2
-  if (nch <= 128) return 2 * 2;               // TPR 128, CPT 1: RR 2
+  if (nch <= 128) return silu ? 4 * 2 : 2 * 2;  // silu: TPR 64, CPT 2, RR 2; else TPR 128, CPT 1, RR 2
   if (nch <= 256) return silu ? 2 : 1;        // TPR 256
-  if (nch == 384) return 2 * (silu ? 2 : 1);  // TPR 128, CPT 3
+  if (nch == 384) return 2 * 2;               // TPR 128, CPT 3: RR 2
   return silu ? 2 : 1;                        // TPR 256, CPT 2
 }
 
