@@ -36,6 +36,20 @@ constexpr uint32_t kGemmSkinnyMaxM = 32;
 // More than kGemmTileMinM rows run on the 128-row tile kernel; between the two, 64 x 64 tiles.
 constexpr uint32_t kGemmTileMinM = 64;
 
+// Verify passes and chunks of up to kMvRowsMaxM tokens run the projections as a matvec over their
+// token rows: out[m][.] for m < M from x [M][cols] (see launch_mv_rows). Each further row adds its
+// own products and lane reductions to every wave of that matvec, so past 4 rows the skinny GEMM
+// on the matrix cores is faster (measured at 5, 8 and 9 rows).
+constexpr uint32_t kMvRowsMaxM = 4;
+struct MvRowsParams {
+  const uint16_t* w;     // bf16 [rows][cols], row-major
+  const float* x;        // [M][cols]
+  const uint16_t* gain;  // bf16 [cols]: the RMSNorm gain (norm launches only)
+  float* out;            // [M][ldo]
+  uint32_t M, rows, cols, ldo;
+  float eps;
+};
+
 struct BatchAttnParams {
   const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections
   float* q;                // [M][n_heads][128] normalized + rotated q
@@ -63,6 +77,11 @@ hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t s
 // the residual add of a split GEMM fused with the next RMSNorm's row scale. N % 4 == 0.
 hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, uint32_t M, uint32_t N, float eps,
                                   float* s, hipStream_t st);
+// out[m][r] (=, +=) sum_c W[r][c] x'[m][c] for m < M (kGemmStore / kGemmResAdd), or
+// out[m][i] = silu(gate_i) * up_i over the interleaved gate/up rows (kGemmSiluPair, ldo >= rows/2);
+// x' = x, or RMSNorm(x_m) * gain with `norm`. f32 FMA on bf16 weights, as the decode matvec.
+// cols % 8 == 0, cols <= 4096, 1 <= M <= kMvRowsMaxM; out must not alias x.
+hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st);
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
 // causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);

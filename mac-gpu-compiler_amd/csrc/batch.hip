@@ -902,7 +902,195 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
 // column tile of k_gemm_tile: 128 when that alone gives a tile per CU, else 64
 uint32_t tile_bn(uint32_t M, uint32_t N) { return ceil_div(M, 128) * ceil_div(N, 128) >= 256 ? 128 : 64; }
 
+// ---------------------------------------------------------------------------------------------
+// Matvec over the NV = M token rows of a short verify pass or chunk (M <= kMvRowsMaxM): the
+// decode step's matvec layout. A row group of TPR threads covers one weight row in 8-column
+// chunks (CPT per thread) and RR rows per group; each weight chunk is loaded once (128-bit) and
+// multiplied by the NV token rows in f32 FMA, so the weights stream once per pass as in a decode
+// step. With NORM every row group computes the sum of squares of each token row over its own
+// chunks (which cover the row) and scales the dot products, s * sum_c W[r,c] (x_c * g_c)
+// (cpu_inference.rs:189-194, 225-257). All loads are issued before the first use. Each token row
+// costs every wave its own products and lane reductions, so past a few rows the matrix cores
+// (k_gemm_skinny) are faster.
+// ---------------------------------------------------------------------------------------------
+template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI>
+__global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
+  constexpr int NG = 256 / TPR, WPG = TPR / 64, NS = NV * (RR + 1);
+  __shared__ float red[4][NS];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = tid / TPR, t = tid % TPR;
+  const uint32_t nch = p.cols >> 3;
+  const uint32_t row0 = (blockIdx.x * NG + uint32_t(grp)) * RR;
+  uint32_t cc[CPT];
+#pragma unroll
+  for (int k = 0; k < CPT; k++) cc[k] = min(uint32_t(t) + uint32_t(TPR) * k, nch - 1);
+
+  const uint4* W = reinterpret_cast<const uint4*>(p.w);
+  uint4 wv[RR][CPT];
+#pragma unroll
+  for (int r = 0; r < RR; r++) {
+    const size_t row = min(row0 + uint32_t(r), p.rows - 1);
+#pragma unroll
+    for (int k = 0; k < CPT; k++) wv[r][k] = W[row * nch + cc[k]];
+  }
+  const float4* X = reinterpret_cast<const float4*>(p.x);
+  float4 xa[NV][CPT], xb[NV][CPT];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      xa[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k]];
+      xb[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k] + 1];
+    }
+  }
+  uint4 gains[CPT];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int k = 0; k < CPT; k++) gains[k] = reinterpret_cast<const uint4*>(p.gain)[cc[k]];
+  }
+  float res[NV][RR];
+  if constexpr (EPI == kGemmResAdd) {
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+      for (int r = 0; r < RR; r++) res[v][r] = p.out[size_t(v) * p.ldo + min(row0 + uint32_t(r), p.rows - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  if (uint32_t(TPR) * CPT > nch) {  // chunks past the row end contribute 0
+#pragma unroll
+    for (int k = 0; k < CPT; k++) {
+      // component-wise: a ternary between float4 objects selects their addresses and sends the
+      // arrays to scratch memory
+      const bool in = uint32_t(t) + uint32_t(TPR) * k < nch;
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const float4 a = xa[v][k], b = xb[v][k];
+        xa[v][k] = make_float4(in ? a.x : 0.f, in ? a.y : 0.f, in ? a.z : 0.f, in ? a.w : 0.f);
+        xb[v][k] = make_float4(in ? b.x : 0.f, in ? b.y : 0.f, in ? b.z : 0.f, in ? b.w : 0.f);
+      }
+    }
+  }
+  float ss[NV];
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    ss[v] = 0.f;
+    if constexpr (NORM) {
+#pragma unroll
+      for (int k = 0; k < CPT; k++) {
+        const float4 a = xa[v][k], b = xb[v][k];
+        ss[v] += (a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w) + (b.x * b.x + b.y * b.y + b.z * b.z + b.w * b.w);
+        const uint4 g = gains[k];
+        xa[v][k] = make_float4(a.x * __uint_as_float(g.x << 16), a.y * __uint_as_float(g.x & 0xFFFF0000u),
+                               a.z * __uint_as_float(g.y << 16), a.w * __uint_as_float(g.y & 0xFFFF0000u));
+        xb[v][k] = make_float4(b.x * __uint_as_float(g.z << 16), b.y * __uint_as_float(g.z & 0xFFFF0000u),
+                               b.z * __uint_as_float(g.w << 16), b.w * __uint_as_float(g.w & 0xFFFF0000u));
+      }
+      ss[v] = wave_sum(ss[v]);
+    }
+  }
+  float acc[NV][RR];
+#pragma unroll
+  for (int v = 0; v < NV; v++)
+#pragma unroll
+    for (int r = 0; r < RR; r++) {
+      float a = 0.f;
+#pragma unroll
+      for (int k = 0; k < CPT; k++) a = dot8(wv[r][k], xa[v][k], xb[v][k], a);
+      acc[v][r] = wave_sum(a);
+    }
+  if constexpr (WPG > 1) {
+    if (lane == 0) {
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+#pragma unroll
+        for (int r = 0; r < RR; r++) red[wave][v * (RR + 1) + r] = acc[v][r];
+        red[wave][v * (RR + 1) + RR] = ss[v];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+      for (int r = 0; r <= RR; r++) {
+        float a = 0.f;
+#pragma unroll
+        for (int w = 0; w < WPG; w++) a += red[grp * WPG + w][v * (RR + 1) + r];
+        if (r < RR) acc[v][r] = a;
+        else ss[v] = a;
+      }
+  }
+  if (t != 0) return;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    float sc = 1.f;
+    if constexpr (NORM) sc = 1.0f / sqrtf(ss[v] / float(p.cols) + p.eps);
+    float* o = p.out + size_t(v) * p.ldo;
+    if constexpr (EPI == kGemmSiluPair) {
+#pragma unroll
+      for (int r = 0; r + 1 < RR; r += 2) {
+        const uint32_t row = row0 + uint32_t(r);
+        if (row + 1 < p.rows) {
+          const float g = acc[v][r] * sc;
+          o[row >> 1] = g / (1.0f + expf(-g)) * (acc[v][r + 1] * sc);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < RR; r++) {
+        const uint32_t row = row0 + uint32_t(r);
+        if (row < p.rows) o[row] = EPI == kGemmResAdd ? res[v][r] + acc[v][r] * sc : acc[v][r] * sc;
+      }
+    }
+  }
+}
+
+template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI>
+hipError_t launch_mv_rows_t(const MvRowsParams& p, hipStream_t st) {
+  constexpr int rows_per_block = (256 / TPR) * RR;
+  hipLaunchKernelGGL((k_mv_rows<TPR, CPT, RR, NV, NORM, EPI>), dim3(ceil_div(p.rows, rows_per_block)), dim3(256), 0,
+                     st, p);
+  return hipGetLastError();
+}
+
+// the decode matvec's shapes: an exact fit of threads x chunks where one exists; silu rows pair up
+template <int NV, bool NORM, int EPI>
+hipError_t launch_mv_rows_cols(const MvRowsParams& p, hipStream_t st) {
+  const uint32_t nch = p.cols / 8;
+  constexpr bool SILU = EPI == kGemmSiluPair;
+  if (nch <= 64) return launch_mv_rows_t<64, 1, 2, NV, NORM, EPI>(p, st);
+  if (nch <= 128) {
+    if (SILU) return launch_mv_rows_t<64, 2, 2, NV, NORM, EPI>(p, st);
+    return launch_mv_rows_t<128, 1, 2, NV, NORM, EPI>(p, st);
+  }
+  if (nch <= 256) return launch_mv_rows_t<256, 1, SILU ? 2 : 1, NV, NORM, EPI>(p, st);
+  if (nch == 384) return launch_mv_rows_t<128, 3, 2, NV, NORM, EPI>(p, st);
+  if (nch <= 512) return launch_mv_rows_t<256, 2, SILU ? 2 : 1, NV, NORM, EPI>(p, st);
+  return hipErrorInvalidValue;
+}
+
+template <int NV>
+hipError_t launch_mv_rows_nv(const MvRowsParams& p, bool norm, int epi, hipStream_t st) {
+  if (norm && epi == kGemmStore) return launch_mv_rows_cols<NV, true, kGemmStore>(p, st);
+  if (norm && epi == kGemmSiluPair) return launch_mv_rows_cols<NV, true, kGemmSiluPair>(p, st);
+  if (!norm && epi == kGemmResAdd) return launch_mv_rows_cols<NV, false, kGemmResAdd>(p, st);
+  if (!norm && epi == kGemmStore) return launch_mv_rows_cols<NV, false, kGemmStore>(p, st);
+  return hipErrorInvalidValue;
+}
+
 }  // namespace
+
+hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st) {
+  if (!p.w || !p.x || !p.out || (norm && !p.gain) || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||
+      p.cols % 8 || p.cols / 8 > 512 || (epi == kGemmSiluPair ? p.rows % 2 || p.ldo < p.rows / 2 : p.ldo < p.rows))
+    return hipErrorInvalidValue;
+  switch (p.M) {
+    case 1: return launch_mv_rows_nv<1>(p, norm, epi, st);
+    case 2: return launch_mv_rows_nv<2>(p, norm, epi, st);
+    case 3: return launch_mv_rows_nv<3>(p, norm, epi, st);
+    default: return launch_mv_rows_nv<4>(p, norm, epi, st);
+  }
+}
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st) {
   if (M == 0 || K % 4) return hipErrorInvalidValue;

@@ -92,6 +92,9 @@ struct qe_model {
   uint64_t weight_bytes = 0;
   // decode attention launches also load the next weights into L2 (QE_L2_PREFETCH=0 turns it off)
   bool l2_prefetch = true;
+  // verify passes and chunks of up to kMvRowsMaxM tokens run their projections as multi-row
+  // matvecs (QE_MV_ROWS=0: on the skinny GEMM)
+  bool mv_rows = true;
   // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
@@ -196,6 +199,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (rc != QE_OK) return fail(rc, "%s", err.c_str());
   m->cfg = m->ckpt.config();
   if (const char* pf = getenv("QE_L2_PREFETCH")) m->l2_prefetch = strcmp(pf, "0") != 0;
+  if (const char* mr = getenv("QE_MV_ROWS")) m->mv_rows = strcmp(mr, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
   const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
@@ -510,16 +514,25 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
   // residuals in its epilogue. Past that, m->bs holds the row scales of the current norm input:
   // from a rownorm launch for layer 0, then from the reduction that finishes each split o_proj /
   // down (residual add + the next norm's scales in one pass).
+  // Up to kMvRowsMaxM rows the projections are matvecs over the M token rows: each weight is
+  // loaded once per pass, the norm is computed per row in the kernel and the residual is added in
+  // its epilogue (the lm_head of a verify stays on the skinny GEMM).
   const bool skinny = M <= qe::kGemmSkinnyMaxM;
+  const bool mv = m->mv_rows && M <= qe::kMvRowsMaxM;
   auto gemm = [&](const float* A, uint32_t lda, const uint16_t* gain, const uint16_t* W, uint32_t N, uint32_t K,
                   float* C, uint32_t ldc, int epi) -> int {
+    if (mv && lda == K && W != m->lm_head) {
+      qe::MvRowsParams r{W, A, gain, C, M, N, K, ldc, eps};
+      HIP_TRY(qe::launch_mv_rows(r, gain != nullptr, epi, s));
+      return QE_OK;
+    }
     qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc, eps};
     HIP_TRY(qe::launch_gemm(g, gain != nullptr, epi, s));
     return QE_OK;
   };
   // x += A W^T, then m->bs = the row scales of the updated x
   auto gemm_resadd = [&](const float* A, uint32_t lda, const uint16_t* W, uint32_t K) -> int {
-    if (skinny && qe::gemm_splits(M, H, K) == 1) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
+    if (mv || (skinny && qe::gemm_splits(M, H, K) == 1)) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
     if (!skinny && K % 64) {  // no split: residual epilogue, then the row scales
       if (int rc2 = gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd)) return rc2;
       HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));

@@ -50,7 +50,8 @@ def test_gemm_matches_float64(gpu, m, n, k):
     assert np.all(np.abs(got - ref) <= bound), f"max excess {np.max(np.abs(got - ref) / bound)}"
 
 
-@pytest.mark.parametrize("n_prompt,chunk", [(1, 0), (100, 32), (300, 0), (513, 512), (700, 2048)])
+# chunks of up to 4 tokens run their projections as multi-row matvecs (11 in chunks of 4: 4, 4, 3)
+@pytest.mark.parametrize("n_prompt,chunk", [(1, 0), (11, 4), (100, 32), (300, 0), (513, 512), (700, 2048)])
 def test_tiny_prefill_batch_matches_oracle(gpu, tiny_ckpt, n_prompt, chunk):
     m = qe.Model.load_model(tiny_ckpt)
     om = oracle.Model(tiny_ckpt)
@@ -75,8 +76,13 @@ def test_tiny_prefill_batch_matches_oracle(gpu, tiny_ckpt, n_prompt, chunk):
         assert toks[i] == tok
 
 
-@pytest.mark.parametrize("k", [1, 4, 17])
-def test_tiny_verify_matches_oracle(gpu, tiny_ckpt, k):
+# k <= 4: the projections are multi-row matvecs over the k token rows; k = 5, 9, 17: the skinny
+# GEMM; "skinny": k = 4 with the multi-row matvec switched off
+@pytest.mark.parametrize("k,path", [(1, "rows"), (2, "rows"), (3, "rows"), (4, "rows"), (5, "rows"), (9, "rows"),
+                                    (17, "rows"), (4, "skinny")])
+def test_tiny_verify_matches_oracle(gpu, tiny_ckpt, k, path, monkeypatch):
+    if path == "skinny":
+        monkeypatch.setenv("QE_MV_ROWS", "0")  # read when the model loads
     m = qe.Model.load_model(tiny_ckpt)
     om = oracle.Model(tiny_ckpt)
     prefix = qe.random_prompt(31, 40, TINY.vocab_size)
@@ -168,7 +174,7 @@ def test_real_prefill_batch_then_decode_matches_fixture(gpu, real_ckpt):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("k", [4, 20])
+@pytest.mark.parametrize("k", [2, 3, 4, 20])
 def test_real_verify_matches_fixture(gpu, real_ckpt, k):
     """verify of the greedy continuation: row i is the oracle's logits after token i + 1"""
     import os
