@@ -151,7 +151,9 @@ uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, ui
  *      events. Writes, per stage, the mean duration of one launch in microseconds to us_out,
  *      the launches per decode step to launches_out (nullable) and the stage name (a static
  *      string) to names_out (nullable); *n_out = stages written. The replays leave the cache's
- *      step state advanced; the next forward/prefill/decode call resets it. No reference
+ *      step state advanced; the next forward/prefill/decode call resets it. The stage
+ *      "qkv+attention" times each layer's q|k|v and attention launches together (2 per layer),
+ *      so that the attention's time behind its producer is that minus the "qkv" stage's. No reference
  *      counterpart: the reference timed kernels by removing them by hand (README.md:64-71). ---- */
 int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out,
                     uint32_t* launches_out, const char** names_out, uint32_t max_stages, uint32_t* n_out);

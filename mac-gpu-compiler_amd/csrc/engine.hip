@@ -375,8 +375,12 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
   hipStream_t s = m->stream;
+  // `only` names one stage, or "qkv+attention" for each layer's q|k|v and attention launches
+  // (the attention then runs behind its producer, as in the step)
+  const bool pair = only && strcmp(only, "qkv+attention") == 0;
   auto want = [&](const char* name) {
-    const bool w = !only || strcmp(only, name) == 0;
+    const bool w = !only || strcmp(only, name) == 0 ||
+                   (pair && (strcmp(name, "qkv") == 0 || strcmp(name, "attention") == 0));
     if (w && launches) ++*launches;
     return w;
   };
@@ -790,7 +794,9 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   // then each stage alone: a graph of its launches (28 per-layer launches, or the one lm_head /
   // argmax), replayed kReps times between two events; argmax replays advance the step state,
   // which the next call's set_state resets
-  static const char* const kStages[] = {"embed", "qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"};
+  // (the pair before argmax, whose replays advance the position that attention reads)
+  static const char* const kStages[] = {"qkv",  "attention", "qkv+attention", "o_proj",
+                                        "gate_up", "down",   "lm_head",       "argmax"};
   constexpr int kReps = 8;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   HIP_TRY(hipEventCreate(&e0));

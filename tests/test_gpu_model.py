@@ -108,6 +108,27 @@ def test_prefill_equals_forward_loop(gpu, tiny_ckpt):
     np.testing.assert_array_equal(a, b)
 
 
+def test_profile_step_stages_and_next_step(gpu, tiny_ckpt):
+    """qe_profile_step times every stage (and each layer's q|k|v + attention pair) and leaves a
+    cache from which the next forward still matches the oracle"""
+    m = qe.Model.load_model(tiny_ckpt)
+    om = oracle.Model(tiny_ckpt)
+    prompt = qe.random_prompt(19, 9, TINY.vocab_size)
+    c = qe.KVCache(m, 16)
+    m.prefill(prompt[:8], 0, c, want_logits=False)
+    stages = {name: (us, n) for name, us, n in m.profile_step(int(prompt[8]), 8, c)}
+    L = TINY.num_hidden_layers
+    assert set(stages) == {"qkv", "attention", "qkv+attention", "o_proj", "gate_up", "down", "lm_head", "argmax"}
+    assert stages["qkv+attention"][1] == 2 * L and stages["attention"][1] == L
+    assert all(us > 0 for us, _ in stages.values())
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        om.forward(int(tok), pos, oc)
+    ref = om.forward(3, 9, oc)
+    got = m.forward(3, 9, c)
+    assert float(np.max(np.abs(got - ref))) < MAX_ABS_DIFF
+
+
 def test_position_contract(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 4)
