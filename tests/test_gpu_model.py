@@ -129,6 +129,26 @@ def test_profile_step_stages_and_next_step(gpu, tiny_ckpt):
     assert float(np.max(np.abs(got - ref))) < MAX_ABS_DIFF
 
 
+@pytest.mark.parametrize("env", [{"QE_L2_PREFETCH": "0"}, {"QE_LAUNCH": "eager"}])
+def test_switches_change_no_result(gpu, tiny_ckpt, env, monkeypatch):
+    """the L2 weight prefetch and graph replay change timing only: the same tokens and bit-identical
+    logits as the default path"""
+    prompt = qe.random_prompt(23, 12, TINY.vocab_size)
+
+    def run():
+        m = qe.Model.load_model(tiny_ckpt)  # QE_L2_PREFETCH is read here
+        c = qe.KVCache(m, 48)               # QE_LAUNCH here
+        first = oracle.argmax(m.prefill(prompt, 0, c))
+        return m.decode(first, len(prompt), 30, c, want_logits=True)
+
+    toks0, logits0 = run()
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    toks1, logits1 = run()
+    assert list(toks1) == list(toks0)
+    np.testing.assert_array_equal(logits1, logits0)
+
+
 def test_position_contract(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 4)
