@@ -92,7 +92,8 @@ uint64_t qe_kv_len(const qe_kv* kv);
 int qe_forward(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* logits_out);
 
 /* ---- prefill: the prompt loop of bench.rs:174-176 (one forward per token). Writes the last
- *      position's logits to last_logits (nullable). ---- */
+ *      position's logits to last_logits (nullable). n = 0 does nothing: last_logits and the
+ *      cache are left as they were. ---- */
 int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv,
                float* last_logits);
 
@@ -100,7 +101,7 @@ int qe_prefill(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_
  *      start_pos; each step's GPU argmax (lowest index on ties, main.rs:37-42) feeds the next
  *      step on the device. on_token (nullable) is called with each step's token as the step
  *      finishes. If logits_per_step is not NULL it receives steps*vocab_size floats (slower:
- *      one device-to-host copy per step; meant for parity tests). ---- */
+ *      one device-to-host copy per step; meant for parity tests). steps = 0 does nothing. ---- */
 int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv,
               qe_on_token on_token, void* user, float* logits_per_step);
 
@@ -111,7 +112,7 @@ int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t step
  * activations split into two bf16 halves (about 16 mantissa bits), causal attention over the
  * cache and the chunk. Appends the K/V of every position and writes the last token's logits
  * (nullable). Same position contract as qe_prefill; logits agree with it within 1e-2, not bit for
- * bit. The model's chunk buffers are allocated on first use. */
+ * bit. The model's chunk buffers are allocated on first use. n = 0 does nothing. */
 int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv,
                      uint32_t chunk, float* last_logits);
 /* Verify k (1..64) tokens at positions start_pos.. in one pass (the k-token check of speculative

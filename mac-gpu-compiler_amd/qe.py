@@ -245,10 +245,10 @@ class Model:
 
     def prefill(self, ids, start_pos: int, cache: "KVCache", want_logits: bool = True) -> Optional[np.ndarray]:
         arr = np.ascontiguousarray(np.asarray(ids, dtype=np.uint32))
-        out = np.empty(self._cfg.vocab_size, dtype=np.float32) if want_logits else None
+        out = np.empty(self._cfg.vocab_size, dtype=np.float32) if want_logits and arr.size else None
         _check(lib().qe_prefill(self._h, arr.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), arr.size, int(start_pos),
                                 cache._h, _fptr(out) if out is not None else None))
-        return out
+        return out  # None for an empty prompt: there are no logits
 
     def profile_step(self, token: int, pos: int, cache: "KVCache"):
         """Runs `token` at `pos`, then times every stage of the step as a graph of that stage's
@@ -265,10 +265,10 @@ class Model:
     def prefill_batch(self, ids, start_pos: int, cache: "KVCache", chunk: int = 0, want_logits: bool = True):
         """Chunked prefill on the matrix cores (qe_prefill_batch): the last token's logits or None."""
         ids = np.ascontiguousarray(ids, dtype=np.uint32)
-        out = np.empty(self.config().vocab_size, dtype=np.float32) if want_logits else None
+        out = np.empty(self.config().vocab_size, dtype=np.float32) if want_logits and len(ids) else None
         _check(lib().qe_prefill_batch(self._h, ids.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ids),
-                                      int(start_pos), cache._h, int(chunk), _fptr(out) if want_logits else None))
-        return out
+                                      int(start_pos), cache._h, int(chunk), _fptr(out) if out is not None else None))
+        return out  # None for an empty prompt: there are no logits
 
     def verify(self, ids, start_pos: int, cache: "KVCache") -> np.ndarray:
         """k tokens in one pass (qe_verify): logits [k, vocab]."""

@@ -149,6 +149,24 @@ def test_switches_change_no_result(gpu, tiny_ckpt, env, monkeypatch):
     np.testing.assert_array_equal(logits1, logits0)
 
 
+def test_empty_inputs_do_nothing(gpu, tiny_ckpt):
+    """an empty prompt and a zero-step decode leave the cache as it was; a one-position cache
+    holds exactly one forward"""
+    m = qe.Model.load_model(tiny_ckpt)
+    c = qe.KVCache(m, 8)
+    assert m.prefill([], 0, c) is None and len(c) == 0
+    assert m.prefill_batch(np.zeros(0, dtype=np.uint32), 0, c) is None and len(c) == 0
+    toks, logits = m.decode(1, 0, 0, c, want_logits=True)
+    assert list(toks) == [] and logits.shape == (0, TINY.vocab_size) and len(c) == 0
+    one = qe.KVCache(m, 1)
+    a = m.forward(5, 0, one)
+    om = oracle.Model(tiny_ckpt)
+    assert float(np.max(np.abs(a - om.forward(5, 0, om.new_cache())))) < MAX_ABS_DIFF
+    with pytest.raises(qe.QeError) as e:
+        m.decode(oracle.argmax(a), 1, 1, one)  # no room for a second position
+    assert e.value.code == qe.QE_ERR_POS
+
+
 def test_position_contract(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 4)
