@@ -523,6 +523,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
+        # what the kernels do with that type: the weights stream as bf16 and are unpacked exactly to
+        # f32 (cpu_inference.rs:182-183), and every product, sum, norm and softmax runs in f32
+        "arithmetic": "bf16 weights, f32 activations, f32 FMA and accumulation; KV cache " + args.kv,
         "data": "synthetic",
         "config": {
             "workload": f"Qwen3-0.6B-architecture decoder, seeded random-init bf16 weights (seed {SEED}), "
