@@ -79,12 +79,13 @@ def build_cli(verbose: bool = False) -> str:
 
 
 
-PMC_SRCS = ["qe_stage_pmc.hip", "kernels.hip", "attention.hip"]
+PMC_SRCS = ["qe_stage_pmc.hip", "kernels.hip", "attention.hip", "batch.hip"]
 PMC = os.path.join(PKG, "qe_stage_pmc")
 
 
 def build_stage_pmc(verbose: bool = False) -> str:
-    """qe_stage_pmc: each decode-step kernel on synthetic inputs, for counter collection."""
+    """qe_stage_pmc: each decode-step kernel (or, with --gemm, the prefill GEMM) on synthetic
+    inputs, for counter collection."""
     tmp = PMC + ".tmp"
     flags = [f for f in HIPCC_FLAGS if f not in ("-fPIC", "-shared")]
     cmd = [hipcc(), *flags, "-I", os.path.join(ROOT, "include"), "-o", tmp,

@@ -6,11 +6,16 @@
 // the attention launch's L2 prefetch of the layer's gate/up and down weights.
 //
 //   qe_stage_pmc [--pos P] [--no-prefetch]   (attention attends positions 0..P, default 193)
+//   qe_stage_pmc --gemm   the chunked prefill's GEMM (k_gemm_tile) instead, 3 launches at each of
+//                         M x N x K = 2048 x 4096 x 1024 (q|k|v of a 2048-token chunk) and
+//                         512 x 6144 x 1024 (gate|up of a 512-token chunk), for the matrix-core
+//                         counters (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, ...)
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <vector>
 
+#include "batch.h"
 #include "kernels.h"
 
 namespace {
@@ -52,10 +57,34 @@ T* dalloc(size_t n) {
 
 int main(int argc, char** argv) {
   uint32_t pos = 193;
-  bool prefetch = true;
+  bool prefetch = true, gemm = false;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
     else if (!strcmp(argv[i], "--no-prefetch")) prefetch = false;
+    else if (!strcmp(argv[i], "--gemm")) gemm = true;
+  }
+  if (gemm) {
+    CK(hipSetDevice(0));
+    hipStream_t gs;
+    CK(hipStreamCreate(&gs));
+    const uint32_t shapes[2][3] = {{2048, 4096, 1024}, {512, 6144, 1024}};
+    for (const auto& sh : shapes) {
+      const uint32_t M = sh[0], N = sh[1], K = sh[2];
+      float* A = dalloc<float>(size_t(M) * K);
+      uint16_t* W = dalloc<uint16_t>(size_t(N) * K);
+      float* C = dalloc<float>(size_t(M) * N);
+      k_fill_f32<<<1024, 256, 0, gs>>>(A, size_t(M) * K, 0.5f);
+      // bf16 pairs (0, 0.0078125): any finite values give the same matrix-core work
+      k_fill_f32<<<1024, 256, 0, gs>>>(reinterpret_cast<float*>(W), size_t(N) * K / 2, 0.0078125f);
+      const qe::GemmParams g{A, K, nullptr, nullptr, W, M, N, K, C, N, 1e-6f};
+      for (int r = 0; r < 3; r++) CK(qe::launch_gemm(g, false, qe::kGemmStore, gs));
+      CK(hipStreamSynchronize(gs));
+      CK(hipFree(A));
+      CK(hipFree(W));
+      CK(hipFree(C));
+      std::printf("gemm %u x %u x %u: 3 launches\n", M, N, K);
+    }
+    return 0;
   }
   const uint32_t H = 1024, I = 3072, V = 151936, NH = 16, NKV = 8, D = qe::kHeadDim, G = NH / NKV;
   const uint32_t QD = NH * D, KD = NKV * D, max_seq = 258;
