@@ -66,6 +66,8 @@ def lib() -> ctypes.CDLL:
         "or_tensor_info": (ctypes.c_int, [vp, sz, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_char_p),
                                           ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int64)]),
         "or_kv_new": (vp, [vp]),
+        "or_kv_new_bf16": (vp, [vp]),
+        "or_round_bf16": (ctypes.c_float, [ctypes.c_float]),
         "or_kv_free": (None, [vp]),
         "or_kv_len": (sz, [vp]),
         "or_forward": (ctypes.c_int, [vp, ctypes.c_uint32, sz, vp, f32p]),
@@ -134,8 +136,10 @@ class Model:
     def kv_bytes_at(self, pos: int) -> int:
         return int(lib().or_kv_bytes_at(ctypes.byref(self._c), pos))
 
-    def new_cache(self) -> "KVCache":
-        return KVCache(self)
+    def new_cache(self, bf16: bool = False) -> "KVCache":
+        """An f32 cache (KVCache::new), or with bf16=True one that rounds every appended K/V
+        element to bf16 (nearest, ties to even) and attends with the rounded values."""
+        return KVCache(self, bf16)
 
     def forward(self, token: int, pos: int, cache: "KVCache") -> np.ndarray:
         out = np.empty(self.config["vocab_size"], dtype=np.float32)
@@ -157,9 +161,11 @@ class Model:
 
 
 class KVCache:
-    def __init__(self, model: Model):
-        self._h = ctypes.c_void_p(lib().or_kv_new(model._h))
+    def __init__(self, model: Model, bf16: bool = False):
+        new = lib().or_kv_new_bf16 if bf16 else lib().or_kv_new
+        self._h = ctypes.c_void_p(new(model._h))
         self._model = model
+        self.bf16 = bool(bf16)
 
     def __len__(self):
         return int(lib().or_kv_len(self._h))
@@ -174,6 +180,13 @@ class KVCache:
 def argmax(x: np.ndarray) -> int:
     x = np.ascontiguousarray(x, dtype=np.float32)
     return int(lib().or_argmax(f32p(x), x.size))
+
+
+def round_bf16(x) -> np.ndarray:
+    """Element-wise f32 -> nearest bf16 (ties to even), widened back to f32 (or_round_bf16)."""
+    a = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    f = lib().or_round_bf16
+    return np.array([f(float(v)) for v in a], dtype=np.float32).reshape(np.shape(x))
 
 
 def set_threads(n: int) -> None:

@@ -277,6 +277,7 @@ struct or_model {
 
 struct or_kvcache {
   size_t layers, kv_dim, len, cap;   /* len = cached positions */
+  int bf16;                          /* append K/V rounded to bf16 (or_kv_new_bf16) */
   float** k;
   float** v;
 };
@@ -620,11 +621,34 @@ void or_matvec(float* out, const uint16_t* w, const float* x, size_t rows, size_
 
 or_kvcache* or_kv_new(const or_model* m) {
   or_kvcache* c = calloc(1, sizeof(*c));
+  c->bf16 = 0;
   c->layers = m->cfg.num_hidden_layers;
   c->kv_dim = m->cfg.num_key_value_heads * m->cfg.head_dim;
   c->k = calloc(c->layers ? c->layers : 1, sizeof(float*));
   c->v = calloc(c->layers ? c->layers : 1, sizeof(float*));
   return c;
+}
+
+/* A cache that keeps each appended K/V element rounded to bf16 (round to nearest, ties to even)
+ * and attends with the rounded values. The reference has no such cache on its main branch
+ * (README.md:23,90 reports one only as an experiment); this mode states that rounding exactly so
+ * a bf16 device cache has something independent to be compared with. */
+or_kvcache* or_kv_new_bf16(const or_model* m) {
+  or_kvcache* c = or_kv_new(m);
+  c->bf16 = 1;
+  return c;
+}
+
+/* f32 -> nearest bf16 value (ties to even), returned widened back to f32. NaN stays NaN (quiet),
+ * values past the largest bf16 round to infinity as IEEE rounding does. */
+float or_round_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) u = (u | 0x00400000u) & 0xFFFF0000u;
+  else u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
 }
 
 void or_kv_free(or_kvcache* c) {
@@ -732,7 +756,9 @@ int or_forward(const or_model* m, uint32_t token, size_t pos, or_kvcache* cache,
     /* :134-138 per-head q/k rmsnorm, then rope */
     for (size_t h = 0; h < c->num_attention_heads; h++) { or_rmsnorm_inplace(q + h * hd, wqn, hd, eps); or_rope(q + h * hd, hd, pos, c->rope_theta); }
     for (size_t h = 0; h < c->num_key_value_heads; h++) { or_rmsnorm_inplace(k + h * hd, wkn, hd, eps); or_rope(k + h * hd, hd, pos, c->rope_theta); }
-    /* :140-142 append */
+    /* :140-142 append (a bf16 cache stores, and later attends with, the rounded values) */
+    if (cache->bf16)
+      for (size_t i = 0; i < kv_dim; i++) { k[i] = or_round_bf16(k[i]); v[i] = or_round_bf16(v[i]); }
     memcpy(cache->k[l] + pos * kv_dim, k, kv_dim * sizeof(float));
     memcpy(cache->v[l] + pos * kv_dim, v, kv_dim * sizeof(float));
     /* :144-162 */

@@ -59,6 +59,12 @@ int or_tensor_info(const or_model* m, size_t i, const char** name, const char** 
 
 /* cpu_inference.rs:50-55 KVCache::new */
 or_kvcache* or_kv_new(const or_model* m);
+/* The same cache, but every appended K/V element is rounded to bf16 (nearest, ties to even) and
+ * attention reads the rounded values: the semantics of a bf16 KV cache, which the reference has
+ * only as an experiment (README.md:23,90). */
+or_kvcache* or_kv_new_bf16(const or_model* m);
+/* f32 -> nearest bf16 (ties to even), widened back to f32; NaN stays a quiet NaN */
+float or_round_bf16(float f);
 void or_kv_free(or_kvcache* c);
 size_t or_kv_len(const or_kvcache* c);
 

@@ -191,3 +191,40 @@ def test_kv_bytes_formula():
     c = oracle._Cfg(1024, 3072, 28, 16, 8, 128, 151936, 1e-6, 1e6, 0)
     assert L.or_kv_bytes_at(ctypes.byref(c), 0) == 229376
     assert L.or_kv_bytes_at(ctypes.byref(c), 257) == 229376 * 258
+
+
+def _bf16_round_f64(u32: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even to bf16 from the definition: the two bf16 neighbours of x (its upper
+    16 bits truncated, and the next value away from zero), the closer one in float64, the one with
+    an even last bit on a tie."""
+    x = u32.view(np.float32).astype(np.float64)
+    lo_bits = (u32 & 0xFFFF0000).astype(np.uint32)
+    hi_bits = (lo_bits.astype(np.uint64) + 0x10000).astype(np.uint32)
+    lo = lo_bits.view(np.float32).astype(np.float64)
+    hi = hi_bits.view(np.float32).astype(np.float64)  # callers pass values below the overflow boundary
+    dlo, dhi = np.abs(x - lo), np.abs(hi - x)
+    even_lo = ((lo_bits >> 16) & 1) == 0
+    pick_hi = (dhi < dlo) | ((dhi == dlo) & ~even_lo)
+    return np.where(pick_hi, hi_bits, lo_bits).astype(np.uint32)
+
+
+def test_round_bf16_definition_and_torch():
+    """or_round_bf16 (the oracle's bf16 KV cache rounding): nearest bf16, ties to even, against
+    the float64 definition and against torch's float32 -> bfloat16 conversion, on every bf16
+    value with the low halves that decide rounding (0, just below / at / just above the tie,
+    all ones), plus random patterns; NaN stays NaN"""
+    torch = pytest.importorskip("torch")
+    hi = np.arange(65536, dtype=np.uint32) << 16
+    lows = np.array([0x0000, 0x0001, 0x7FFF, 0x8000, 0x8001, 0xFFFF], dtype=np.uint32)
+    u = (hi[:, None] | lows[None, :]).ravel()
+    u = np.concatenate([u, np.random.default_rng(3).integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32)])
+    got = np.array([oracle.lib().or_round_bf16(float(v)) for v in u.view(np.float32)], np.float32).view(np.uint32)
+    ref_t = torch.from_numpy(u.view(np.float32).copy()).to(torch.bfloat16).to(torch.float32).numpy().view(np.uint32)
+    nan = np.isnan(u.view(np.float32))
+    assert np.all(np.isnan(got.view(np.float32)[nan]))
+    np.testing.assert_array_equal(got[~nan], ref_t[~nan])
+    finite = np.isfinite(u.view(np.float32)) & (np.abs(u.view(np.float32)) < 3.3e38)
+    np.testing.assert_array_equal(got[finite], _bf16_round_f64(u[finite]))
+    # ties go to the even neighbour in both directions
+    assert oracle.lib().or_round_bf16(1.0 + 2.0 ** -8) == 1.0
+    assert oracle.lib().or_round_bf16(1.0 + 3 * 2.0 ** -8) == 1.0 + 2.0 ** -6
