@@ -149,12 +149,14 @@ uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, ui
 /* ---- per-stage kernel timing: runs `token` at `pos` like qe_forward, then times each stage
  *      of the step (qkv, attention, o_proj, gate_up, down, lm_head, argmax) as a graph of that
  *      stage's launches only (28 per-layer launches, or one), replayed 8 times between two HIP
- *      events. Writes, per stage, the mean duration of one launch in microseconds to us_out,
- *      the launches per decode step to launches_out (nullable) and the stage name (a static
- *      string) to names_out (nullable); *n_out = stages written. The replays leave the cache's
- *      step state advanced; the next forward/prefill/decode call resets it. The stage
- *      "qkv+attention" times each layer's q|k|v and attention launches together (2 per layer),
- *      so that the attention's time behind its producer is that minus the "qkv" stage's. No reference
+ *      events, each stage from the step state of `pos`. Writes, per stage, the mean duration of
+ *      one launch in microseconds to us_out, the launches per decode step to launches_out
+ *      (nullable) and the stage name (a static string) to names_out (nullable); *n_out = stages
+ *      written. The stage "qkv+attention" times each layer's q|k|v and attention launches together
+ *      (2 per layer), so that the attention's time behind its producer is that minus the "qkv"
+ *      stage's. A cache of fewer than 9 positions skips the argmax stage (its replays advance the
+ *      token ring). Afterwards the step is run once more, so the cache holds what qe_forward(token,
+ *      pos) leaves; a kernel error raised by any replay is returned as QE_ERR_KERNEL. No reference
  *      counterpart: the reference timed kernels by removing them by hand (README.md:64-71). ---- */
 int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out,
                     uint32_t* launches_out, const char** names_out, uint32_t max_stages, uint32_t* n_out);
@@ -189,6 +191,12 @@ uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint6
 int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
                     uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,
                     void* work, void* stream);
+/* Greedy token of each of `rows` logit rows of n floats (device memory, row-major): the argmax
+ * of main.rs:37-42 -- the first maximum wins (lowest index on ties, -0.0 ties +0.0), NaN entries
+ * never win, a NaN at index 0 gives 0, and a row with nothing above -inf gives 0. tokens_out:
+ * `rows` uint32 in device memory. The verify pass's device argmax (qe_verify_greedy) runs this
+ * kernel. */
+int qe_op_argmax(const float* logits, uint64_t rows, uint64_t n, uint32_t* tokens_out, void* stream);
 /* Streaming read of n floats (n % 4 == 0): the read_sum kernel of tests/read_bandwidth.rs:16-54,
  * writing one partial sum per block to partial[grid]. grid == 0 picks a default. */
 int qe_op_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream);

@@ -322,6 +322,15 @@ int Checkpoint::open(const std::string& path, std::string& err) {
     err = "safetensors data section is not 2-byte aligned";
     return QE_ERR_FORMAT;
   }
+  // every entry's byte range must lie in the data section, also for tensors the engine never
+  // loads: the byte formula (bench.rs:106-116) sums off1 - off0 over all of them
+  for (const auto& t : tensors_) {
+    if (t.off0 < 0 || t.off1 < t.off0 || uint64_t(t.off1) > data_len_) {
+      err = "tensor " + t.name + ": data_offsets [" + std::to_string(t.off0) + ", " + std::to_string(t.off1) +
+            ") are not a range inside the " + std::to_string(data_len_) + "-byte data section";
+      return QE_ERR_FORMAT;
+    }
+  }
   // cpu_inference.rs:80-81
   std::string cpath = sibling_config(path), text;
   if (!read_file(cpath, text)) {
@@ -361,7 +370,12 @@ const uint16_t* Checkpoint::bf16(const std::string& name, uint64_t numel, std::s
     return nullptr;
   }
   uint64_t n = 1;
-  for (int64_t d : t.shape) n *= uint64_t(d < 0 ? 0 : d);
+  bool wrapped = false;
+  for (int64_t d : t.shape) wrapped |= __builtin_mul_overflow(n, uint64_t(d < 0 ? 0 : d), &n);
+  if (wrapped) {
+    err = name + ": the shape's element count overflows 64 bits";
+    return nullptr;
+  }
   if (t.off0 < 0 || t.off1 < t.off0 || uint64_t(t.off1 - t.off0) / 2 != n || n != numel) {
     err = name + ": expected " + std::to_string(numel) + " elements";
     return nullptr;

@@ -19,6 +19,7 @@
 #include "batch.h"
 #include "checkpoint.h"
 #include "kernels.h"
+#include "status.h"
 
 using qe::ArgCand;
 using qe::AttnParams;
@@ -29,15 +30,34 @@ namespace {
 
 thread_local std::string g_err;
 
-int fail(int code, const char* fmt, ...) {
+int vfail(int code, const char* fmt, va_list ap) {
   char buf[1024];
-  va_list ap;
-  va_start(ap, fmt);
   vsnprintf(buf, sizeof(buf), fmt, ap);
-  va_end(ap);
   g_err = buf;
   return code;
 }
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vfail(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+}  // namespace
+
+namespace qe {
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vfail(code, fmt, ap);
+  va_end(ap);
+  return code;
+}
+}  // namespace qe
+
+namespace {
 
 #define HIP_TRY(expr)                                                                       \
   do {                                                                                      \
@@ -668,7 +688,9 @@ int check_err(qe_model* m) {
   if (e) {
     HIP_TRY(hipMemsetAsync(m->err, 0, 4, m->stream));
     HIP_TRY(hipStreamSynchronize(m->stream));
-    return fail(QE_ERR_KERNEL, "kernel error bits 0x%x (1: pos >= max_seq, 2: token >= vocab, 4: token ring full)", e);
+    return fail(QE_ERR_KERNEL,
+                "kernel error bits 0x%x (1: pos >= max_seq, 2: token >= vocab, 4: token ring full, "
+                "8: attention runs do not cover pos)", e);
   }
   return QE_OK;
 }
@@ -794,9 +816,10 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   if ((rc = check_err(model))) return rc;
   kv->len = pos + 1;
   // then each stage alone: a graph of its launches (28 per-layer launches, or the one lm_head /
-  // argmax), replayed kReps times between two events; argmax replays advance the step state,
-  // which the next call's set_state resets
-  // (the pair before argmax, whose replays advance the position that attention reads)
+  // argmax), replayed kReps times between two events. Every stage starts from the step state of
+  // `pos` (set_state), so its replays run at that position as the step did; the argmax replays
+  // each advance the token ring by one, which a cache of fewer than kReps + 2 positions cannot
+  // hold, so such a cache skips the argmax stage.
   static const char* const kStages[] = {"qkv",  "attention", "qkv+attention", "o_proj",
                                         "gate_up", "down",   "lm_head",       "argmax"};
   constexpr int kReps = 8;
@@ -806,6 +829,8 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   uint32_t n = 0;
   for (const char* stage : kStages) {
     if (he != hipSuccess || rc != QE_OK) break;
+    if (strcmp(stage, "argmax") == 0 && kv->tok_cap < uint32_t(kReps + 3)) continue;
+    if ((rc = set_state(model, kv, token, pos)) != QE_OK) break;
     uint32_t launches = 0;
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
@@ -835,9 +860,13 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   if (e1) (void)hipEventDestroy(e1);
   if (rc != QE_OK) return rc;
   if (he != hipSuccess) return fail(QE_ERR_HIP, "stage timing failed: %s", hipGetErrorString(he));
-  // argmax replays may leave ring/position error bits on this profiling state: clear them
-  HIP_TRY(hipMemsetAsync(model->err, 0, 4, model->stream));
-  HIP_TRY(hipStreamSynchronize(model->stream));
+  // a kernel error raised by any of the replays is reported like one of a step
+  if ((rc = check_err(model))) return rc;
+  // the stage replays ran on the activations the step left behind, so the K/V they wrote at pos
+  // are not the step's: run the step once more, which leaves the cache as qe_forward would
+  if ((rc = set_state(model, kv, token, pos))) return rc;
+  if ((rc = launch_step(model, kv, pos))) return rc;
+  if ((rc = check_err(model))) return rc;
   *n_out = n;
   return QE_OK;
 }
@@ -1140,6 +1169,13 @@ int qe_op_attention(const float* q, const float* k, const float* v, float* out, 
   uint64_t splits = n_splits ? n_splits : (n_pos + 63) / 64;
   splits = std::min<uint64_t>(std::max<uint64_t>(splits, 1), qe::kAttnMaxSplits);
   HIP_TRY(qe::launch_attention_op(a, uint32_t(splits), out, static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+int qe_op_argmax(const float* logits, uint64_t rows, uint64_t n, uint32_t* tokens_out, void* stream) {
+  if (!logits || !tokens_out) return fail(QE_ERR_ARG, "null argument");
+  if (rows == 0 || n == 0 || rows > 0x7FFFFFFFull || n > 0x7FFFFFFFull) return fail(QE_ERR_ARG, "need 0 < rows, n < 2^31");
+  HIP_TRY(qe::launch_row_argmax(logits, uint32_t(rows), uint32_t(n), tokens_out, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }
 

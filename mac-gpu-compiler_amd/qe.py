@@ -123,26 +123,31 @@ def l2_prefetch_max_pos(cfg: Config, kv_el: int = 4) -> int:
     return int(0.5 * pf_bytes / (2 * cfg.num_key_value_heads * cfg.head_dim * kv_el))
 
 
-def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4, prefetch: bool = False) -> dict:
+def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> dict:
     """Algorithmic bytes per launch of each decode-step stage: a matvec moves its bf16 weights
     plus its f32 input and output once (out*in*2 + in*4 + out*4, bench.rs:106-119 counts the
-    weights), attention its K/V history at mean_pos plus q/k/v in and the output out. With
-    `prefetch` (and mean_pos below l2_prefetch_max_pos), the attention launch also streams the
-    layer's gate/up and down weights (the bytes it moves from HBM; the per-token total still
-    counts each weight once)."""
+    weights); the attention its K/V history at mean_pos (positions 0..mean_pos) plus the raw
+    q/k/v it reads and its output. The gate/up and down weights that the attention launch also
+    pulls into L2 (prefetch_bytes) are counted with the gate_up and down stages, which read them."""
     H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
-    pf = (2 * I * H * 2 + H * I * 2) if prefetch and mean_pos < l2_prefetch_max_pos(cfg, kv_el) else 0
     return {
         "embed": H * 2 + H * 4,
         "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
-        "attention": 2 * KD * (mean_pos + 1) * kv_el + (QD + 2 * KD) * 4 + QD * 4 + pf,
+        "attention": 2 * KD * (mean_pos + 1) * kv_el + (QD + 2 * KD) * 4 + QD * 4,
         "o_proj": H * QD * 2 + QD * 4 + 2 * H * 4,
         "gate_up": 2 * I * H * 2 + H * 2 + H * 4 + I * 4,
         "down": H * I * 2 + I * 4 + 2 * H * 4,
         "lm_head": V * H * 2 + H * 2 + H * 4 + V * 4,
         "argmax": 8 * ((V + 15) // 16),
     }
+
+
+def prefetch_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> int:
+    """Weight bytes one decode attention launch pulls into L2 for the later stages (the layer's
+    gate/up and down), or 0 at positions where the engine no longer prefetches."""
+    H, I = cfg.hidden_size, cfg.intermediate_size
+    return 3 * I * H * 2 if mean_pos < l2_prefetch_max_pos(cfg, kv_el) else 0
 
 
 def lib() -> ctypes.CDLL:
@@ -191,6 +196,7 @@ def lib() -> ctypes.CDLL:
         "qe_op_attention_work_bytes": (u64, [u64, u64, u64]),
         "qe_op_attention": (i32, [vp, vp, vp, vp, u64, u64, u64, u64, u32, vp, vp]),
         "qe_op_read_sum": (i32, [vp, u64, vp, u32, vp]),
+        "qe_op_argmax": (i32, [vp, u64, u64, vp, vp]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -410,6 +416,12 @@ def op_attention(q, k, v, out, n_pos: int, n_heads: int, n_kv_heads: int, work, 
     kv_stride = k.shape[1]
     _check(lib().qe_op_attention(_ptr(q), _ptr(k), _ptr(v), _ptr(out), n_pos, kv_stride, n_heads, n_kv_heads,
                                  n_splits, _ptr(work), _stream_ptr(stream)))
+
+
+def op_argmax(logits, tokens, stream=None) -> None:
+    """tokens[r] = greedy token of logits[r] (f32 [rows, n] on the device; tokens int32/uint32 [rows])."""
+    rows, n = logits.shape
+    _check(lib().qe_op_argmax(_ptr(logits), rows, n, _ptr(tokens), _stream_ptr(stream)))
 
 
 def op_read_sum(src, partial, grid: int = 0, stream=None) -> None:

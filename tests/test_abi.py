@@ -129,6 +129,35 @@ def test_missing_tensor_wrong_dtype_wrong_shape(tmp_path):
         assert code == qe.QE_ERR_TENSOR, (name, msg)
 
 
+def test_bad_offsets_and_overflowing_shapes(tmp_path):
+    """an entry the engine never loads still needs a byte range inside the data section (the byte
+    formula sums every entry's off1 - off0), and a shape whose element count wraps around 2^64 to
+    the expected count is rejected rather than accepted"""
+    path = qe.write_random_checkpoint(str(tmp_path / "ok"), 1, TINY)
+    raw = open(path, "rb").read()
+    hl = int.from_bytes(raw[:8], "little")
+    header = json.loads(raw[8:8 + hl])
+    data = raw[8 + hl:]
+    cases = {}
+    for name, offs in {"reversed": [10, 4], "negative": [-2, 4], "past_end": [0, len(data) + 2]}.items():
+        h = json.loads(json.dumps(header))
+        h["extra.unused"] = {"dtype": "BF16", "shape": [2], "data_offsets": offs}
+        cases[name] = (h, qe.QE_ERR_FORMAT)
+    # q_norm has 128 elements: 99789673 * 1444189401 = 2^57 + 1, so with a dim of 128 the product
+    # is 2^64 + 128, which wraps to 128 in 64-bit arithmetic (every dim fits an i32)
+    h = json.loads(json.dumps(header))
+    assert 99789673 * 1444189401 == 2 ** 57 + 1
+    h["model.layers.0.self_attn.q_norm.weight"]["shape"] = [99789673, 1444189401, 128]
+    cases["wrapping_shape"] = (h, qe.QE_ERR_TENSOR)
+    for name, (h, want) in cases.items():
+        d = tmp_path / name
+        d.mkdir()
+        p = str(d / "model.safetensors")
+        write_st(p, h, data)
+        code, msg = load_err(p)
+        assert code == want, (name, msg)
+
+
 @pytest.mark.skipif(gpu_visible(), reason="with a GPU the valid file loads; covered by the gpu tests")
 def test_valid_file_reports_no_device(tmp_path):
     path = qe.write_random_checkpoint(str(tmp_path), 1, TINY)
