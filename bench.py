@@ -2,10 +2,15 @@
 
 Workload (the reference's bench protocol, metal_infrence_engine/src/bin/bench.rs:165-191, on
 synthetic weights): a seeded random-init checkpoint, a 130-token prompt of uniform-random ids,
-prefill, then K greedy decode steps (default 128, positions 130..257) with an f32 KV cache.
-A "step" is one decode token. Prints ONE JSON line (the last line of stdout).
+an untimed prefill, then one greedy decode of 128 steps (positions 130..257) with an f32 KV cache.
+A "step" of this benchmark is that whole 128-token decode: --steps K times K of them back to back
+(each from position 130 of the prefilled cache, which rewrites positions 130..257 before reading
+them, so every step sees the state of a freshly prefilled cache) after --warmup W untimed ones.
+value = 128 K / timed seconds. Every decode's 129 greedy tokens are checked against the oracle's
+committed run. Prints ONE JSON line (the last line of stdout).
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--kv f32|bf16] [--no-cpu-baseline]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--kv f32|bf16] [--decode-steps 128]
+                  [--no-cpu-baseline]
 """
 import argparse
 import json
@@ -63,6 +68,11 @@ def measured_read_ceiling(torch, qe) -> float:
             best = max(best, (gib << 30) * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9)
         del src, part
     torch.cuda.empty_cache()
+    # tests/read_bandwidth.rs:139-140: a reading above the spec means the buffer was served from
+    # a cache, and the figure cannot be a DRAM ceiling
+    if not 0.0 < best <= 1.05 * SPEC_HBM_GBS:
+        raise RuntimeError(f"read ceiling {best:.1f} GB/s is outside (0, 1.05 x {SPEC_HBM_GBS:.0f}] GB/s: "
+                           "the buffer is probably being served from cache")
     return best
 
 
@@ -102,21 +112,23 @@ def pmc_traffic(stage: str):
     return int(row["traffic_bytes"]) if row and "traffic_bytes" in row else None
 
 
-def cpu_baseline(ckpt: str, prompt, target_s: float = 12.0):
-    """The oracle (C restatement of cpu_inference.rs) on this host: a short prefill, then decode
-    steps until ~target_s of decode work; tok/s over the decode steps."""
+def cpu_baseline(ckpt: str, prompt, target_s: float = 15.0, min_steps: int = 16):
+    """The oracle (C restatement of cpu_inference.rs) on this host at the benchmark's own
+    positions: an untimed prefill of the whole prompt, then greedy decode steps from the prompt's
+    end until ~target_s of decode work (at least min_steps); tok/s over the decode steps."""
     import oracle
 
     m = oracle.Model(ckpt)
     cache = m.new_cache()
-    n_prefill = 4
-    for pos in range(n_prefill):
-        logits = m.forward(int(prompt[pos]), pos, cache)
+    t0 = time.perf_counter()
+    for pos, tok in enumerate(prompt):
+        logits = m.forward(int(tok), pos, cache)
+    prefill_s = time.perf_counter() - t0
     tok = oracle.argmax(logits)
     times = []
     t_start = time.perf_counter()
-    pos = n_prefill
-    while time.perf_counter() - t_start < target_s and len(times) < 64:
+    pos = len(prompt)
+    while len(times) < min_steps or (time.perf_counter() - t_start < target_s and len(times) < 128):
         t0 = time.perf_counter()
         logits = m.forward(tok, pos, cache)
         tok = oracle.argmax(logits)
@@ -129,8 +141,9 @@ def cpu_baseline(ckpt: str, prompt, target_s: float = 12.0):
         "cores": oracle.get_threads(),
         "kind": "port",
         "sample": f"oracle forward (C restatement of cpu_inference.rs, rows split over {oracle.get_threads()} threads "
-                  f"per matvec), {n_prefill}-token prefill then {len(times)} greedy decode steps at positions "
-                  f"{n_prefill}..{pos - 1}; median {sorted(times)[len(times) // 2] * 1e3:.1f} ms/token; host {cpu_model()}",
+                  f"per matvec, attention single-threaded), untimed {len(prompt)}-token prefill ({prefill_s:.1f} s), "
+                  f"then {len(times)} greedy decode steps at positions {len(prompt)}..{pos - 1}; median "
+                  f"{sorted(times)[len(times) // 2] * 1e3:.1f} ms/token; host {cpu_model()}",
     }
 
 
@@ -318,11 +331,11 @@ def prefill_bench(torch, qe, model, cfg, args):
 
 def lookup_bench(qe, model, cfg, args):
     """Prompt-lookup speculative decode (qe_decode_lookup) against plain greedy decode on the
-    decode workload: the 130-token prompt, then `steps` greedy tokens. Both must give the same
+    decode workload: the 130-token prompt, then --decode-steps greedy tokens. Both must give the same
     tokens; reports tok/s of each, verify passes and tokens per pass for k_max = 3 (a verify of 4
     rows, on the multi-row matvec), 4 and 8."""
     import numpy as np
-    P, K = args.prompt_len, args.steps
+    P, K = args.prompt_len, args.decode_steps
     prompt = qe.random_prompt(PROMPT_SEED, P, cfg.vocab_size)
 
     def run(fn):
@@ -349,8 +362,10 @@ def lookup_bench(qe, model, cfg, args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=128)
-    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--steps", type=int, default=10,
+                    help="timed benchmark steps; one step is a whole --decode-steps greedy decode")
+    ap.add_argument("--warmup", type=int, default=2, help="untimed decodes before the timed ones")
+    ap.add_argument("--decode-steps", type=int, default=128, help="greedy decode steps (tokens) per benchmark step")
     ap.add_argument("--kv", choices=["f32", "bf16"], default="f32")
     ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
     ap.add_argument("--workdir", default=os.environ.get("QE_BENCH_DIR", "/tmp/qe_bench"))
@@ -424,59 +439,81 @@ def main():
         return
     kv_dtype = qe.QE_KV_BF16 if args.kv == "bf16" else qe.QE_KV_F32
     prompt = qe.random_prompt(PROMPT_SEED, args.prompt_len, cfg.vocab_size)
-    K, W = args.steps, args.warmup
+    K, W, DS = args.steps, args.warmup, args.decode_steps
     P = args.prompt_len
+    el = 2 if kv_dtype == qe.QE_KV_BF16 else 4
 
-    # warm-up: prefill + W decode steps on a throwaway cache (kept for the per-kernel profile)
-    n_prof = 8
-    wc = qe.KVCache(model, P + max(W, n_prof) + 1, kv_dtype)
-    logits = model.prefill(prompt, 0, wc)
-    warm_tokens, _ = model.decode(int(np.argmax(logits)), P, max(W, n_prof), wc)
+    # the oracle's committed greedy run of this workload, if there is one
+    ref = []
+    fx = {(128, "f32"): "qwen3_0_6b_decode.npz", (4096, "f32"): "qwen3_0_6b_long_f32.npz",
+          (4096, "bf16"): "qwen3_0_6b_long_bf16.npz"}.get((DS, args.kv))
+    if fx and P == PROMPT_LEN and os.path.exists(os.path.join(ROOT, "tests", "golden", fx)):
+        ref = [int(t) for t in np.load(os.path.join(ROOT, "tests", "golden", fx), allow_pickle=False)["tokens"]]
 
-    # timed: fresh cache, prefill, then exactly K decode steps
-    cache = qe.KVCache(model, P + K + 1, kv_dtype)
+    # untimed: the prompt's prefill. Each decode below starts at position P of this cache and
+    # rewrites positions P..P+DS-1 before reading them, so every one sees a freshly prefilled cache.
+    cache = qe.KVCache(model, P + DS + 1, kv_dtype)
     logits = model.prefill(prompt, 0, cache)
     first = int(np.argmax(logits))
     stream = torch.cuda.ExternalStream(model.stream_handle())
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    gaps = []
-    last = [0.0]
+    runs = []  # per timed decode: tokens, host gaps between tokens
 
-    def on_token(_t):
-        now = time.perf_counter()
-        gaps.append(now - last[0])
-        last[0] = now
+    def decode_once():
+        gaps, last = [], [time.perf_counter()]
 
+        def on_token(_t):
+            now = time.perf_counter()
+            gaps.append(now - last[0])
+            last[0] = now
+
+        toks, _ = model.decode(first, P, DS, cache, on_token=on_token)
+        return [first] + toks, gaps
+
+    for _ in range(W):
+        decode_once()
     torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     t_start = time.perf_counter()
-    last[0] = t_start
-    tokens, _ = model.decode(first, P, K, cache, on_token=on_token)
+    for _ in range(K):
+        runs.append(decode_once())
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
     gpu_s = ev0.elapsed_time(ev1) * 1e-3
+    tokens = runs[0][0]
+    gaps = [g for _, gs in runs for g in gs]
+
+    # every timed decode against the oracle's run (and against each other)
+    parity = None
+    if ref:
+        n = min(len(ref), len(tokens))
+        divs = [next((i for i in range(n) if r[i] != ref[i]), None) for r, _ in runs]
+        parity = {"compared": n, "decodes": len(runs), "first_divergence": next((d for d in divs if d is not None), None)}
+    if any(r != tokens for r, _ in runs):
+        raise RuntimeError("the timed decodes produced different tokens")
 
     weight_bytes = model.weight_bytes_per_token()
-    kv_bytes = [model.kv_bytes_at(p, kv_dtype) for p in range(P, P + K)]
-    bytes_total = K * weight_bytes + sum(kv_bytes)
-    avg_bytes = bytes_total / K
-    tps = K / wall
-    ms_per_step = wall / K * 1e3
-    per_token_gpu_s = gpu_s / K
+    kv_bytes = [model.kv_bytes_at(p, kv_dtype) for p in range(P, P + DS)]
+    bytes_per_decode = DS * weight_bytes + sum(kv_bytes)
+    avg_bytes = bytes_per_decode / DS
+    n_tok = K * DS
+    tps = n_tok / wall
+    per_token_gpu_s = gpu_s / n_tok
     achieved_gbs = avg_bytes / per_token_gpu_s / 1e9
 
     # per-stage launch durations: each stage's launches alone as a graph, replayed between two
-    # HIP events on the engine stream (qe_profile_step), on the warm cache at n_prof positions
+    # HIP events on the engine stream (qe_profile_step), at 8 positions around the decode's mean
+    # position, on the benchmark's cache (outside the timed region)
+    n_prof = 8
+    mid = P + DS // 2 - n_prof // 2
+    prof_positions = list(range(mid, mid + n_prof))
     stages = {}
-    prof_positions = list(range(P, P + n_prof))
-    for i, pos in enumerate([] if args.no_profile else prof_positions):
-        for name, us, launches in model.profile_step(warm_tokens[i], pos, wc):
+    for pos in ([] if args.no_profile else prof_positions):
+        for name, us, launches in model.profile_step(tokens[pos - P], pos, cache):
             stages.setdefault(name, ([], launches))[0].append(us)
-    del wc
-    el = 2 if kv_dtype == qe.QE_KV_BF16 else 4
     mean_pos = sum(prof_positions) / n_prof
-    stage_bytes = qe.stage_bytes(cfg, mean_pos, el, prefetch=qe.l2_prefetch_enabled())
+    stage_bytes = qe.stage_bytes(cfg, mean_pos, el)
     # The attention stage alone replays 28 attention launches back to back; in the step each one
     # runs behind its layer's q|k|v launch, which it reads. Its in-step launch time is therefore
     # taken as the q|k|v + attention pair's time minus the q|k|v stage's.
@@ -492,24 +529,16 @@ def main():
         kernel_table[name] = {"launches_per_step": per_step, "mean_us": round(mean_us, 3),
                               "us_per_step": round(mean_us * per_step, 2), "bytes_per_launch": int(b),
                               "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
+    pf = qe.prefetch_bytes(cfg, mean_pos, el) if qe.l2_prefetch_enabled() else 0
+    if "attention" in kernel_table:
+        # the gate/up and down weights this launch also pulls into L2 (counted with those stages)
+        kernel_table["attention"]["prefetch_bytes"] = int(pf)
     if kernel_table:
         dom_name = max(kernel_table, key=lambda k: kernel_table[k]["us_per_step"])
         dom = kernel_table[dom_name]
     else:
         dom_name, dom = None, {"achieved_gbs": None, "bytes_per_launch": None, "mean_us": None,
                                "launches_per_step": None}
-
-    # token parity against the oracle's committed run of the same workload
-    parity = None
-    ref = []
-    fx = os.path.join(ROOT, "tests", "golden", "qwen3_0_6b_decode.npz")
-    if os.path.exists(fx) and P == PROMPT_LEN and kv_dtype == qe.QE_KV_F32:
-        g = np.load(fx, allow_pickle=False)
-        ref = [int(t) for t in g["tokens"]]
-        got = [first] + tokens
-        n = min(len(ref), len(got))
-        div = next((i for i in range(n) if ref[i] != got[i]), None)
-        parity = {"compared": n, "first_divergence": div}
 
     result = {
         "metric": "decode tok/s @ batch 1, Qwen3-0.6B-arch bf16; achieved HBM GB/s vs roofline",
@@ -518,7 +547,8 @@ def main():
         "n_gpus": 1,
         "steps": K,
         "warmup": W,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(wall / K * 1e3, 3),
+        "ms_per_token": round(wall / n_tok * 1e3, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -529,10 +559,10 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"Qwen3-0.6B-architecture decoder, seeded random-init bf16 weights (seed {SEED}), "
-                        f"{P}-token random prompt (seed {PROMPT_SEED}), {K} greedy decode steps at batch 1, "
-                        f"{args.kv} KV cache",
+                        f"{P}-token random prompt (seed {PROMPT_SEED}) prefilled untimed, then {DS} greedy decode "
+                        f"steps at batch 1 (positions {P}..{P + DS - 1}) per benchmark step, {args.kv} KV cache",
             "prompt_tokens": P,
-            "decode_steps": K,
+            "decode_steps": DS,
             "kv_cache": args.kv,
             "batch": 1,
         },
@@ -545,6 +575,7 @@ def main():
             "traffic": pmc_traffic(dom_name),
             "kernel": dom_name,
             "bytes_per_launch": dom["bytes_per_launch"],
+            "mean_position": mean_pos,
             "launch_us": dom["mean_us"],
             "launches_per_step": dom["launches_per_step"],
             "measured_ceiling_gbs": round(ceiling, 1),
@@ -562,7 +593,7 @@ def main():
         },
         "kernels": kernel_table,
         "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
-        "by_position": by_position(gaps, P, 512) if K >= 1024 else None,
+        "by_position": by_position(runs[0][1], P, 512) if DS >= 1024 else None,
         "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),
         "weight_bytes_per_token": weight_bytes,
         "parity_vs_oracle_fixture": parity,
@@ -573,12 +604,12 @@ def main():
         import harness
         rec = harness.engine_record(
             engine="hip", label=args.label, chip=torch.cuda.get_device_name(0), prompt_name=args.prompt_name,
-            prompt_tokens=P, load_ms=load_ms, step_ms=[g * 1e3 for g in gaps], tokens=[first] + tokens,
-            weight_bytes_per_token=weight_bytes, total_bytes=bytes_total, peak_bw_gbs=SPEC_HBM_GBS,
+            prompt_tokens=P, load_ms=load_ms, step_ms=[g * 1e3 for g in runs[0][1]], tokens=tokens,
+            weight_bytes_per_token=weight_bytes, total_bytes=bytes_per_decode, peak_bw_gbs=SPEC_HBM_GBS,
             ref_tokens=ref, repo_dir=ROOT)
         log(f"wrote {harness.write_records(args.results, rec)}")
     if args.json_out:
-        detail = dict(result, tokens=[first] + tokens, samples_ms=[round(g * 1e3, 4) for g in gaps])
+        detail = dict(result, tokens=tokens, samples_ms=[round(g * 1e3, 4) for g in gaps])
         with open(args.json_out, "w") as f:
             json.dump(detail, f, indent=1)
     print(json.dumps(result), flush=True)

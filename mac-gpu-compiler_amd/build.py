@@ -7,13 +7,16 @@ import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 
 PKG = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(PKG)
 CSRC = os.path.join(PKG, "csrc")
 LIB = os.path.join(PKG, "libqe.so")
 
-SOURCES = ["engine.hip", "kernels.hip", "attention.hip", "batch.hip", "checkpoint.cpp"]
+# every source in csrc/ except the profiling programs' own mains
+TOOL_SOURCES = {"qe_decode_cli.cpp", "qe_stage_pmc.hip"}
+SOURCES = sorted(f for f in os.listdir(CSRC) if f.endswith((".hip", ".cpp")) and f not in TOOL_SOURCES)
 
 HIPCC_FLAGS = [
     "-O3",
@@ -38,24 +41,46 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libqe.so)")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = [os.path.join(CSRC, s) for s in SOURCES]
-    tmp = LIB + ".tmp"
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", os.path.join(ROOT, "include"), "-o", tmp, *srcs, "-lpthread"]
+OBJ_DIR = os.path.join(PKG, "_build")
+# the host pass warns that it does not know the packed-fp32 feature; that is expected
+NOISE = "is not a recognized feature for this target"
+
+
+def _run(cmd, what: str, verbose: bool) -> None:
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # the host pass warns that it does not know the packed-fp32 feature; that is expected
-    noise = "is not a recognized feature for this target"
-    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if noise not in l)
+    out = "\n".join(l for l in (res.stdout + res.stderr).splitlines() if NOISE not in l)
     if res.returncode != 0:
-        raise RuntimeError("libqe.so build failed:\n" + out)
+        raise RuntimeError(f"{what} build failed:\n" + out)
     if verbose and out.strip():
         print(out)
+
+
+def build(verbose: bool = False) -> str:
+    """libqe.so: every source compiled in parallel, then linked."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
+        _run([hipcc(), *flags, "-I", os.path.join(ROOT, "include"), "-c", "-o", obj, os.path.join(CSRC, src)],
+             src, verbose)
+        return obj
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(compile_one, SOURCES))
+    tmp = LIB + ".tmp"
+    _run([hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, *objs, "-lpthread"], "libqe.so link",
+         verbose)
     os.replace(tmp, LIB)
-    build_cli(verbose)
-    build_stage_pmc(verbose)
     return LIB
+
+
+def build_tools(verbose: bool = False) -> list:
+    """The profiling programs beside the library (qe_decode, qe_stage_pmc). They are not part of
+    libqe.so: a failure here leaves the library as built."""
+    return [build_cli(verbose), build_stage_pmc(verbose)]
 
 
 CLI_SRC = os.path.join(CSRC, "qe_decode_cli.cpp")
@@ -102,3 +127,5 @@ def build_stage_pmc(verbose: bool = False) -> str:
 
 if __name__ == "__main__":
     print(build(verbose="-v" in sys.argv))
+    if "--tools" in sys.argv:
+        print(build_tools(verbose="-v" in sys.argv))

@@ -75,7 +75,9 @@ def main():
     ff, fw = copy_kib / cf, copy_kib / cw
 
     mean_pos = float(a.attn_pos)
-    algo = qe.stage_bytes(qe.QWEN3_0_6B, mean_pos, 4, prefetch=not a.no_prefetch)
+    algo = qe.stage_bytes(qe.QWEN3_0_6B, mean_pos, 4)
+    # the attention launch's own HBM traffic also holds the weights it prefetches into L2
+    pf = 0 if a.no_prefetch else qe.prefetch_bytes(qe.QWEN3_0_6B, mean_pos, 4)
     stages = {}
     for rows, key in ((fetch, "fetch_kib"), (write, "write_kib")):
         for kernel, v in rows:
@@ -93,6 +95,7 @@ def main():
         fk = sum(d["fetch_kib"]) / len(d["fetch_kib"])
         wk = sum(d["write_kib"]) / len(d["write_kib"])
         traffic = (fk * ff + wk * fw) * 1024.0
+        extra = pf if st == "attention" else 0
         out["stages"][st] = {
             "kernel": d["kernel"],
             "dispatches": len(d["fetch_kib"]),
@@ -100,7 +103,8 @@ def main():
             "write_kib": round(wk, 2),
             "traffic_bytes": int(round(traffic)),
             "algorithmic_bytes": int(round(algo[st])),
-            "traffic_over_algorithmic": round(traffic / algo[st], 4),
+            "prefetch_bytes": int(extra),
+            "traffic_over_algorithmic": round(traffic / (algo[st] + extra), 4),
         }
     with open(a.out_json, "w") as f:
         json.dump(out, f, indent=1)
@@ -116,8 +120,9 @@ def main():
         f"{a.copy_mib} MiB copy kernel (read {a.copy_mib} MiB, write {a.copy_mib} MiB): FETCH_SIZE x {ff:.4f},",
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
-        "for attention" + ("" if a.no_prefetch else ", plus the gate/up and down weights its launch streams into L2") +
-        " (the figures `bench.py` divides by the launch time).",
+        "for attention (the figures `bench.py` divides by the launch time)." +
+        ("" if a.no_prefetch else " The attention launch also streams the layer's gate/up and down weights into"
+         " L2 (prefetch bytes, counted with those stages); its ratio is traffic over own + prefetch bytes."),
         "",
         "Commands (MI355X, one GPU; committed files only):",
         "",
@@ -125,14 +130,15 @@ def main():
         a.command.strip(),
         "```",
         "",
-        "| Stage | Kernel | Dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes/launch | Algorithmic bytes | Ratio |",
-        "|---|---|---|---|---|---|---|---|",
+        "| Stage | Kernel | Dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | HBM bytes/launch | Algorithmic bytes | Prefetch bytes | Ratio |",
+        "|---|---|---|---|---|---|---|---|---|",
     ]
     for st in order:
         r = out["stages"].get(st)
         if r:
             lines.append(f"| {st} | `{r['kernel']}` | {r['dispatches']} | {r['fetch_kib']:.1f} | {r['write_kib']:.1f} | "
-                         f"{r['traffic_bytes']:,} | {r['algorithmic_bytes']:,} | {r['traffic_over_algorithmic']:.3f} |")
+                         f"{r['traffic_bytes']:,} | {r['algorithmic_bytes']:,} | {r['prefetch_bytes']:,} | "
+                         f"{r['traffic_over_algorithmic']:.3f} |")
     with open(a.out_md, "w") as f:
         f.write("\n".join(lines) + "\n")
     print(json.dumps(out["stages"], indent=1))
