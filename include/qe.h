@@ -191,6 +191,16 @@ uint64_t qe_op_attention_work_bytes(uint64_t n_heads, uint64_t n_kv_heads, uint6
 int qe_op_attention(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
                     uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,
                     void* work, void* stream);
+/* qe_op_attention with no work buffer and no allocation: the partial sums go to a 1 MiB array in
+ * device memory that the library holds on each GPU it runs on until the process ends. No
+ * counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops that forbid hipMalloc). Same arguments and results as
+ * qe_op_attention; calls with n_heads x runs above 2048 (runs = n_splits, or n_pos / 64 rounded
+ * up, at most 128) are refused with QE_ERR_ARG. Every call on one GPU shares that GPU's array, so
+ * calls that overlap on one GPU (two streams or two threads) race. */
+int qe_op_attention_static(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
+                           uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,
+                           void* stream);
 /* Greedy token of each of `rows` logit rows of n floats (device memory, row-major): the argmax
  * of main.rs:37-42 -- the first maximum wins (lowest index on ties, -0.0 ties +0.0), NaN entries
  * never win, a NaN at index 0 gives 0, and a row with nothing above -inf gives 0. tokens_out:
