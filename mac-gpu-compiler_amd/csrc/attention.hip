@@ -115,12 +115,10 @@ __device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16>& X, int i) {
 
 template <int G, bool KV_BF16, bool DECODE>
 __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk) {
-  if constexpr (DECODE) {
-    if (blockIdx.y >= p.splits) {  // a prefetch workgroup (whole workgroup, before any load)
-      const uint32_t q = (blockIdx.y - p.splits) * gridDim.x + blockIdx.x;
-      if (q < 8 * p.pf_slots && p.state->pos < p.pf_max_pos) l2_prefetch(p.pf, p.pf_slots, q, p.err);
-      return;
-    }
+  if (blockIdx.y >= p.splits) {  // a prefetch workgroup (whole workgroup, before any load)
+    const uint32_t q = (blockIdx.y - p.splits) * gridDim.x + blockIdx.x;
+    if (q < 8 * p.pf_slots && (!DECODE || p.state->pos < p.pf_max_pos)) l2_prefetch(p.pf, p.pf_slots, q, p.err);
+    return;
   }
   // DECODE: q/k RMSNorm + RoPE on the raw q|k|v rows, append of the new K/V row, positions
   // 0..state->pos; otherwise (the isolated op) q is final and positions are 0..n_pos_fixed-1
@@ -148,8 +146,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
 #pragma unroll
   for (int i = 0; i < RPW; i++) {
     const int r = min(wave + 4 * i, NR - 1);
-    const size_t off = r < G ? (size_t(g) * G + r) * D
-                             : size_t(p.n_heads) * D + (r == G ? 0 : size_t(p.n_kv) * D) + size_t(g) * D;
+    size_t off = r < G ? (size_t(g) * G + r) * D
+                       : size_t(p.n_heads) * D + (r == G ? 0 : size_t(p.n_kv) * D) + size_t(g) * D;
+    if (!DECODE && p.tok_heads)  // rows of several tokens: token r / tok_heads, head g tok_heads + r % tok_heads
+      off = size_t(r / p.tok_heads) * p.q_tok_stride + (size_t(g) * p.tok_heads + r % p.tok_heads) * D;
     ra[i] = p.qkv[off + lane];
     rb[i] = p.qkv[off + lane + 64];
   }
@@ -197,6 +197,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   }
   const uint32_t t1 = min(n, t0 + run);
   float* part = p.partial + (size_t(g) * p.splits + s) * G * kPartStride;
+  // per-row causal limit: with rows of several tokens, token i of T sees positions < n - (T - 1 - i)
+  uint32_t lim[G];
+#pragma unroll
+  for (int j = 0; j < G; j++) {
+    lim[j] = n;
+    if (!DECODE && p.tok_heads) lim[j] = n - (uint32_t(G) / p.tok_heads - 1u - uint32_t(j) / p.tok_heads);
+  }
 
   // ---- q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215) ----
 #pragma unroll
@@ -261,7 +268,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
       }
       if (dc == 0) {
 #pragma unroll
-        for (int j = 0; j < G; j++) sc[j][pg + 32 * u] = t < t1 ? sv[j] * p.scale : -INFINITY;
+        for (int j = 0; j < G; j++) sc[j][pg + 32 * u] = t < t1 && t < lim[j] ? sv[j] * p.scale : -INFINITY;
       }
     }
     __syncthreads();
@@ -339,7 +346,8 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
 // issued at once (indexes past the last split re-read it and weigh 0); the 8 groups meet in LDS.
 // ---------------------------------------------------------------------------------------------
 __global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
-                                                             float* __restrict__ out) {
+                                                             float* __restrict__ out, uint32_t tok_heads,
+                                                             uint32_t q_tok_stride) {
   constexpr int U = kAttnMaxSplits / 8, PS = kPartStride;
   const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x & (kHeadDim - 1), grp = threadIdx.x >> 7;
   const float* base = part + (size_t(g) * splits * G + j) * PS;
@@ -377,7 +385,10 @@ __global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __rest
     LL += e * gl[k];
     AA += e * ga[k][d];
   }
-  out[size_t(h) * kHeadDim + d] = AA / LL;
+  // rows of several tokens: row j of KV head g is token j / tok_heads, head g tok_heads + j % tok_heads
+  const size_t o = tok_heads ? size_t(j / tok_heads) * q_tok_stride + (size_t(g) * tok_heads + j % tok_heads) * kHeadDim
+                             : size_t(h) * kHeadDim;
+  out[o + d] = AA / LL;
 }
 
 // shapes the kernels support; the runs [s*chunk, (s+1)*chunk) must cover positions 0..n-1
@@ -393,7 +404,6 @@ hipError_t launch_split(const AttnParams& pin, uint32_t splits, uint32_t chunk, 
   const uint32_t G = pin.n_heads / pin.n_kv;
   AttnParams p = pin;
   p.splits = splits;
-  if (!DECODE) p.pf_slots = 0;
   // prefetch workgroups: whole rows of n_kv after the attention's `splits` rows (dispatched
   // after them: ahead of them, they delay the attention more than they gain)
   const dim3 grid(p.n_kv, splits + ceil_div(8 * p.pf_slots, p.n_kv));
@@ -427,7 +437,23 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out);
+  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out,
+                     0u, 0u);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
+  if (p.n_pos_fixed == 0 || p.n_pos_fixed > p.max_seq || splits == 0 || splits > uint32_t(kAttnMaxSplits) || !out ||
+      !p.n_kv || !p.tok_heads || (p.n_heads / p.n_kv) % p.tok_heads || !p.q_tok_stride)
+    return hipErrorInvalidValue;
+  const uint32_t tokens = p.n_heads / p.n_kv / p.tok_heads;
+  if (tokens > p.n_pos_fixed) return hipErrorInvalidValue;
+  const uint32_t chunk = ceil_div(p.n_pos_fixed, splits);
+  if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed)) return hipErrorInvalidValue;
+  hipError_t e = launch_split<false>(p, splits, chunk, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out,
+                     p.tok_heads, p.q_tok_stride);
   return hipGetLastError();
 }
 

@@ -67,6 +67,9 @@ struct BatchAttnParams {
 };
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
+// The L2 prefetch of W [N][K] for the unsplit skinny GEMM (M <= 16): workgroup j reads rows
+// 16 j .. 16 j + 15.
+L2Prefetch skinny_prefetch_target(const uint16_t* W, uint32_t N, uint32_t K);
 hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
 // K splits for a split GEMM: enough workgroups to fill the chip, each split a multiple of the
 // kernel's k step deep (1 when K does not split)

@@ -1092,6 +1092,10 @@ hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t
   }
 }
 
+L2Prefetch skinny_prefetch_target(const uint16_t* W, uint32_t N, uint32_t K) {
+  return L2Prefetch{W, N * (K / 8), 16 * (K / 8), ceil_div(N, 16u)};
+}
+
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st) {
   if (M == 0 || K % 4) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_rownorm, dim3(ceil_div(M, 4)), dim3(256), 0, st, x, M, K, eps, s);

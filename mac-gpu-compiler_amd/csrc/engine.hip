@@ -115,6 +115,10 @@ struct qe_model {
   // verify passes and chunks of up to kMvRowsMaxM tokens run their projections as multi-row
   // matvecs (QE_MV_ROWS=0: on the skinny GEMM)
   bool mv_rows = true;
+  // passes of at most 8 / (q heads per KV head) tokens (a verify of up to 4 rows) attend on the
+  // decode step's split kernel, all their q heads of a KV head sharing one read of its K/V
+  // (QE_ROWS_SPLIT_ATTN=0: on the causal matrix-core kernel)
+  bool rows_split_attn = true;
   // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
@@ -220,6 +224,7 @@ int qe_model_load(const char* path, qe_model** out) {
   m->cfg = m->ckpt.config();
   if (const char* pf = getenv("QE_L2_PREFETCH")) m->l2_prefetch = strcmp(pf, "0") != 0;
   if (const char* mr = getenv("QE_MV_ROWS")) m->mv_rows = strcmp(mr, "0") != 0;
+  if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
   const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
@@ -485,6 +490,8 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   for (uint32_t M = 1; M <= cap; M++)
     part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
                                                                      uint32_t(c.num_key_value_heads)));
+  // the split kernel's partials for passes of up to 8 tokens: tokens x runs rows per q head
+  part_rows = std::max(part_rows, size_t(std::min<uint32_t>(cap, 8)) * qe::kAttnMaxSplits);
   const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
   const size_t osplit = take(size_t(8) * cap * H * 4);  // gemm_splits returns at most 8
   const size_t otok = take(size_t(kVerifyMaxTokens) * 4);
@@ -586,8 +593,29 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.eps = eps; a.scale = 1.0f / sqrtf(float(D)); a.kv_bf16 = kv->dtype == QE_KV_BF16;
     HIP_TRY(qe::launch_qk_rope(a, s));
-    a.part = m->bpart;
-    HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
+    const uint32_t rows_per_kv = (a.n_heads / a.n_kv) * M;
+    if (m->rows_split_attn && (rows_per_kv == 1 || rows_per_kv == 2 || rows_per_kv == 4 || rows_per_kv == 8)) {
+      // few tokens: the split kernel, the q heads of all M tokens of a KV head over one read of
+      // its K/V, each token causal (positions up to its own), runs of 64 positions
+      AttnParams r{};
+      r.qkv = m->bq; r.k_cache = a.k_cache; r.v_cache = a.v_cache; r.partial = m->bpart;
+      r.n_kv = a.n_kv; r.n_heads = a.n_kv * rows_per_kv; r.max_seq = a.max_seq; r.scale = a.scale;
+      r.kv_bf16 = a.kv_bf16; r.n_pos_fixed = start + M; r.tok_heads = a.n_heads / a.n_kv; r.q_tok_stride = QD;
+      if (m->l2_prefetch && mv) {
+        // as in the decode step: the attention is latency-bound, so extra workgroups load this
+        // layer's gate|up (the skinny GEMM's rows at 4 tokens, else the multi-row matvec's) and
+        // down weights into the L2 of the XCDs that will read them
+        r.pf[0] = M >= 4 ? qe::skinny_prefetch_target(w.w_gu, 2 * I, H)
+                         : qe::l2_prefetch_target(w.w_gu, 2 * I, H, qe::kNorm, qe::kSiluPair);
+        r.pf[1] = qe::l2_prefetch_target(w.w_down, H, I, qe::kCopy, qe::kResAdd);
+        r.pf_slots = qe::l2_prefetch_slots(r.pf, qe::kMaxPrefetch);
+      }
+      const uint32_t splits = std::min<uint32_t>(qe::kAttnMaxSplits, (start + M + 63) / 64);
+      HIP_TRY(qe::launch_attention_rows(r, splits, m->batt, s));
+    } else {
+      a.part = m->bpart;
+      HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
+    }
     // o_proj + residual (cpu_inference.rs:163-164)
     if ((rc = gemm_resadd(m->batt, QD, w.w_o, QD))) return rc;
     // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)

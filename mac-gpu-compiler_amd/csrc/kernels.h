@@ -84,6 +84,12 @@ struct AttnParams {
   float eps, scale;
   int kv_bf16;
   uint32_t n_pos_fixed;    // isolated op: attend positions 0..n_pos_fixed-1 with a final q
+  // rows of several tokens (launch_attention_rows): the G' = n_heads / n_kv rows of KV head g are
+  // tok_heads q heads of each of G' / tok_heads consecutive tokens; row r is token r / tok_heads,
+  // head g * tok_heads + r % tok_heads, its q at r / tok_heads * q_tok_stride + head * 128 (and
+  // its output there too), and it sees positions up to n_pos_fixed - tokens + token (causal).
+  // tok_heads = 0: one token (the rows are the G' heads of g)
+  uint32_t tok_heads, q_tok_stride;
   uint32_t splits;         // runs per KV head (set by the launchers)
   uint32_t run;            // decode: positions per run (a multiple of 64) chosen by the host for
                            // the step's position; 0: derived from pos on the device
@@ -114,6 +120,12 @@ uint32_t l2_prefetch_slots(const L2Prefetch* pf, int n);
 // The isolated op: final q [n_heads][D], complete K/V [n_kv][max_seq][D] (f32), positions
 // 0..n_pos_fixed-1 in `splits` runs (<= kAttnMaxSplits), partials merged into out [n_heads][D].
 hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);
+// Attention of T tokens at positions n_pos_fixed - T .. n_pos_fixed - 1 over positions
+// 0..n_pos_fixed-1 of a cache that already holds their K/V (f32 or bf16), causal among them, with
+// the same kernels: q [T][heads][128] final (normalized, rotated), out [T][heads][128]. The T
+// tokens' q heads of a KV head share one read of its K/V: p.n_heads = n_kv * T * tok_heads must
+// give 1, 2, 4 or 8 rows per KV head. partial: n_kv * splits * (rows per KV head) * kPartStride floats.
+hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);
 // Greedy token from the lm_head candidates; advances the step state and, with `rope`, copies the
 // RoPE row of the next position ([half] (cos, sin) pairs) to rope_cur for the next step.
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,
