@@ -304,6 +304,12 @@ def prefill_bench(torch, qe, model, cfg, args):
     for _ in range(reps):
         model.verify(draft, n, vcache)
     verify_ms = (time.perf_counter() - t0) / reps * 1e3
+    # the same pass with each row's greedy token taken on the device (qe_verify_greedy, what
+    # prompt-lookup decoding calls): no logits leave the device
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        model.verify_greedy(draft, n, vcache)
+    verify_greedy_ms = (time.perf_counter() - t0) / reps * 1e3
     t0 = time.perf_counter()
     for _ in range(reps):
         model.forward(int(draft[0]), n, vcache)
@@ -324,6 +330,7 @@ def prefill_bench(torch, qe, model, cfg, args):
         "one_chunk_ms": round(best_one * 1e3, 3) if best_one < float("inf") else None,
         "one_chunk_tok_s": round(n / best_one, 1) if best_one < float("inf") else None,
         "verify_k4_ms": round(verify_ms, 3),
+        "verify_greedy_k4_ms": round(verify_greedy_ms, 3),
         "forward_1_ms": round(forward_ms, 3),
         "verify_k4_tokens_per_s_if_all_accepted": round(4 / verify_ms * 1e3, 1),
     }

@@ -41,6 +41,11 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libqe.so)")
 
 
+# Per-source additions. batch.hip: matrix-core results go to ordinary VGPRs, where the MFMAs
+# accumulate in place; with the default accumulation registers the compiler moves the GEMM
+# accumulators between register files on every k stage.
+SOURCE_FLAGS = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
 OBJ_DIR = os.path.join(PKG, "_build")
 # the host pass warns that it does not know the packed-fp32 feature; that is expected
 NOISE = "is not a recognized feature for this target"
@@ -64,8 +69,8 @@ def build(verbose: bool = False) -> str:
 
     def compile_one(src):
         obj = os.path.join(OBJ_DIR, os.path.splitext(src)[0] + ".o")
-        _run([hipcc(), *flags, "-I", os.path.join(ROOT, "include"), "-c", "-o", obj, os.path.join(CSRC, src)],
-             src, verbose)
+        _run([hipcc(), *flags, *SOURCE_FLAGS.get(src, []), "-I", os.path.join(ROOT, "include"), "-c", "-o", obj,
+              os.path.join(CSRC, src)], src, verbose)
         return obj
 
     with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
@@ -113,7 +118,9 @@ def build_stage_pmc(verbose: bool = False) -> str:
     inputs, for counter collection."""
     tmp = PMC + ".tmp"
     flags = [f for f in HIPCC_FLAGS if f not in ("-fPIC", "-shared")]
-    cmd = [hipcc(), *flags, "-I", os.path.join(ROOT, "include"), "-o", tmp,
+    # the same code generation as the library's (one flag set for all four sources)
+    extra = [f for src in PMC_SRCS for f in SOURCE_FLAGS.get(src, [])]
+    cmd = [hipcc(), *flags, *extra, "-I", os.path.join(ROOT, "include"), "-o", tmp,
            *[os.path.join(CSRC, f) for f in PMC_SRCS]]
     if verbose:
         print(" ".join(cmd), flush=True)

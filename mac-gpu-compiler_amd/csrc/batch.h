@@ -33,8 +33,11 @@ struct GemmParams {
 };
 
 constexpr uint32_t kGemmSkinnyMaxM = 32;
-// More than kGemmTileMinM rows run on the 128-row tile kernel; between the two, 64 x 64 tiles.
+// Between kGemmSkinnyMaxM and kGemmTileMinM rows, 64 x 64 tiles (k_gemm_lds). Above, up to
+// kGemmRowsMaxM rows (K a multiple of 64), the 64-row eight-wave kernel (k_gemm_rows8), then
+// 128-row tiles (k_gemm_tile): the faster at each size measured (128, 256, 512, 1024, 2048 rows).
 constexpr uint32_t kGemmTileMinM = 64;
+constexpr uint32_t kGemmRowsMaxM = 1024;
 
 // Verify passes and chunks of up to kMvRowsMaxM tokens run the projections as a matvec over their
 // token rows: out[m][.] for m < M from x [M][cols] (see launch_mv_rows). Each further row adds its

@@ -277,11 +277,13 @@ __global__ __launch_bounds__(256) void k_gemm_lds(GemmParams p) {
 // - 1, i.e. 4 x BN / 32 MFMA tiles of 16 x 16, so each fragment read from LDS feeds BN / 32 (A)
 // or 8 (W) MFMAs. Both operands are staged in LDS: the thread that loads an f32 A element
 // applies the norm scale and splits it into hi + lo bf16 once for the whole workgroup; W rows go
-// in as they are. Two LDS buffers, two register stages: while stage s is computed, stage s + 1
-// (already in registers) is written to the other buffer and stage s + 2 is loaded from memory.
-// gridDim.z > 1 splits K as in k_gemm_lds.
+// in as they are. Two LDS buffers and D register stages (stage t in register slot t % D): while
+// stage s is computed from one buffer, stage s + 1 goes from its slot to the other buffer and the
+// slot is refilled with stage s + 1 + D, so each load has D steps of MFMA work to arrive in (one
+// step is short next to the L2 / MALL latency). The stage count K / 32 (per split) is a multiple
+// of D (the launcher checks). gridDim.z > 1 splits K as in k_gemm_lds.
 // ---------------------------------------------------------------------------------------------
-template <bool NORM, int EPI, int BN>
+template <bool NORM, int EPI, int BN, int D>
 __global__ __launch_bounds__(256) void k_gemm_tile(GemmParams p) {
   constexpr int BM = 128, BK = 32, NT = BN / 32, KP = BK + 8;
   constexpr int WCH = BN * BK / 8 / 256;  // 16-byte W chunks per thread per stage
@@ -356,38 +358,47 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmParams p) {
   for (int i = 0; i < 4; i++)
 #pragma unroll
     for (int j = 0; j < NT; j++) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // All fragments of the stage are read before the first MFMA, so the LDS latency is paid once
+  // per stage; then the hi products, then the lo products (each accumulator still adds hi . w
+  // before lo . w).
   auto compute = [&](int buf) __attribute__((always_inline)) {
-    bf16x8 b[NT];
+    bf16x8 b[NT], hi[4], lo[4];
 #pragma unroll
     for (int j = 0; j < NT; j++)
       b[j] = *reinterpret_cast<const bf16x8*>(&bs[buf][wn * (BN / 2) + 16 * j + li][8 * kg]);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
       const int row = wm * 64 + 16 * i + li;
-      const bf16x8 hi = *reinterpret_cast<const bf16x8*>(&as[buf][0][row][8 * kg]);
-      const bf16x8 lo = *reinterpret_cast<const bf16x8*>(&as[buf][1][row][8 * kg]);
-#pragma unroll
-      for (int j = 0; j < NT; j++) {
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b[j], acc[i][j], 0, 0, 0);
-        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b[j], acc[i][j], 0, 0, 0);
-      }
+      hi[i] = *reinterpret_cast<const bf16x8*>(&as[buf][0][row][8 * kg]);
+      lo[i] = *reinterpret_cast<const bf16x8*>(&as[buf][1][row][8 * kg]);
     }
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < NT; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi[i], b[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int j = 0; j < NT; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo[i], b[j], acc[i][j], 0, 0, 0);
   };
-  // step s: x is free (its stage is in LDS), y holds stage s + 1
-  auto step = [&](Stage& x, Stage& y, uint32_t s) __attribute__((always_inline)) {
-    load(x, min(s + 2, nst - 1));  // unconditional: the last steps reload the last stage
-    if (s < nst) compute(int(s & 1));
-    if (s + 1 < nst) store(y, int((s + 1) & 1));
-    __syncthreads();
-  };
-  Stage r0, r1;
-  load(r0, 0);
-  load(r1, min(1u, nst - 1));
-  store(r0, 0);
+  Stage r[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) load(r[i], min(uint32_t(i), nst - 1));
+  store(r[0], 0);
+  load(r[0], min(uint32_t(D), nst - 1));
   __syncthreads();
-  for (uint32_t s = 0; s < nst; s += 2) {
-    step(r0, r1, s);
-    step(r1, r0, s + 1);
+  // Every step is unconditional: the loads past the last stage re-read the last stage (in
+  // bounds), and the last step's store goes to the buffer no later step reads.
+  for (uint32_t s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      const uint32_t s = s0 + uint32_t(i);
+      compute(int(s & 1));
+      __builtin_amdgcn_sched_barrier(0);
+      store(r[(i + 1) % D], int((s + 1) & 1));
+      load(r[(i + 1) % D], min(s + 1 + D, nst - 1));
+      __syncthreads();
+    }
   }
 
   // epilogue: lane holds C[m0 + 64 wm + 16 i + 4 kg + r][n0 + (BN / 2) wn + 16 j + li]
@@ -409,6 +420,142 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmParams p) {
         } else {
           if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] = c;
         }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Tiled GEMM for chunks of up to kGemmRowsMaxM rows, A straight to registers: workgroup tile 64
+// (m) x BN (n), k steps of 64, eight waves. Wave w owns the 16-row block w % 4 and the k half w / 4
+// of every step (k 64 s + 32 (w / 4) .. + 31). An A row belongs to one wave pair only, so each lane
+// loads its own f32 A fragment (row li of its block, k 8 kg .. 8 kg + 7), applies the norm scale
+// and splits it into hi + lo bf16 in registers; only the W tile, which all eight waves read, goes
+// through LDS (two buffers, rows staged 128 bytes = 64 k at a time). A 64 x 128 tile keeps the
+// bytes each CU pulls per MFMA lower than the 128-row tile does at these sizes, where the loads
+// from L2 and not the matrix cores set the pace, and still gives one tile per CU at 512 rows.
+// D steps in flight: A of step s + D is loaded as soon as step s is computed, W of step s + 1 + D
+// as soon as step s + 1 is in LDS. At the end the k-half-1 waves hand their sums to the k-half-0
+// waves through LDS: C = (sum over the even 32-k blocks) + (sum over the odd ones). The step
+// count K / 64 (per split) is a multiple of D. gridDim.z > 1 splits K as in k_gemm_lds.
+// ---------------------------------------------------------------------------------------------
+template <bool NORM, int EPI, int BN, int D>
+__global__ __launch_bounds__(512) void k_gemm_rows8(GemmParams p) {
+  constexpr int BK = 64, KP = BK + 8, NT = BN / 16;
+  constexpr int WCH = BN * BK / 8 / 512;  // 16-byte W chunks per thread per step
+  static_assert(WCH >= 1, "tile");
+  static_assert(2 * BN * KP * 2 >= 4 * 64 * NT * 16, "the reduction reuses the W buffers");
+  __shared__ __align__(16) uint16_t bs[2][BN][KP];  // [buffer][n][k]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
+  const int wr = wave & 3, kh = wave >> 2;
+  const uint32_t m0 = blockIdx.y * 64 + uint32_t(wr) * 16, n0 = blockIdx.x * BN;
+  const uint32_t kz = p.K / gridDim.z, kbeg = blockIdx.z * kz, nst = kz / BK;
+  const uint32_t row = min(m0 + uint32_t(li), p.M - 1);
+  const float* Ar = p.A + size_t(row) * p.lda + kbeg + 32 * kh + 8 * kg;
+  const float rs = NORM ? p.rowscale[row] : 1.0f;
+  const uint16_t* gsrc = NORM ? p.gain + kbeg + 32 * kh + 8 * kg : nullptr;
+  // W staging: chunk c = tid + 512 i is row c / 8, k (c % 8) * 8
+  const uint16_t* Wsrc[WCH];
+#pragma unroll
+  for (int i = 0; i < WCH; i++) {
+    const int c = tid + 512 * i;
+    Wsrc[i] = p.W + size_t(min(n0 + uint32_t(c >> 3), p.N - 1)) * p.K + kbeg + 8 * (c & 7);
+  }
+  struct AStage {
+    f32x4 a[2];
+    u32x4 g;
+  };
+  struct WStage {
+    u32x4 w[WCH];
+  };
+  auto load_a = [&](AStage& r, uint32_t stg) __attribute__((always_inline)) {
+    const uint32_t k = stg * BK;
+    r.a[0] = *reinterpret_cast<const f32x4*>(Ar + k);
+    r.a[1] = *reinterpret_cast<const f32x4*>(Ar + k + 4);
+    if constexpr (NORM) r.g = *reinterpret_cast<const u32x4*>(gsrc + k);
+  };
+  auto load_w = [&](WStage& r, uint32_t stg) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < WCH; i++) r.w[i] = *reinterpret_cast<const u32x4*>(Wsrc[i] + stg * BK);
+  };
+  auto store_w = [&](const WStage& r, int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < WCH; i++) {
+      const int c = tid + 512 * i;
+      *reinterpret_cast<u32x4*>(&bs[buf][c >> 3][8 * (c & 7)]) = r.w[i];
+    }
+  };
+  f32x4 acc[NT];
+#pragma unroll
+  for (int j = 0; j < NT; j++) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto compute = [&](const AStage& r, int buf) __attribute__((always_inline)) {
+    bf16x8 b[NT], hi, lo;
+#pragma unroll
+    for (int j = 0; j < NT; j++) b[j] = *reinterpret_cast<const bf16x8*>(&bs[buf][16 * j + li][32 * kh + 8 * kg]);
+    float v[8] = {r.a[0][0], r.a[0][1], r.a[0][2], r.a[0][3], r.a[1][0], r.a[1][1], r.a[1][2], r.a[1][3]};
+    if constexpr (NORM) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        v[2 * e] = (v[2 * e] * rs) * __uint_as_float(r.g[e] << 16);
+        v[2 * e + 1] = (v[2 * e + 1] * rs) * __uint_as_float(r.g[e] & 0xFFFF0000u);
+      }
+    }
+    split8(v, hi, lo);
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, b[j], acc[j], 0, 0, 0);
+#pragma unroll
+    for (int j = 0; j < NT; j++) acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, b[j], acc[j], 0, 0, 0);
+  };
+  AStage ra[D];
+  WStage rw[D];
+#pragma unroll
+  for (int i = 0; i < D; i++) {
+    load_a(ra[i], min(uint32_t(i), nst - 1));
+    load_w(rw[i], min(uint32_t(i), nst - 1));
+  }
+  store_w(rw[0], 0);
+  load_w(rw[0], min(uint32_t(D), nst - 1));
+  __syncthreads();
+  // Every step is unconditional: loads past the last step re-read the last step (in bounds), and
+  // the last step's W store goes to the buffer no later step reads.
+  for (uint32_t s0 = 0; s0 < nst; s0 += D) {
+#pragma unroll
+    for (int i = 0; i < D; i++) {
+      const uint32_t s = s0 + uint32_t(i);
+      compute(ra[i], int(s & 1));
+      load_a(ra[i], min(s + D, nst - 1));
+      store_w(rw[(i + 1) % D], int((s + 1) & 1));
+      load_w(rw[(i + 1) % D], min(s + 1 + D, nst - 1));
+      __syncthreads();
+    }
+  }
+  // the k-half-1 waves' sums, lane-major per (row block, column block), through the W buffers
+  f32x4* red = reinterpret_cast<f32x4*>(&bs[0][0][0]);
+  if (kh == 1) {
+#pragma unroll
+    for (int j = 0; j < NT; j++) red[(wr * NT + j) * 64 + lane] = acc[j];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int j = 0; j < NT; j++) acc[j] += red[(wr * NT + j) * 64 + lane];
+
+  // epilogue: lane holds C[m0 + 4 kg + r][n0 + 16 j + li]
+  float* C = p.C + (EPI == kGemmPartial ? size_t(blockIdx.z) * p.M * p.ldc : 0);
+#pragma unroll
+  for (int j = 0; j < NT; j++) {
+    const uint32_t n = n0 + uint32_t(16 * j + li);
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t m = m0 + uint32_t(4 * kg + r);
+      const float c = acc[j][r];
+      if constexpr (EPI == kGemmSiluPair) {
+        const float up = __shfl_xor(c, 1);  // columns 2i (gate) and 2i+1 (up) in neighbouring lanes
+        if (m < p.M && n < p.N && (li & 1) == 0) C[size_t(m) * p.ldc + (n >> 1)] = c / (1.0f + expf(-c)) * up;
+      } else if constexpr (EPI == kGemmResAdd) {
+        if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] += c;
+      } else {
+        if (m < p.M && n < p.N) C[size_t(m) * p.ldc + n] = c;
       }
     }
   }
@@ -902,6 +1049,36 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
 // column tile of k_gemm_tile: 128 when that alone gives a tile per CU, else 64
 uint32_t tile_bn(uint32_t M, uint32_t N) { return ceil_div(M, 128) * ceil_div(N, 128) >= 256 ? 128 : 64; }
 
+// register prefetch depth of k_gemm_tile: stages in flight per thread
+constexpr int kTileDepth = 2;
+
+// k_gemm_rows8 serves M rows of a K-deep product
+bool rows_kernel(uint32_t M, uint32_t K) { return M > kGemmTileMinM && M <= kGemmRowsMaxM && K % 64 == 0; }
+
+// k_gemm_rows8 over `splits` K splits (K % (64 splits) == 0, checked by the callers)
+template <bool NRM, int E>
+void launch_rows(const GemmParams& p, uint32_t splits, hipStream_t st) {
+  const dim3 g(ceil_div(p.N, 128), ceil_div(p.M, 64), splits);
+  hipLaunchKernelGGL((k_gemm_rows8<NRM, E, 128, 1>), g, dim3(512), 0, st, p);
+}
+
+// k_gemm_tile over `splits` K splits (K % (32 splits) == 0, checked by the callers), with the
+// deepest register prefetch that divides the stage count
+template <bool NRM, int E>
+void launch_tile(const GemmParams& p, uint32_t splits, hipStream_t st) {
+  const uint32_t bn = tile_bn(p.M, p.N), nst = p.K / splits / 32;
+  const dim3 tg(ceil_div(p.N, bn), ceil_div(p.M, 128), splits);
+#define QE_TILE_D(D)                                                                             \
+  do {                                                                                           \
+    if (bn == 128) hipLaunchKernelGGL((k_gemm_tile<NRM, E, 128, D>), tg, dim3(256), 0, st, p);   \
+    else hipLaunchKernelGGL((k_gemm_tile<NRM, E, 64, D>), tg, dim3(256), 0, st, p);              \
+  } while (0)
+  if (nst % kTileDepth == 0) QE_TILE_D(kTileDepth);
+  else if (nst % 2 == 0) QE_TILE_D(2);
+  else QE_TILE_D(1);
+#undef QE_TILE_D
+}
+
 // ---------------------------------------------------------------------------------------------
 // Matvec over the NV = M token rows of a short verify pass or chunk (M <= kMvRowsMaxM): the
 // decode step's matvec layout. A row group of TPR threads covers one weight row in 8-column
@@ -1115,18 +1292,19 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st) 
     return hipGetLastError();
   }
   if (norm && !p.rowscale) return hipErrorInvalidValue;
+  if (rows_kernel(p.M, p.K)) {
+    if (norm && epi == kGemmStore) launch_rows<true, kGemmStore>(p, 1, st);
+    else if (norm && epi == kGemmSiluPair) launch_rows<true, kGemmSiluPair>(p, 1, st);
+    else if (!norm && epi == kGemmStore) launch_rows<false, kGemmStore>(p, 1, st);
+    else if (!norm && epi == kGemmResAdd) launch_rows<false, kGemmResAdd>(p, 1, st);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (p.M > kGemmTileMinM) {
-    const uint32_t bn = tile_bn(p.M, p.N);
-    const dim3 tg(ceil_div(p.N, bn), ceil_div(p.M, 128));
-#define QE_TILE(NRM, E)                                                                          \
-  do {                                                                                           \
-    if (bn == 128) hipLaunchKernelGGL((k_gemm_tile<NRM, E, 128>), tg, dim3(256), 0, st, p);      \
-    else hipLaunchKernelGGL((k_gemm_tile<NRM, E, 64>), tg, dim3(256), 0, st, p);                 \
-  } while (0)
-    if (norm && epi == kGemmStore) QE_TILE(true, kGemmStore);
-    else if (norm && epi == kGemmSiluPair) QE_TILE(true, kGemmSiluPair);
-    else if (!norm && epi == kGemmStore) QE_TILE(false, kGemmStore);
-    else if (!norm && epi == kGemmResAdd) QE_TILE(false, kGemmResAdd);
+    if (norm && epi == kGemmStore) launch_tile<true, kGemmStore>(p, 1, st);
+    else if (norm && epi == kGemmSiluPair) launch_tile<true, kGemmSiluPair>(p, 1, st);
+    else if (!norm && epi == kGemmStore) launch_tile<false, kGemmStore>(p, 1, st);
+    else if (!norm && epi == kGemmResAdd) launch_tile<false, kGemmResAdd>(p, 1, st);
     else return hipErrorInvalidValue;
     return hipGetLastError();
   }
@@ -1163,6 +1341,9 @@ uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K) {
   } else if (M <= kGemmTileMinM) {
     tiles = ceil_div(N, 64) * ceil_div(M, 64);
     unit = 64;
+  } else if (rows_kernel(M, K)) {
+    tiles = ceil_div(N, 128) * ceil_div(M, 64);
+    unit = 64;
   } else {
     tiles = ceil_div(N, tile_bn(M, N)) * ceil_div(M, 128);
     unit = 32;
@@ -1180,12 +1361,13 @@ hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t s
     launch_skinny<false, kGemmPartial>(p, splits, st);
     return hipGetLastError();
   }
+  if (rows_kernel(p.M, p.K) && p.K % (64 * splits) == 0) {
+    launch_rows<false, kGemmPartial>(p, splits, st);
+    return hipGetLastError();
+  }
   if (p.M > kGemmTileMinM) {
     if (p.K % (32 * splits)) return hipErrorInvalidValue;
-    const uint32_t bn = tile_bn(p.M, p.N);
-    const dim3 tg(ceil_div(p.N, bn), ceil_div(p.M, 128), splits);
-    if (bn == 128) hipLaunchKernelGGL((k_gemm_tile<false, kGemmPartial, 128>), tg, dim3(256), 0, st, p);
-    else hipLaunchKernelGGL((k_gemm_tile<false, kGemmPartial, 64>), tg, dim3(256), 0, st, p);
+    launch_tile<false, kGemmPartial>(p, splits, st);
     return hipGetLastError();
   }
   if (p.K % (64 * splits)) return hipErrorInvalidValue;
