@@ -769,56 +769,70 @@ __global__ __launch_bounds__(256) void k_qk_rope(BatchAttnParams p) {
 // operands: q, and f32 K / V, are split into hi + lo bf16 (K and V once, when a tile is staged
 // in LDS), and each product keeps the hi*hi, hi*lo and lo*hi terms (lo*lo is below 2^-16 of the
 // product); a bf16 cache is exact in hi, so its tiles take two terms.
-// Workgroup (KV head g, block of TOK = 64 / G tokens, key run s) serves 64 query rows, row
-// r = token mb + r / G of head g G + r % G; wave w owns rows 16 w .. 16 w + 15 and lane l the
-// row 16 w + l % 16. Keys come in LDS tiles of 64 positions (the next tile is loaded into
-// registers while this one is used). Per tile a wave computes the transposed scores
-// S^T[key][row] (A = K rows: lane has key 16 j + l % 16, dims 32 s + 8 kg .. +7 with
+// Workgroup (KV head g, block of TOK = 64 RB / G tokens, key run s) serves 64 RB query rows,
+// row r = token mb + r / G of head g G + r % G; wave w owns RB blocks of 16 rows (rows 16 (RB w
+// + b) .. + 15) and lane l the row l % 16 of each. Keys come in LDS tiles of 64 positions (the
+// next tile is loaded into registers while this one is used), and every fragment a wave reads
+// from LDS feeds the MFMAs of all its RB row blocks. Per tile a wave computes the transposed
+// scores S^T[key][row] (A = K rows: lane has key 16 j + l % 16, dims 32 s + 8 kg .. +7 with
 // kg = l / 16; B = q of row l % 16, same dims). In the 16 x 16 output layout a lane then holds
 // keys 16 j + 4 kg + r (j, r < 4) of its own row, so the online softmax (max, rescale, sum)
 // stays in the lane plus two shuffles across kg, with no LDS round trip for P. Next
 // O^T[d][row] += V^T P^T, with the k index of a 32-key step mapped so that lane kg's eight B
 // values are its own probabilities for keys 4 kg + r and 16 + 4 kg + r (r < 4); the A side
-// reads those keys from a transposed V tile (Vt[d][key], written from key pairs when staging),
-// and O^T's column is again the lane's row. Rows with no visible key in the run keep m = -inf,
+// reads those keys from a transposed V tile whose key slots are permuted to match (Vt[d][slot],
+// key 32 s + 16 h + 4 kg + r in slot 32 s + 8 kg + 4 h + r), so a lane's eight keys are one
+// 16-byte read, and O^T's column is again the lane's row. Rows with no visible key in the run keep m = -inf,
 // l = 0. One run: normalized output to att [M][n_heads][128]; several: (m, l, acc) partials to
 // part [M][n_heads][runs][kPartStride], combined by k_attn_merge_rows.
 // ---------------------------------------------------------------------------------------------
-template <int G, bool KV_BF16>
+template <int G, bool KV_BF16, int RB>
 __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
-  constexpr int D = kHeadDim, BK = 64, TOK = 64 / G, KP = D + 8, VP = BK + 8, NL = KV_BF16 ? 1 : 2;
+  constexpr int D = kHeadDim, BK = 64, TOK = 64 * RB / G, KP = D + 8, VP = BK + 8, NL = KV_BF16 ? 1 : 2;
   __shared__ __align__(16) uint16_t ks[NL][BK][KP];  // [hi, lo][key][dim]
-  __shared__ __align__(16) uint16_t vt[NL][D][VP];   // [hi, lo][dim][key]
+  __shared__ __align__(16) uint16_t vt[NL][D][VP];   // [hi, lo][dim][key slot]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
   const uint32_t g = blockIdx.x, mb = blockIdx.y * TOK, run = blockIdx.z, runs = gridDim.z;
-  const uint32_t row = uint32_t(wave) * 16 + uint32_t(li);
-  const uint32_t tok = mb + row / G, head = g * G + row % G;
-  const uint32_t tok_c = min(tok, p.M - 1);
-  const uint32_t my_pos = p.start + tok_c;
+  uint32_t tok[RB], head[RB], my_pos[RB];
+#pragma unroll
+  for (int b = 0; b < RB; b++) {
+    const uint32_t row = uint32_t(wave * RB + b) * 16 + uint32_t(li);
+    tok[b] = mb + row / G;
+    head[b] = g * G + row % G;
+    my_pos[b] = p.start + min(tok[b], p.M - 1);
+  }
   const uint32_t last = p.start + min(mb + TOK - 1, p.M - 1);  // positions 0..last are needed
   const uint32_t k_begin = run * p.key_run;
   const uint32_t k_end = min(last + 1, k_begin + p.key_run);  // this run: positions [k_begin, k_end)
 
-  bf16x8 qh[4], ql[4];
-  {
-    const float* qp = p.q + (size_t(tok_c) * p.n_heads + head) * D + 8 * kg;
+  bf16x8 qh[RB][4], ql[RB][4];
+#pragma unroll
+  for (int b = 0; b < RB; b++) {
+    const float* qp = p.q + (size_t(min(tok[b], p.M - 1)) * p.n_heads + head[b]) * D + 8 * kg;
 #pragma unroll
     for (int st = 0; st < 4; st++) {
-      const float4 a = *reinterpret_cast<const float4*>(qp + 32 * st);
-      const float4 b = *reinterpret_cast<const float4*>(qp + 32 * st + 4);
-      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      split8(v, qh[st], ql[st]);
+      const float4 x = *reinterpret_cast<const float4*>(qp + 32 * st);
+      const float4 y = *reinterpret_cast<const float4*>(qp + 32 * st + 4);
+      const float v[8] = {x.x, x.y, x.z, x.w, y.x, y.y, y.z, y.w};
+      split8(v, qh[b][st], ql[b][st]);
     }
   }
-  f32x4 o[8];
+  f32x4 o[RB][8];
+  float m_run[RB], l_run[RB];
 #pragma unroll
-  for (int i = 0; i < 8; i++) o[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int b = 0; b < RB; b++) {
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[b][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run[b] = -INFINITY;
+    l_run[b] = 0.f;
+  }
 
   // staging: K rows lr + 8 i (i < 8) at dims ld .. ld + 3 (coalesced rows); V key pair
   // 2 vk, 2 vk + 1 at dims 4 vb + 32 i .. +3 (i < 4), so that Vt gets (key, key + 1) words
   const size_t hbase = size_t(g) * p.max_seq * D;
   const int lr = tid >> 5, ld = (tid & 31) * 4, vk = tid & 31, vb = tid >> 5;
+  // Vt slot of keys 2 vk, 2 vk + 1 (adjacent slots): key 32 s + 16 h + 4 c + r -> 32 s + 8 c + 4 h + r
+  const int vslot = (2 * vk & 32) | ((2 * vk >> 2) & 3) << 3 | ((2 * vk >> 4) & 1) << 2 | (2 * vk & 3);
   using Pre = typename std::conditional<KV_BF16, uint2, float4>::type;
   Pre kp[8], vp[8];
   auto load_tile = [&](uint32_t t0) __attribute__((always_inline)) {
@@ -837,8 +851,8 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
   };
   typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
-  auto pk = [](float a, float b) __attribute__((always_inline)) {
-    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+  auto pk = [](float x, float y) __attribute__((always_inline)) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{x, y}), bf16x2));
   };
   auto store_tile = [&]() __attribute__((always_inline)) {
 #pragma unroll
@@ -858,20 +872,20 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
     for (int i = 0; i < 8; i += 2) {  // vp[i]: key 2 vk, vp[i + 1]: key 2 vk + 1, dims 4 vb + 16 i ..
       const int d0 = 4 * vb + 16 * i;
       if constexpr (KV_BF16) {
-        const uint2 a = vp[i], b = vp[i + 1];
-        const uint32_t w[4] = {(a.x & 0xFFFFu) | (b.x << 16), (a.x >> 16) | (b.x & 0xFFFF0000u),
-                               (a.y & 0xFFFFu) | (b.y << 16), (a.y >> 16) | (b.y & 0xFFFF0000u)};
+        const uint2 x = vp[i], y = vp[i + 1];
+        const uint32_t w[4] = {(x.x & 0xFFFFu) | (y.x << 16), (x.x >> 16) | (y.x & 0xFFFF0000u),
+                               (x.y & 0xFFFFu) | (y.y << 16), (x.y >> 16) | (y.y & 0xFFFF0000u)};
 #pragma unroll
-        for (int c = 0; c < 4; c++) *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][2 * vk]) = w[c];
+        for (int c = 0; c < 4; c++) *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][vslot]) = w[c];
       } else {
-        const float a[4] = {vp[i].x, vp[i].y, vp[i].z, vp[i].w};
-        const float b[4] = {vp[i + 1].x, vp[i + 1].y, vp[i + 1].z, vp[i + 1].w};
+        const float x[4] = {vp[i].x, vp[i].y, vp[i].z, vp[i].w};
+        const float y[4] = {vp[i + 1].x, vp[i + 1].y, vp[i + 1].z, vp[i + 1].w};
 #pragma unroll
         for (int c = 0; c < 4; c++) {
-          const uint32_t h = pk(a[c], b[c]);
-          *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][2 * vk]) = h;
-          *reinterpret_cast<uint32_t*>(&vt[NL - 1][d0 + c][2 * vk]) =
-              pk(a[c] - __uint_as_float(h << 16), b[c] - __uint_as_float(h & 0xFFFF0000u));
+          const uint32_t h = pk(x[c], y[c]);
+          *reinterpret_cast<uint32_t*>(&vt[0][d0 + c][vslot]) = h;
+          *reinterpret_cast<uint32_t*>(&vt[NL - 1][d0 + c][vslot]) =
+              pk(x[c] - __uint_as_float(h << 16), y[c] - __uint_as_float(h & 0xFFFF0000u));
         }
       }
     }
@@ -883,90 +897,103 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
     __syncthreads();
     if (t0 + BK < k_end) load_tile(t0 + BK);
 
-    f32x4 s[4];
+    f32x4 s[RB][4];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
-      s[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int b = 0; b < RB; b++) s[b][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 4; st++) {
         const bf16x8 kh = *reinterpret_cast<const bf16x8*>(&ks[0][16 * j + li][32 * st + 8 * kg]);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[st], s[j], 0, 0, 0);
-        s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[st], s[j], 0, 0, 0);
-        if constexpr (!KV_BF16) {
-          const bf16x8 kl = *reinterpret_cast<const bf16x8*>(&ks[NL - 1][16 * j + li][32 * st + 8 * kg]);
-          s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[st], s[j], 0, 0, 0);
+        bf16x8 kl;
+        if constexpr (!KV_BF16) kl = *reinterpret_cast<const bf16x8*>(&ks[NL - 1][16 * j + li][32 * st + 8 * kg]);
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+          s[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, qh[b][st], s[b][j], 0, 0, 0);
+          s[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kh, ql[b][st], s[b][j], 0, 0, 0);
+          if constexpr (!KV_BF16) s[b][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kl, qh[b][st], s[b][j], 0, 0, 0);
         }
       }
     }
-    float mx = -INFINITY;
+    bf16x8 ph[RB][2], pl[RB][2];
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
+    for (int b = 0; b < RB; b++) {
+      float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const uint32_t t = t0 + uint32_t(16 * j + 4 * kg + r);
-        const float v = t <= my_pos && t < k_end ? s[j][r] * p.scale : -INFINITY;
-        s[j][r] = v;
-        mx = fmaxf(mx, v);
+      for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const uint32_t t = t0 + uint32_t(16 * j + 4 * kg + r);
+          const float v = t <= my_pos[b] && t < k_end ? s[b][j][r] * p.scale : -INFINITY;
+          s[b][j][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run[b], mx);  // -inf while no key of the run is visible to this row
+      const float corr = m_run[b] == -INFINITY ? 0.f : expf(m_run[b] - m_new);
+      float sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float e = s[b][j][r] == -INFINITY ? 0.f : expf(s[b][j][r] - m_new);
+          s[b][j][r] = e;
+          sum += e;
+        }
+      }
+      sum += __shfl_xor(sum, 16);
+      sum += __shfl_xor(sum, 32);
+      l_run[b] = l_run[b] * corr + sum;
+      m_run[b] = m_new;
+#pragma unroll
+      for (int i = 0; i < 8; i++) o[b][i] *= corr;
+#pragma unroll
+      for (int st = 0; st < 2; st++) {
+        const float pv[8] = {s[b][2 * st][0], s[b][2 * st][1], s[b][2 * st][2], s[b][2 * st][3],
+                             s[b][2 * st + 1][0], s[b][2 * st + 1][1], s[b][2 * st + 1][2], s[b][2 * st + 1][3]};
+        split8(pv, ph[b][st], pl[b][st]);
       }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16));
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);  // -inf while no key of the run is visible to this row
-    const float corr = m_run == -INFINITY ? 0.f : expf(m_run - m_new);
-    float sum = 0.f;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float e = s[j][r] == -INFINITY ? 0.f : expf(s[j][r] - m_new);
-        s[j][r] = e;
-        sum += e;
-      }
-    }
-    sum += __shfl_xor(sum, 16);
-    sum += __shfl_xor(sum, 32);
-    l_run = l_run * corr + sum;
-    m_run = m_new;
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] *= corr;
 #pragma unroll
     for (int st = 0; st < 2; st++) {
-      const float pv[8] = {s[2 * st][0], s[2 * st][1], s[2 * st][2], s[2 * st][3],
-                           s[2 * st + 1][0], s[2 * st + 1][1], s[2 * st + 1][2], s[2 * st + 1][3]};
-      bf16x8 ph, pl;
-      split8(pv, ph, pl);
 #pragma unroll
       for (int i = 0; i < 8; i++) {
-        const int d = 16 * i + li, k0 = 32 * st + 4 * kg;
-        const uint2 a = *reinterpret_cast<const uint2*>(&vt[0][d][k0]);
-        const uint2 b = *reinterpret_cast<const uint2*>(&vt[0][d][k0 + 16]);
-        const bf16x8 vh = __builtin_bit_cast(bf16x8, u32x4{a.x, a.y, b.x, b.y});
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph, o[i], 0, 0, 0);
-        o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl, o[i], 0, 0, 0);
-        if constexpr (!KV_BF16) {
-          const uint2 c = *reinterpret_cast<const uint2*>(&vt[NL - 1][d][k0]);
-          const uint2 e = *reinterpret_cast<const uint2*>(&vt[NL - 1][d][k0 + 16]);
-          const bf16x8 vl = __builtin_bit_cast(bf16x8, u32x4{c.x, c.y, e.x, e.y});
-          o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph, o[i], 0, 0, 0);
+        const bf16x8 vh = *reinterpret_cast<const bf16x8*>(&vt[0][16 * i + li][32 * st + 8 * kg]);
+        bf16x8 vl;
+        if constexpr (!KV_BF16) vl = *reinterpret_cast<const bf16x8*>(&vt[NL - 1][16 * i + li][32 * st + 8 * kg]);
+#pragma unroll
+        for (int b = 0; b < RB; b++) {
+          o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[b][st], o[b][i], 0, 0, 0);
+          o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pl[b][st], o[b][i], 0, 0, 0);
+          if constexpr (!KV_BF16) o[b][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vl, ph[b][st], o[b][i], 0, 0, 0);
         }
       }
     }
   }
-  if (tok >= p.M) return;
   // lane holds O^T[16 i + 4 kg + r][row], r < 4
-  const size_t vec = size_t(tok) * p.n_heads + head;
-  if (runs == 1) {
-    const float inv = 1.0f / l_run;
-    float* out = p.att + vec * D + 4 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      *reinterpret_cast<float4*>(out + 16 * i) = make_float4(o[i][0] * inv, o[i][1] * inv, o[i][2] * inv, o[i][3] * inv);
-  } else {
-    float* out = p.part + (vec * runs + run) * kPartStride;
-    if (kg == 0) { out[0] = m_run; out[1] = l_run; }
+  for (int b = 0; b < RB; b++) {
+    if (tok[b] >= p.M) continue;
+    const size_t vec = size_t(tok[b]) * p.n_heads + head[b];
+    if (runs == 1) {
+      const float inv = 1.0f / l_run[b];
+      float* out = p.att + vec * D + 4 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-      *reinterpret_cast<float4*>(out + 4 + 16 * i + 4 * kg) = make_float4(o[i][0], o[i][1], o[i][2], o[i][3]);
+      for (int i = 0; i < 8; i++)
+        *reinterpret_cast<float4*>(out + 16 * i) =
+            make_float4(o[b][i][0] * inv, o[b][i][1] * inv, o[b][i][2] * inv, o[b][i][3] * inv);
+    } else {
+      float* out = p.part + (vec * runs + run) * kPartStride;
+      if (kg == 0) {
+        out[0] = m_run[b];
+        out[1] = l_run[b];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; i++)
+        *reinterpret_cast<float4*>(out + 4 + 16 * i + 4 * kg) = make_float4(o[b][i][0], o[b][i][1], o[b][i][2], o[b][i][3]);
+    }
   }
 }
 
@@ -1389,6 +1416,11 @@ hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+// Row blocks per wave of k_attn_causal_bf. One: at 2048 tokens in chunks of 512, two (half the
+// workgroups, each LDS fragment feeding twice the MFMAs) took 15.1 ms against 13.9, and eight
+// waves of one block (twice the LDS reads per tile) 14.6.
+constexpr uint32_t kAttnCausalRB = 1;
+
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st) {
   if (!p.n_kv || p.n_heads % p.n_kv || runs == 0 || runs > uint32_t(kBatchMaxRuns) || (runs > 1 && !p.part))
     return hipErrorInvalidValue;
@@ -1398,12 +1430,13 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
   const uint32_t tiles = ceil_div(p.start + p.M, 64), per_run = ceil_div(tiles, runs);
   runs = ceil_div(tiles, per_run);
   q.key_run = 64 * per_run;
-  const dim3 grid(p.n_kv, ceil_div(p.M, 64 / G), runs);
+  constexpr uint32_t RB = kAttnCausalRB;
+  const dim3 grid(p.n_kv, ceil_div(p.M, 64 * RB / G), runs);
   hipError_t e = hipErrorInvalidValue;
 #define QE_ATT(GG)                                                                                         \
   if (G == GG) {                                                                                           \
-    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal_bf<GG, true>), grid, dim3(256), 0, st, q);            \
-    else hipLaunchKernelGGL((k_attn_causal_bf<GG, false>), grid, dim3(256), 0, st, q);                     \
+    if (p.kv_bf16) hipLaunchKernelGGL((k_attn_causal_bf<GG, true, RB>), grid, dim3(256), 0, st, q);        \
+    else hipLaunchKernelGGL((k_attn_causal_bf<GG, false, RB>), grid, dim3(256), 0, st, q);                 \
     e = hipGetLastError();                                                                                 \
   }
   QE_ATT(1)
@@ -1423,7 +1456,7 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
 
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv) {
   if (!M || !n_kv || n_heads % n_kv || n_heads / n_kv > 16) return 1;
-  const uint32_t wgs = n_kv * ceil_div(M, 64 / (n_heads / n_kv));
+  const uint32_t wgs = n_kv * ceil_div(M, 64 * kAttnCausalRB / (n_heads / n_kv));
   // at least 4 runs, more while that leaves under 512 workgroups (measured: 4 runs beat 2 and 8
   // at M = 512 and 1 and 2 at M = 2048); at most kBatchMaxRuns
   uint32_t runs = std::min(std::max(ceil_div(512, wgs), 4u), uint32_t(kBatchMaxRuns));
