@@ -101,8 +101,11 @@ def measured_copy(torch) -> float:
 def pmc_traffic(stage: str):
     """HBM bytes per launch of `stage` from the committed rocprofv3 counter summary
     (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the same counter's reading for the
-    1 GiB copy), or None when the summary does not cover that stage."""
-    path = os.path.join(ROOT, "profiles", "decode_step_qwen3_0_6b_pmc.json")
+    1 GiB copy), or None when the summary does not cover that stage. The attention's figure is
+    from the counter runs without the L2 prefetch, so that it covers the same bytes as the
+    attention's algorithmic bytes (its own K/V, q/k/v and output)."""
+    name = "decode_step_qwen3_0_6b_pmc_no_prefetch.json" if stage == "attention" else "decode_step_qwen3_0_6b_pmc.json"
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             summary = json.load(f)

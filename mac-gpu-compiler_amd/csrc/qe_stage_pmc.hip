@@ -6,10 +6,11 @@
 // the attention launch's L2 prefetch of the layer's gate/up and down weights.
 //
 //   qe_stage_pmc [--pos P] [--no-prefetch]   (attention attends positions 0..P, default 193)
-//   qe_stage_pmc --gemm   the chunked prefill's GEMM (k_gemm_tile) instead, 3 launches at each of
-//                         M x N x K = 2048 x 4096 x 1024 (q|k|v of a 2048-token chunk) and
-//                         512 x 6144 x 1024 (gate|up of a 512-token chunk), for the matrix-core
-//                         counters (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, ...)
+//   qe_stage_pmc --gemm   the chunked prefill's GEMM instead (launch_gemm, no norm, plain store),
+//                         3 launches at each of M x N x K = 2048 x 4096 x 1024 (q|k|v of a
+//                         2048-token chunk: k_gemm_tile), 512 x 6144 x 1024 and 512 x 4096 x 1024
+//                         (gate|up and q|k|v of a 512-token chunk: k_gemm_rows8), for the
+//                         matrix-core counters (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, ...)
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -67,7 +68,7 @@ int main(int argc, char** argv) {
     CK(hipSetDevice(0));
     hipStream_t gs;
     CK(hipStreamCreate(&gs));
-    const uint32_t shapes[2][3] = {{2048, 4096, 1024}, {512, 6144, 1024}};
+    const uint32_t shapes[3][3] = {{2048, 4096, 1024}, {512, 6144, 1024}, {512, 4096, 1024}};
     for (const auto& sh : shapes) {
       const uint32_t M = sh[0], N = sh[1], K = sh[2];
       float* A = dalloc<float>(size_t(M) * K);

@@ -3,8 +3,8 @@
   python mac-gpu-compiler_amd/pmc_kernels.py RUN1.csv [RUN2.csv ...]
 
 Each argument is the counter_collection CSV of one `rocprofv3 --pmc ...` run (one row per
-dispatch and counter). Prints a markdown table: per kernel, the dispatches and the mean value of
-every counter per dispatch, over all runs given.
+dispatch and counter). Prints a markdown table: per kernel and grid size (threads), the dispatches
+and the mean value of every counter per dispatch, over all runs given.
 """
 import csv
 import sys
@@ -18,6 +18,7 @@ def main(paths):
         with open(path, newline="") as f:
             for r in csv.DictReader(f):
                 k = r["Kernel_Name"]
+                k = (k if len(k) <= 60 else k[:57] + "...") + f" [grid {r.get('Grid_Size', '?')}]"
                 vals[k][r["Counter_Name"]].append(float(r["Counter_Value"]))
                 disp[k].add((path, r.get("Dispatch_Id", r.get("Correlation_Id", ""))))
     counters = sorted({c for k in vals for c in vals[k]})
@@ -28,8 +29,7 @@ def main(paths):
         for c in counters:
             v = vals[k].get(c)
             cells.append(f"{sum(v) / len(v):,.0f}" if v else "")
-        name = k if len(k) <= 60 else k[:57] + "..."
-        print(f"| `{name}` | {len(disp[k])} | " + " | ".join(cells) + " |")
+        print(f"| `{k}` | {len(disp[k])} | " + " | ".join(cells) + " |")
 
 
 if __name__ == "__main__":
