@@ -94,9 +94,19 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
 // key runs for a chunk of M tokens at positions start.. : at least 4, more while the chunk has
 // under 512 workgroups, and at most one per 128 keys
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv);
-// tokens[r] = greedy token of row r of logits [rows][V] (the decode step's argmax rule)
-hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, hipStream_t st);
+// tokens[r] = greedy token of row r of logits [rows][V] (the decode step's argmax rule);
+// cand: rows * kArgParts candidates of scratch (device memory); rows <= 65535
+constexpr uint32_t kArgParts = 64;
+hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, ArgCand* cand,
+                             hipStream_t st);
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
+                             hipStream_t st);
+// The ids of a short pass (M <= kIdsByValue) as a kernel argument: no host-to-device copy.
+constexpr uint32_t kIdsByValue = 64;
+struct TokenIds {
+  uint32_t id[kIdsByValue];
+};
+hipError_t launch_embed_rows(const uint16_t* table, const TokenIds& ids, uint32_t M, uint32_t H, float* x,
                              hipStream_t st);
 
 }  // namespace qe

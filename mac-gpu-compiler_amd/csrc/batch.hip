@@ -1030,25 +1030,30 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float* __restrict
 
 // tokens[r] = the greedy token of logits row r by the reference's scan (bench.rs:98-103,
 // main.rs:37-42): the largest non-NaN value, lowest index on ties, and 0 when the row starts
-// with NaN. One workgroup per row; each thread's loads of a pass are issued together.
-__global__ __launch_bounds__(1024) void k_row_argmax(const float* __restrict__ logits, uint32_t V,
-                                                     uint32_t* __restrict__ tokens) {
-  __shared__ float sv[16];
-  __shared__ uint32_t si[16];
+// with NaN (or has nothing above -inf). Two launches: kArgParts workgroups per row each reduce
+// one slice of the row to a (value, index) candidate, then one wave per row reduces the
+// candidates. The comparison is a total order on (value, index) among non-NaN values, so the
+// result does not depend on how the row is cut.
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_row_argmax_part(const float* __restrict__ logits, uint32_t V, uint32_t S,
+                                                         ArgCand* __restrict__ cand) {
+  __shared__ float sv[4];
+  __shared__ uint32_t si[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const float* x = logits + size_t(blockIdx.x) * V;
+  const float* x = logits + size_t(blockIdx.y) * V;
+  const uint32_t beg = blockIdx.x * S, end = min(V, beg + S);
   float bv = -INFINITY;
   uint32_t bi = 0xFFFFFFFFu;
-  constexpr int U = 8;
-  for (uint32_t base = 0; base < V; base += 1024u * U) {
+  constexpr int U = 4;
+  for (uint32_t base = beg; base < end; base += 256u * U) {
     float v[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) v[u] = x[min(base + uint32_t(tid) + 1024u * u, V - 1)];
+    for (int u = 0; u < U; u++) v[u] = x[min(base + uint32_t(tid) + 256u * u, V - 1)];
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int u = 0; u < U; u++) {
-      const uint32_t i = base + uint32_t(tid) + 1024u * u;
-      if (i < V && cand_better(v[u], i, bv, bi)) { bv = v[u]; bi = i; }  // NaN never wins
+      const uint32_t i = base + uint32_t(tid) + 256u * u;
+      if (i < end && cand_better(v[u], i, bv, bi)) { bv = v[u]; bi = i; }  // NaN never wins
     }
   }
   for (int o = 1; o < 64; o <<= 1) {
@@ -1059,10 +1064,27 @@ __global__ __launch_bounds__(1024) void k_row_argmax(const float* __restrict__ l
   if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
   __syncthreads();
   if (tid == 0) {
-    for (int w = 1; w < 16; w++)
+    for (int w = 1; w < 4; w++)
       if (cand_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
-    tokens[blockIdx.x] = (isnan(x[0]) || bi == 0xFFFFFFFFu) ? 0u : bi;
+    cand[size_t(blockIdx.y) * kArgParts + blockIdx.x] = ArgCand{bv, bi};
   }
+}
+
+__global__ __launch_bounds__(64) void k_row_argmax_final(const ArgCand* __restrict__ cand,
+                                                         const float* __restrict__ logits, uint32_t V,
+                                                         uint32_t* __restrict__ tokens) {
+  static_assert(kArgParts == 64, "one candidate per lane");
+  const uint32_t row = blockIdx.x, lane = threadIdx.x;
+  const ArgCand c = cand[size_t(row) * kArgParts + lane];
+  const bool nan0 = isnan(logits[size_t(row) * V]);
+  float bv = c.v;
+  uint32_t bi = c.i;
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    if (cand_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) tokens[row] = (nan0 || bi == 0xFFFFFFFFu) ? 0u : bi;
 }
 
 // x[m] = bf16 embedding row of ids[m] (cpu_inference.rs:109-111)
@@ -1071,6 +1093,14 @@ __global__ __launch_bounds__(256) void k_embed_rows(const uint16_t* __restrict__
   const uint32_t m = blockIdx.y;
   for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < H; i += gridDim.x * 256)
     x[size_t(m) * H + i] = bf16f(table[size_t(ids[m]) * H + i]);
+}
+
+// the same with the ids in the kernel argument
+__global__ __launch_bounds__(256) void k_embed_rows_v(const uint16_t* __restrict__ table, TokenIds ids, uint32_t H,
+                                                      float* __restrict__ x) {
+  const uint32_t m = blockIdx.y;
+  for (uint32_t i = blockIdx.x * 256 + threadIdx.x; i < H; i += gridDim.x * 256)
+    x[size_t(m) * H + i] = bf16f(table[size_t(ids.id[m]) * H + i]);
 }
 
 // column tile of k_gemm_tile: 128 when that alone gives a tile per CU, else 64
@@ -1463,15 +1493,25 @@ uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t
   return std::max(1u, std::min(runs, ceil_div(start + M, 128)));
 }
 
-hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, hipStream_t st) {
-  if (!rows || !V) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_row_argmax, dim3(rows), dim3(1024), 0, st, logits, V, tokens);
+hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, ArgCand* cand,
+                             hipStream_t st) {
+  if (!rows || !V || !cand || rows > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_row_argmax_part, dim3(kArgParts, rows), dim3(256), 0, st, logits, V, ceil_div(V, kArgParts),
+                     cand);
+  hipLaunchKernelGGL(k_row_argmax_final, dim3(rows), dim3(64), 0, st, cand, logits, V, tokens);
   return hipGetLastError();
 }
 
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
                              hipStream_t st) {
   hipLaunchKernelGGL(k_embed_rows, dim3(ceil_div(H, 256), M), dim3(256), 0, st, table, ids, M, H, x);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(const uint16_t* table, const TokenIds& ids, uint32_t M, uint32_t H, float* x,
+                             hipStream_t st) {
+  if (M == 0 || M > kIdsByValue) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_embed_rows_v, dim3(ceil_div(H, 256), M), dim3(256), 0, st, table, ids, H, x);
   return hipGetLastError();
 }
 

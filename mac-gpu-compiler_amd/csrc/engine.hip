@@ -81,6 +81,7 @@ size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 constexpr uint32_t kBatchDefaultChunk = 512;  // tokens per chunk of qe_prefill_batch (chunk = 0)
 constexpr uint32_t kBatchMaxChunk = 2048;
 constexpr uint32_t kVerifyMaxTokens = 64;  // tokens of one qe_verify call
+static_assert(kVerifyMaxTokens <= qe::kIdsByValue, "verify ids travel in a kernel argument");
 
 }  // namespace
 
@@ -125,7 +126,7 @@ struct qe_model {
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
   float* bpart = nullptr;   // causal attention partials
   float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
-  uint32_t* btok = nullptr;  // greedy tokens of verify rows [kVerifyMaxTokens]
+  ArgCand* bcand = nullptr;  // row argmax candidates of a verify pass [kVerifyMaxTokens][kArgParts]
   float* blogits = nullptr;
   uint32_t* ids_dev = nullptr;  // the token ids of one qe_prefill_batch / qe_verify call
   uint64_t ids_cap = 0;
@@ -494,7 +495,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   part_rows = std::max(part_rows, size_t(std::min<uint32_t>(cap, 8)) * qe::kAttnMaxSplits);
   const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
   const size_t osplit = take(size_t(8) * cap * H * 4);  // gemm_splits returns at most 8
-  const size_t otok = take(size_t(kVerifyMaxTokens) * 4);
+  const size_t ocand = take(size_t(kVerifyMaxTokens) * qe::kArgParts * sizeof(ArgCand));
   HIP_TRY(hipStreamSynchronize(m->stream));
   if (m->batch_mem) HIP_TRY(hipFree(m->batch_mem));
   m->batch_mem = nullptr;
@@ -510,7 +511,7 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   m->blogits = reinterpret_cast<float*>(m->batch_mem + ologit);
   m->bpart = reinterpret_cast<float*>(m->batch_mem + opart);
   m->bsplit = reinterpret_cast<float*>(m->batch_mem + osplit);
-  m->btok = reinterpret_cast<uint32_t*>(m->batch_mem + otok);
+  m->bcand = reinterpret_cast<ArgCand*>(m->batch_mem + ocand);
   return QE_OK;
 }
 
@@ -530,10 +531,12 @@ int upload_ids(qe_model* m, const uint32_t* ids, uint64_t n) {
 
 enum BatchLogits { kNoLogits, kLastLogits, kAllLogits };
 
-// One chunk of M tokens (device ids) at positions start..start+M-1 through every layer,
-// appending their K/V. kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the
-// last row's logits to m->logits (the decode step's buffer); kNoLogits: none (an inner chunk).
-int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint32_t* ids, BatchLogits logits) {
+// One chunk of M tokens at positions start..start+M-1 through every layer, appending their K/V.
+// The ids are device memory (ids), or for a short pass the kernel argument ids_v (ids null).
+// kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the last row's logits to
+// m->logits (the decode step's buffer); kNoLogits: none (an inner chunk).
+int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint32_t* ids, BatchLogits logits,
+                  const qe::TokenIds* ids_v = nullptr) {
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -578,7 +581,8 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
     return QE_OK;
   };
   int rc;
-  HIP_TRY(qe::launch_embed_rows(m->embed, ids, M, H, m->bx, s));
+  if (ids_v) HIP_TRY(qe::launch_embed_rows(m->embed, *ids_v, M, H, m->bx, s));
+  else HIP_TRY(qe::launch_embed_rows(m->embed, ids, M, H, m->bx, s));
   if (!skinny) HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
@@ -973,13 +977,16 @@ int check_verify_args(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t
 int verify_greedy(qe_model* model, const uint32_t* ids, uint32_t k, uint64_t start_pos, qe_kv* kv, uint32_t* tokens) {
   int rc = ensure_batch(model, k, k);
   if (rc) return rc;
-  if ((rc = upload_ids(model, ids, k))) return rc;
-  if ((rc = enqueue_batch(model, kv, k, uint32_t(start_pos), model->ids_dev, kAllLogits))) return rc;
-  HIP_TRY(qe::launch_row_argmax(model->blogits, k, uint32_t(model->cfg.vocab_size), model->btok, model->stream));
-  // h_logits is pinned and idle here (no decode step is in flight on this stream)
-  HIP_TRY(hipMemcpyAsync(model->h_logits, model->btok, size_t(k) * 4, hipMemcpyDeviceToHost, model->stream));
+  qe::TokenIds tv{};  // k <= kVerifyMaxTokens = kIdsByValue: the ids travel in the kernel argument
+  std::copy(ids, ids + k, tv.id);
+  if ((rc = enqueue_batch(model, kv, k, uint32_t(start_pos), nullptr, kAllLogits, &tv))) return rc;
+  // the greedy tokens go straight to pinned host memory (h_logits is idle here: no decode step
+  // is in flight on this stream)
+  uint32_t* host_tok = reinterpret_cast<uint32_t*>(model->h_logits);
+  HIP_TRY(qe::launch_row_argmax(model->blogits, k, uint32_t(model->cfg.vocab_size), host_tok, model->bcand,
+                                model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
-  memcpy(tokens, model->h_logits, size_t(k) * 4);
+  memcpy(tokens, host_tok, size_t(k) * 4);
   kv->len = std::max<uint64_t>(kv->len, start_pos + k);
   return QE_OK;
 }
@@ -1014,8 +1021,9 @@ int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_p
   if (int rc = check_verify_args(model, ids, k, start_pos, kv)) return rc;
   int rc = ensure_batch(model, uint32_t(k), uint32_t(k));
   if (rc) return rc;
-  if ((rc = upload_ids(model, ids, k))) return rc;
-  if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), model->ids_dev, kAllLogits))) return rc;
+  qe::TokenIds tv{};
+  std::copy(ids, ids + k, tv.id);
+  if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), nullptr, kAllLogits, &tv))) return rc;
   HIP_TRY(hipMemcpyAsync(logits_out, model->blogits, size_t(k) * model->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
                          model->stream));
   HIP_TRY(hipStreamSynchronize(model->stream));
@@ -1203,7 +1211,20 @@ int qe_op_attention(const float* q, const float* k, const float* v, float* out, 
 int qe_op_argmax(const float* logits, uint64_t rows, uint64_t n, uint32_t* tokens_out, void* stream) {
   if (!logits || !tokens_out) return fail(QE_ERR_ARG, "null argument");
   if (rows == 0 || n == 0 || rows > 0x7FFFFFFFull || n > 0x7FFFFFFFull) return fail(QE_ERR_ARG, "need 0 < rows, n < 2^31");
-  HIP_TRY(qe::launch_row_argmax(logits, uint32_t(rows), uint32_t(n), tokens_out, static_cast<hipStream_t>(stream)));
+  // candidate scratch from the stream-ordered allocator, in batches of at most 65535 rows
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  const uint64_t batch = std::min<uint64_t>(rows, 65535);
+  ArgCand* cand = nullptr;
+  HIP_TRY(hipMallocAsync(reinterpret_cast<void**>(&cand), batch * qe::kArgParts * sizeof(ArgCand), st));
+  for (uint64_t r0 = 0; r0 < rows; r0 += batch) {
+    const uint32_t nr = uint32_t(std::min<uint64_t>(batch, rows - r0));
+    const hipError_t e = qe::launch_row_argmax(logits + r0 * n, nr, uint32_t(n), tokens_out + r0, cand, st);
+    if (e != hipSuccess) {
+      (void)hipFreeAsync(cand, st);
+      return fail(QE_ERR_HIP, "row argmax: %s", hipGetErrorString(e));
+    }
+  }
+  HIP_TRY(hipFreeAsync(cand, st));
   return QE_OK;
 }
 
