@@ -10,7 +10,9 @@
 namespace qe {
 
 // kGemmPartial: split over K; split z writes its partial sums to C + z M ldc (launch_gemm_split)
-enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2, kGemmPartial = 3 };
+// kGemmQkRope (launch_gemm_qk_rope): the q|k|v projection of a chunk with the per-head q/k
+// RMSNorm, RoPE and the K/V append of k_qk_rope in its epilogue
+enum GemmEpilogue { kGemmStore = 0, kGemmResAdd = 1, kGemmSiluPair = 2, kGemmPartial = 3, kGemmQkRope = 4 };
 
 // most key runs the causal attention of a chunk is split into (partials merged after)
 constexpr int kBatchMaxRuns = 32;
@@ -89,6 +91,12 @@ hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, 
 // cols % 8 == 0, cols <= 4096, 1 <= M <= kMvRowsMaxM; out must not alias x.
 hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st);
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
+// The q|k|v GEMM of a chunk (A = x with the input RMSNorm, W = [q | k | v] rows, N = (n_heads +
+// 2 n_kv) 128) with k_qk_rope's work in its epilogue: q rows normalized and rotated to a.q, k and
+// v rows (k normalized and rotated) appended to the cache at positions a.start + m. Returns
+// hipErrorNotSupported where the 64-row kernel does not serve the shape (the caller then runs
+// launch_gemm and launch_qk_rope).
+hipError_t launch_gemm_qk_rope(const GemmParams& g, const BatchAttnParams& a, hipStream_t st);
 // causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);
 // key runs for a chunk of M tokens at positions start.. : at least 4, more while the chunk has

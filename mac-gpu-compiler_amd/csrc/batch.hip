@@ -440,7 +440,7 @@ __global__ __launch_bounds__(256) void k_gemm_tile(GemmParams p) {
 // count K / 64 (per split) is a multiple of D. gridDim.z > 1 splits K as in k_gemm_lds.
 // ---------------------------------------------------------------------------------------------
 template <bool NORM, int EPI, int BN, int D>
-__global__ __launch_bounds__(512) void k_gemm_rows8(GemmParams p) {
+__global__ __launch_bounds__(512) void k_gemm_rows8(GemmParams p, BatchAttnParams qa) {
   constexpr int BK = 64, KP = BK + 8, NT = BN / 16;
   constexpr int WCH = BN * BK / 8 / 512;  // 16-byte W chunks per thread per step
   static_assert(WCH >= 1, "tile");
@@ -541,6 +541,62 @@ __global__ __launch_bounds__(512) void k_gemm_rows8(GemmParams p) {
   for (int j = 0; j < NT; j++) acc[j] += red[(wr * NT + j) * 64 + lane];
 
   // epilogue: lane holds C[m0 + 4 kg + r][n0 + 16 j + li]
+  if constexpr (EPI == kGemmQkRope) {
+    // the tile's 128 columns are one head (BN == 128 == head_dim): head hh of [q | k | v]. A row's
+    // 128 values sit in the 16 lanes of its kg group (8 each), and the RoPE pair (d, d + 64) is
+    // (j, j + 4) of one lane (cpu_inference.rs:134-141, 189-215).
+    static_assert(BN == kHeadDim && NT == 8, "one head per tile");
+    const uint32_t hh = n0 / kHeadDim;
+    const bool isq = hh < qa.n_heads, isk = !isq && hh < qa.n_heads + qa.n_kv;
+    float gn[NT];
+    const uint16_t* gsrc = isq ? qa.q_norm : qa.k_norm;
+#pragma unroll
+    for (int j = 0; j < NT; j++) gn[j] = isq || isk ? bf16f(gsrc[16 * j + li]) : 1.0f;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const uint32_t m = m0 + uint32_t(4 * kg + r), pos = qa.start + min(m, p.M - 1);
+      float v[NT];
+#pragma unroll
+      for (int j = 0; j < NT; j++) v[j] = acc[j][r];
+      if (isq || isk) {  // uniform over the workgroup
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < NT; j++) ss += v[j] * v[j];
+        ss += __shfl_xor(ss, 1);
+        ss += __shfl_xor(ss, 2);
+        ss += __shfl_xor(ss, 4);
+        ss += __shfl_xor(ss, 8);
+        const float sc = 1.0f / sqrtf(ss / float(kHeadDim) + qa.eps);
+#pragma unroll
+        for (int j = 0; j < NT; j++) v[j] = v[j] * sc * gn[j];
+        const float2* rope = reinterpret_cast<const float2*>(qa.rope) + size_t(pos) * (kHeadDim / 2);
+#pragma unroll
+        for (int j = 0; j < NT / 2; j++) {
+          const float2 cs = rope[16 * j + li];
+          const float a = v[j], b = v[j + NT / 2];
+          v[j] = a * cs.x - b * cs.y;
+          v[j + NT / 2] = b * cs.x + a * cs.y;
+        }
+      }
+      if (m < p.M) {
+        if (isq) {
+          float* q = qa.q + (size_t(m) * qa.n_heads + hh) * kHeadDim;
+#pragma unroll
+          for (int j = 0; j < NT; j++) q[16 * j + li] = v[j];
+        } else {
+          const uint32_t kvh = isk ? hh - qa.n_heads : hh - qa.n_heads - qa.n_kv;
+          void* cache = isk ? qa.k_cache : qa.v_cache;
+          const size_t slot = (size_t(kvh) * qa.max_seq + pos) * kHeadDim;
+#pragma unroll
+          for (int j = 0; j < NT; j++) {
+            if (qa.kv_bf16) static_cast<uint16_t*>(cache)[slot + 16 * j + li] = f32_to_bf16(v[j]);
+            else static_cast<float*>(cache)[slot + 16 * j + li] = v[j];
+          }
+        }
+      }
+    }
+    return;
+  }
   float* C = p.C + (EPI == kGemmPartial ? size_t(blockIdx.z) * p.M * p.ldc : 0);
 #pragma unroll
   for (int j = 0; j < NT; j++) {
@@ -1116,7 +1172,7 @@ bool rows_kernel(uint32_t M, uint32_t K) { return M > kGemmTileMinM && M <= kGem
 template <bool NRM, int E>
 void launch_rows(const GemmParams& p, uint32_t splits, hipStream_t st) {
   const dim3 g(ceil_div(p.N, 128), ceil_div(p.M, 64), splits);
-  hipLaunchKernelGGL((k_gemm_rows8<NRM, E, 128, 1>), g, dim3(512), 0, st, p);
+  hipLaunchKernelGGL((k_gemm_rows8<NRM, E, 128, 1>), g, dim3(512), 0, st, p, BatchAttnParams{});
 }
 
 // k_gemm_tile over `splits` K splits (K % (32 splits) == 0, checked by the callers), with the
@@ -1437,6 +1493,15 @@ hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, 
                                   float* s, hipStream_t st) {
   if (!M || N % 4 || !splits) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_resadd_partials, dim3(M), dim3(256), 0, st, x, part, splits, M, N, eps, s);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_qk_rope(const GemmParams& g, const BatchAttnParams& a, hipStream_t st) {
+  if (!rows_kernel(g.M, g.K) || g.M != a.M || g.N != (a.n_heads + 2 * a.n_kv) * kHeadDim || !g.rowscale || !g.gain ||
+      !a.q || !a.q_norm || !a.k_norm || !a.rope || !a.k_cache || !a.v_cache || g.lda % 4 || !g.A || !g.W)
+    return hipErrorNotSupported;
+  const dim3 grid(g.N / 128, ceil_div(g.M, 64), 1);
+  hipLaunchKernelGGL((k_gemm_rows8<true, kGemmQkRope, 128, 1>), grid, dim3(512), 0, st, g, a);
   return hipGetLastError();
 }
 

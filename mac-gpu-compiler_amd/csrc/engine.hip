@@ -586,8 +586,6 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
   if (!skinny) HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
-    // input_layernorm + q|k|v (cpu_inference.rs:129-132)
-    if ((rc = gemm(m->bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
     // q/k norm + RoPE, K/V append, causal attention (cpu_inference.rs:134-162)
     qe::BatchAttnParams a{};
     a.qkv = m->bqkv; a.q = m->bq; a.att = m->batt; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
@@ -596,7 +594,18 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
     a.M = M; a.start = start; a.max_seq = uint32_t(kv->max_seq);
     a.n_heads = uint32_t(c.num_attention_heads); a.n_kv = uint32_t(c.num_key_value_heads);
     a.eps = eps; a.scale = 1.0f / sqrtf(float(D)); a.kv_bf16 = kv->dtype == QE_KV_BF16;
-    HIP_TRY(qe::launch_qk_rope(a, s));
+    // input_layernorm + q|k|v (cpu_inference.rs:129-132); chunks on the 64-row GEMM do the q/k
+    // norm, RoPE and K/V append in its epilogue, the others in k_qk_rope
+    hipError_t fused = hipErrorNotSupported;
+    if (!mv && !skinny) {
+      const qe::GemmParams g{m->bx, H, m->bs, w.w_in, w.w_qkv, M, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, eps};
+      fused = qe::launch_gemm_qk_rope(g, a, s);
+      if (fused != hipSuccess && fused != hipErrorNotSupported) HIP_TRY(fused);
+    }
+    if (fused != hipSuccess) {
+      if ((rc = gemm(m->bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
+      HIP_TRY(qe::launch_qk_rope(a, s));
+    }
     const uint32_t rows_per_kv = (a.n_heads / a.n_kv) * M;
     if (m->rows_split_attn && (rows_per_kv == 1 || rows_per_kv == 2 || rows_per_kv == 4 || rows_per_kv == 8)) {
       // few tokens: the split kernel, the q heads of all M tokens of a KV head over one read of
