@@ -564,20 +564,30 @@ def main():
             stages.setdefault(name, ([], launches))[0].append(us)
     mean_pos = sum(prof_positions) / n_prof
     stage_bytes = qe.stage_bytes(cfg, mean_pos, el)
-    # The attention stage alone replays 28 attention launches back to back; in the step each one
-    # runs behind its layer's q|k|v launch, which it reads. Its in-step launch time is therefore
-    # taken as the q|k|v + attention pair's time minus the q|k|v stage's.
-    pair = stages.pop("qkv+attention", None)
-    if pair and "qkv" in stages and "attention" in stages:
-        (pd, pn), (qd, qn) = pair, stages["qkv"]
-        an = stages["attention"][1]
-        stages["attention"] = ([(p_us * pn - q_us * qn) / an for p_us, q_us in zip(pd, qd)], an)
-    kernel_table = {}
-    for name, (durs, per_step) in stages.items():
-        mean_us = sum(durs) / len(durs)
+    # Each stage's cost inside the step: the step's prefixes (q|k|v; + attention; + o_proj; ...;
+    # + lm_head) are timed as graphs, and a stage costs the difference between the prefix that
+    # ends with it and the one before; the argmax, the step's last launch, is timed alone. The
+    # costs add up to the step, which `reconciliation` compares with the timed decode. The
+    # attention, for example, runs behind the q|k|v launch it reads, as in the step. Each stage
+    # replayed alone (its launches back to back, no producer in front) is reported beside it as
+    # isolated_mean_us.
+    order = ["qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"]
+    prefix_names = ["+".join(order[:i + 1]) for i in range(len(order) - 1)] + ["argmax"]
+    kernel_table, prev = {}, None
+    for name, pref in zip(order, prefix_names):
+        if pref not in stages or name not in stages:
+            break
+        durs, launches = stages[pref]
+        tot = [us * launches for us in durs]  # µs per step of the prefix, per profiled position
+        inc = [t - p for t, p in zip(tot, prev)] if prev and name != "argmax" else tot
+        prev = tot
+        per_step = stages[name][1]
+        mean_us = sum(inc) / len(inc) / per_step
+        iso = sum(stages[name][0]) / len(stages[name][0])
         b = stage_bytes.get(name, 0)
         kernel_table[name] = {"launches_per_step": per_step, "mean_us": round(mean_us, 3),
-                              "us_per_step": round(mean_us * per_step, 2), "bytes_per_launch": int(b),
+                              "us_per_step": round(mean_us * per_step, 2), "isolated_mean_us": round(iso, 3),
+                              "bytes_per_launch": int(b),
                               "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
     pf = qe.prefetch_bytes(cfg, mean_pos, el) if qe.l2_prefetch_enabled() else 0
     if "attention" in kernel_table:
@@ -642,6 +652,12 @@ def main():
             "gpu_us_per_token": round(per_token_gpu_s * 1e6, 2),
         },
         "kernels": kernel_table,
+        # the stages' in-step costs add up to the whole-step graph (timed at the profiled
+        # positions); the decode's own GPU time per token is over positions 130..257
+        "reconciliation": {
+            "stages_us_per_token": round(sum(k["us_per_step"] for k in kernel_table.values()), 2) if kernel_table else None,
+            "decode_gpu_us_per_token": round(per_token_gpu_s * 1e6, 2),
+        },
         "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
         "by_position": by_position(runs[0][1], P, 512) if DS >= 1024 else None,
         "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),

@@ -154,7 +154,11 @@ uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, ui
  *      (nullable) and the stage name (a static string) to names_out (nullable); *n_out = stages
  *      written. The stage "qkv+attention" times each layer's q|k|v and attention launches together
  *      (2 per layer), so that the attention's time behind its producer is that minus the "qkv"
- *      stage's. A cache of fewer than 9 positions skips the argmax stage (its replays advance the
+ *      stage's; the stages "qkv+attention+o_proj", ... up to
+ *      "qkv+attention+o_proj+gate_up+down+lm_head" time the step's prefixes the same way, so that
+ *      differences of consecutive prefixes (duration x launches) are the stages' costs inside the
+ *      step (the argmax, the last launch, is timed alone only: its replays advance the step
+ *      state). A cache of fewer than 9 positions skips the argmax stage (its replays advance the
  *      token ring). Afterwards the step is run once more, so the cache holds what qe_forward(token,
  *      pos) leaves; a kernel error raised by any replay is returned as QE_ERR_KERNEL. No reference
  *      counterpart: the reference timed kernels by removing them by hand (README.md:64-71). ---- */

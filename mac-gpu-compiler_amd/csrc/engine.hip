@@ -401,12 +401,13 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
   hipStream_t s = m->stream;
-  // `only` names one stage, or "qkv+attention" for each layer's q|k|v and attention launches
-  // (the attention then runs behind its producer, as in the step)
-  const bool pair = only && strcmp(only, "qkv+attention") == 0;
+  // `only` names one stage or several joined by '+', e.g. "qkv+attention" for each layer's q|k|v
+  // and attention launches (the attention then runs behind its producer, as in the step)
   auto want = [&](const char* name) {
-    const bool w = !only || strcmp(only, name) == 0 ||
-                   (pair && (strcmp(name, "qkv") == 0 || strcmp(name, "attention") == 0));
+    bool w = !only;
+    const size_t n = strlen(name);
+    for (const char* t = only; t && !w; t = strchr(t, '+') ? strchr(t, '+') + 1 : nullptr)
+      w = strncmp(t, name, n) == 0 && (t[n] == '+' || t[n] == '\0');
     if (w && launches) ++*launches;
     return w;
   };
@@ -861,8 +862,22 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   // `pos` (set_state), so its replays run at that position as the step did; the argmax replays
   // each advance the token ring by one, which a cache of fewer than kReps + 2 positions cannot
   // hold, so such a cache skips the argmax stage.
-  static const char* const kStages[] = {"qkv",  "attention", "qkv+attention", "o_proj",
-                                        "gate_up", "down",   "lm_head",       "argmax"};
+  // Each stage alone, then the step's prefixes (each adding the next stage, as the step orders
+  // them) up to the lm_head, whose differences are the stages' in-step costs. The argmax, the
+  // step's last launch, is not in a prefix: it advances the step state, which the attention
+  // launches of a replayed prefix would then follow past the captured position.
+  static const char* const kStages[] = {"qkv",
+                                        "attention",
+                                        "qkv+attention",
+                                        "o_proj",
+                                        "gate_up",
+                                        "down",
+                                        "lm_head",
+                                        "argmax",
+                                        "qkv+attention+o_proj",
+                                        "qkv+attention+o_proj+gate_up",
+                                        "qkv+attention+o_proj+gate_up+down",
+                                        "qkv+attention+o_proj+gate_up+down+lm_head"};
   constexpr int kReps = 8;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   HIP_TRY(hipEventCreate(&e0));

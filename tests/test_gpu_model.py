@@ -120,8 +120,12 @@ def test_profile_step_stages_and_next_step(gpu, tiny_ckpt):
     m.prefill(prompt[:8], 0, c, want_logits=False)
     stages = {name: (us, n) for name, us, n in m.profile_step(int(prompt[8]), 8, c)}
     L = TINY.num_hidden_layers
-    assert set(stages) == {"qkv", "attention", "qkv+attention", "o_proj", "gate_up", "down", "lm_head", "argmax"}
+    prefixes = ["qkv+attention+o_proj", "qkv+attention+o_proj+gate_up", "qkv+attention+o_proj+gate_up+down",
+                "qkv+attention+o_proj+gate_up+down+lm_head"]
+    assert set(stages) == {"qkv", "attention", "qkv+attention", "o_proj", "gate_up", "down", "lm_head", "argmax",
+                           *prefixes}
     assert stages["qkv+attention"][1] == 2 * L and stages["attention"][1] == L
+    assert [stages[p][1] for p in prefixes] == [3 * L, 4 * L, 5 * L, 5 * L + 1]
     assert all(us > 0 for us, _ in stages.values())
     oc = om.new_cache()
     for pos, tok in enumerate(prompt):
