@@ -86,9 +86,8 @@ def run_attention(q, k_pm, v_pm, n_heads, n_kv, n_splits, stride_pad=3):
 @pytest.mark.parametrize("n_splits", [0, 1, 7, 128])
 def test_attention_matches_oracle(gpu, n_pos, n_splits):
     # runs of 1..n_pos positions: one 64-position tile or many per workgroup, runs past the last
-    # position (n_splits > n_pos) write empty partials that the merge must weigh 0
-    if n_pos == 32768 and n_splits == 1:
-        pytest.skip("one workgroup per KV head over 32768 positions only repeats the 8192 case, slowly")
+    # position (n_splits > n_pos) write empty partials that the merge must weigh 0; n_splits = 1
+    # at 32768 is the single pass of config 3 (one workgroup per KV head over all positions)
     rng = np.random.default_rng(n_pos)
     n_kv, G, D = 8, 2, 128
     n_heads = n_kv * G
