@@ -1500,6 +1500,7 @@ hipError_t launch_gemm_qk_rope(const GemmParams& g, const BatchAttnParams& a, hi
   if (!rows_kernel(g.M, g.K) || g.M != a.M || g.N != (a.n_heads + 2 * a.n_kv) * kHeadDim || !g.rowscale || !g.gain ||
       !a.q || !a.q_norm || !a.k_norm || !a.rope || !a.k_cache || !a.v_cache || g.lda % 4 || !g.A || !g.W)
     return hipErrorNotSupported;
+  if (uint64_t(a.start) + a.M > a.max_seq) return hipErrorInvalidValue;  // the K/V rows must fit the cache
   const dim3 grid(g.N / 128, ceil_div(g.M, 64), 1);
   hipLaunchKernelGGL((k_gemm_rows8<true, kGemmQkRope, 128, 1>), grid, dim3(512), 0, st, g, a);
   return hipGetLastError();
