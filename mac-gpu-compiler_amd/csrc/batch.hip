@@ -4,11 +4,14 @@
 // calls forward per position); these kernels run a chunk of M tokens through a layer at once, so
 // every weight is read once per chunk and the projections become GEMMs on the matrix cores:
 //   rownorm        s[m] = 1/sqrt(mean(x_m^2) + eps)                  (cpu_inference.rs:189-194)
-//   k_gemm         C[m][n] = sum_k A'[m][k] W[n][k], A' = f32 A (x s[m] x gain[k] with a norm),
+//   GEMMs          C[m][n] = sum_k A'[m][k] W[n][k], A' = f32 A (x s[m] x gain[k] with a norm),
 //                  split into hi + lo bf16 so the products keep ~16 mantissa bits; epilogues
-//                  store / residual add / silu(gate)*up                 (cpu_inference.rs:225-257)
+//                  store / residual add / silu(gate)*up / q-k norm + RoPE + K/V append
+//                  (cpu_inference.rs:225-257): k_gemm_skinny (<= 32 rows), k_gemm_lds / k_gemm (<= 64),
+//                  k_gemm_rows8 (<= 1024), k_gemm_tile (more); k_mv_rows (<= 4 rows, f32 FMA)
 //   k_qk_rope      per token and head: q/k RMSNorm + RoPE, K/V append   (cpu_inference.rs:134-141)
 //   k_attn_causal_bf  token m attends positions 0..start+m, split bf16 MFMA (cpu_inference.rs:144-162)
+//   k_row_argmax_*    greedy token per logit row (main.rs:37-42)
 #include "batch.h"
 
 #include <algorithm>
