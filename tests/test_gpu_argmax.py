@@ -66,6 +66,17 @@ def test_row_argmax_rules(gpu, n):
     np.testing.assert_array_equal(got, want)
 
 
+def test_row_argmax_many_rows(gpu):
+    """more rows than one launch takes (65535): the op works through them in batches"""
+    rng = np.random.default_rng(9)
+    rows = rng.standard_normal((70000, 7)).astype(np.float32)
+    rows[65534:65537, :] = 1.0  # all-equal rows at the batch edge: index 0 wins
+    rows[69999, 3] = np.nan
+    got = run_argmax(rows)
+    want = np.array([oracle.argmax(r) for r in rows])
+    np.testing.assert_array_equal(got, want)
+
+
 def patch_tensor(path: str, name: str, values: np.ndarray) -> None:
     """Overwrites one bf16 tensor's bytes in a safetensors file in place."""
     with open(path, "r+b") as f:
