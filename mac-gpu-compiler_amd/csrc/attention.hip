@@ -126,7 +126,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform, so branches on it are scalar
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
-  const uint32_t g = blockIdx.x, s = blockIdx.y;
+  // rows of several tokens may be split over row_split workgroups per KV head: this one serves
+  // rows rbase .. rbase + G - 1 of the GT rows of KV head g
+  const uint32_t rsplit = !DECODE && p.row_split > 1 ? p.row_split : 1u;
+  const uint32_t g = blockIdx.x / rsplit, rbase = (blockIdx.x % rsplit) * G, GT = G * rsplit, s = blockIdx.y;
   const size_t head_base = size_t(g) * p.max_seq * D;
   // Decode sizes the runs from the current length (below); the first tile is loaded up front
   // for runs of a single tile, which is what every step up to 64 * splits positions has.
@@ -148,8 +151,10 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     const int r = min(wave + 4 * i, NR - 1);
     size_t off = r < G ? (size_t(g) * G + r) * D
                        : size_t(p.n_heads) * D + (r == G ? 0 : size_t(p.n_kv) * D) + size_t(g) * D;
-    if (!DECODE && p.tok_heads)  // rows of several tokens: token r / tok_heads, head g tok_heads + r % tok_heads
-      off = size_t(r / p.tok_heads) * p.q_tok_stride + (size_t(g) * p.tok_heads + r % p.tok_heads) * D;
+    if (!DECODE && p.tok_heads) {  // rows of several tokens: token r / tok_heads, head g tok_heads + r % tok_heads
+      const uint32_t rr = rbase + uint32_t(r);
+      off = size_t(rr / p.tok_heads) * p.q_tok_stride + (size_t(g) * p.tok_heads + rr % p.tok_heads) * D;
+    }
     ra[i] = p.qkv[off + lane];
     rb[i] = p.qkv[off + lane + 64];
   }
@@ -196,13 +201,13 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     t0 = t0_first;
   }
   const uint32_t t1 = min(n, t0 + run);
-  float* part = p.partial + (size_t(g) * p.splits + s) * G * kPartStride;
+  float* part = p.partial + ((size_t(g) * p.splits + s) * GT + rbase) * kPartStride;
   // per-row causal limit: with rows of several tokens, token i of T sees positions < n - (T - 1 - i)
   uint32_t lim[G];
 #pragma unroll
   for (int j = 0; j < G; j++) {
     lim[j] = n;
-    if (!DECODE && p.tok_heads) lim[j] = n - (uint32_t(G) / p.tok_heads - 1u - uint32_t(j) / p.tok_heads);
+    if (!DECODE && p.tok_heads) lim[j] = n - (GT / p.tok_heads - 1u - (rbase + uint32_t(j)) / p.tok_heads);
   }
 
   // ---- q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215) ----
@@ -401,12 +406,14 @@ bool attn_args_ok(const AttnParams& p, uint32_t splits, uint32_t chunk, uint32_t
 
 template <bool DECODE>
 hipError_t launch_split(const AttnParams& pin, uint32_t splits, uint32_t chunk, hipStream_t s) {
-  const uint32_t G = pin.n_heads / pin.n_kv;
   AttnParams p = pin;
   p.splits = splits;
-  // prefetch workgroups: whole rows of n_kv after the attention's `splits` rows (dispatched
+  const uint32_t rsplit = !DECODE && p.row_split > 1 ? p.row_split : 1u;
+  const uint32_t G = pin.n_heads / pin.n_kv / rsplit;  // rows per workgroup
+  // prefetch workgroups: whole rows of the grid after the attention's `splits` rows (dispatched
   // after them: ahead of them, they delay the attention more than they gain)
-  const dim3 grid(p.n_kv, splits + ceil_div(8 * p.pf_slots, p.n_kv));
+  const uint32_t gx = p.n_kv * rsplit;
+  const dim3 grid(gx, splits + ceil_div(8 * p.pf_slots, gx));
 #define QE_ATT(GG)                                                                                          \
   if (G == GG) {                                                                                            \
     if (p.kv_bf16) hipLaunchKernelGGL((k_attn_split<GG, true, DECODE>), grid, dim3(256), 0, s, p, chunk);   \
@@ -434,7 +441,7 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
   if (p.n_pos_fixed == 0 || p.n_pos_fixed > p.max_seq || splits == 0 || splits > uint32_t(kAttnMaxSplits) || !out)
     return hipErrorInvalidValue;
   const uint32_t chunk = ceil_div(p.n_pos_fixed, splits);
-  if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16) return hipErrorInvalidValue;
+  if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16 || p.row_split > 1) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out,
@@ -448,6 +455,8 @@ hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* ou
     return hipErrorInvalidValue;
   const uint32_t tokens = p.n_heads / p.n_kv / p.tok_heads;
   if (tokens > p.n_pos_fixed) return hipErrorInvalidValue;
+  if (p.row_split > 1 && ((p.n_heads / p.n_kv) % p.row_split || (p.n_heads / p.n_kv / p.row_split) % p.tok_heads))
+    return hipErrorInvalidValue;
   const uint32_t chunk = ceil_div(p.n_pos_fixed, splits);
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed)) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);

@@ -615,6 +615,10 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       r.qkv = m->bq; r.k_cache = a.k_cache; r.v_cache = a.v_cache; r.partial = m->bpart;
       r.n_kv = a.n_kv; r.n_heads = a.n_kv * rows_per_kv; r.max_seq = a.max_seq; r.scale = a.scale;
       r.kv_bf16 = a.kv_bf16; r.n_pos_fixed = start + M; r.tok_heads = a.n_heads / a.n_kv; r.q_tok_stride = QD;
+      // 8 rows (4 tokens): two workgroups of 4 rows per KV head halve each one's score and
+      // P.V work for a second read of the K/V runs, mostly from L2 (verify of 4 tokens at
+      // position 2048: 1.321 -> 1.261 ms; 4 workgroups of 2 rows: 1.399 ms; 4 rows: no change)
+      if (rows_per_kv == 8) r.row_split = 2;
       if (m->l2_prefetch && mv) {
         // as in the decode step: the attention is latency-bound, so extra workgroups load this
         // layer's gate|up (the skinny GEMM's rows at 4 tokens, else the multi-row matvec's) and

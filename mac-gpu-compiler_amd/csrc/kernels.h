@@ -90,6 +90,9 @@ struct AttnParams {
   // its output there too), and it sees positions up to n_pos_fixed - tokens + token (causal).
   // tok_heads = 0: one token (the rows are the G' heads of g)
   uint32_t tok_heads, q_tok_stride;
+  // rows of several tokens: the G' rows of a KV head are served by row_split workgroups of
+  // G' / row_split rows each (0 or 1: one workgroup), all reading the same K/V runs
+  uint32_t row_split;
   uint32_t splits;         // runs per KV head (set by the launchers)
   uint32_t run;            // decode: positions per run (a multiple of 64) chosen by the host for
                            // the step's position; 0: derived from pos on the device
