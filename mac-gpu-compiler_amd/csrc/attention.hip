@@ -347,13 +347,16 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
 // ---------------------------------------------------------------------------------------------
 // The isolated op's merge: out[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s over the split
 // partials of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. One workgroup of
-// 8 x 128 threads per q head: group j (thread = dim) takes splits j, j+8, ..., all of its loads
-// issued at once (indexes past the last split re-read it and weigh 0); the 8 groups meet in LDS.
+// 8 x 128 threads per q head: group j (thread = dim) takes splits j, j+8, ..., j + 8(U-1), all of
+// its loads issued at once (indexes past the last split re-read it and weigh 0; the launch picks
+// the least U with 8U >= splits: at 33 splits, U = 16 instead of 5 cost 1.4 us per launch); the 8
+// groups meet in LDS.
 // ---------------------------------------------------------------------------------------------
+template <int U>
 __global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
                                                              float* __restrict__ out, uint32_t tok_heads,
                                                              uint32_t q_tok_stride) {
-  constexpr int U = kAttnMaxSplits / 8, PS = kPartStride;
+  constexpr int PS = kPartStride;
   const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x & (kHeadDim - 1), grp = threadIdx.x >> 7;
   const float* base = part + (size_t(g) * splits * G + j) * PS;
   float mv[U], lv[U], av[U];
@@ -404,6 +407,24 @@ bool attn_args_ok(const AttnParams& p, uint32_t splits, uint32_t chunk, uint32_t
   return (G == 1 || G == 2 || G == 4 || G == 8) && splits > 0 && chunk > 0 && uint64_t(splits) * chunk >= n;
 }
 
+// the merge over `splits` partials per q head (splits <= kAttnMaxSplits)
+template <int U>
+hipError_t launch_merge_u(const AttnParams& p, uint32_t splits, float* out, uint32_t tok_heads, uint32_t q_tok_stride,
+                          hipStream_t s) {
+  if constexpr (U < kAttnMaxSplits / 8) {
+    if (splits > 8u * U) return launch_merge_u<U + 1>(p, splits, out, tok_heads, q_tok_stride, s);
+  }
+  hipLaunchKernelGGL(k_attn_merge<U>, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits,
+                     p.n_heads / p.n_kv, out, tok_heads, q_tok_stride);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge(const AttnParams& p, uint32_t splits, float* out, uint32_t tok_heads, uint32_t q_tok_stride,
+                        hipStream_t s) {
+  static_assert(kAttnMaxSplits % 8 == 0, "8 groups of splits per q head");
+  return launch_merge_u<1>(p, splits, out, tok_heads, q_tok_stride, s);
+}
+
 template <bool DECODE>
 hipError_t launch_split(const AttnParams& pin, uint32_t splits, uint32_t chunk, hipStream_t s) {
   AttnParams p = pin;
@@ -444,9 +465,7 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed) || p.kv_bf16 || p.row_split > 1) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out,
-                     0u, 0u);
-  return hipGetLastError();
+  return launch_merge(p, splits, out, 0u, 0u, s);
 }
 
 hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
@@ -461,9 +480,7 @@ hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* ou
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed)) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(k_attn_merge, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits, p.n_heads / p.n_kv, out,
-                     p.tok_heads, p.q_tok_stride);
-  return hipGetLastError();
+  return launch_merge(p, splits, out, p.tok_heads, p.q_tok_stride, s);
 }
 
 }  // namespace qe
