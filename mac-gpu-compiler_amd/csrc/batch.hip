@@ -863,6 +863,9 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
   const uint32_t last = p.start + min(mb + TOK - 1, p.M - 1);  // positions 0..last are needed
   const uint32_t k_begin = run * p.key_run;
   const uint32_t k_end = min(last + 1, k_begin + p.key_run);  // this run: positions [k_begin, k_end)
+  // scores in base-2 units: softmax weights are 2^(s log2(e) scale - m), m and the partials' m
+  // in the same units
+  const float sl2 = p.scale * 1.44269504088896341f;
 
   bf16x8 qh[RB][4], ql[RB][4];
 #pragma unroll
@@ -983,7 +986,7 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const uint32_t t = t0 + uint32_t(16 * j + 4 * kg + r);
-          const float v = t <= my_pos[b] && t < k_end ? s[b][j][r] * p.scale : -INFINITY;
+          const float v = t <= my_pos[b] && t < k_end ? s[b][j][r] * sl2 : -INFINITY;
           s[b][j][r] = v;
           mx = fmaxf(mx, v);
         }
@@ -991,13 +994,16 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run[b], mx);  // -inf while no key of the run is visible to this row
-      const float corr = m_run[b] == -INFINITY ? 0.f : expf(m_run[b] - m_new);
+      // 2^(-inf) = 0 on the hardware exp2: masked keys and a first visible tile weigh 0 with no
+      // test per key; m_use keeps -inf - -inf out while nothing is visible
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float corr = __builtin_amdgcn_exp2f(m_run[b] - m_use);
       float sum = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; j++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-          const float e = s[b][j][r] == -INFINITY ? 0.f : expf(s[b][j][r] - m_new);
+          const float e = __builtin_amdgcn_exp2f(s[b][j][r] - m_use);
           s[b][j][r] = e;
           sum += e;
         }
@@ -1057,7 +1063,7 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
 }
 
 // att[v] = sum_s e_s acc_s / sum_s e_s l_s over the runs of query vector v = (token, head),
-// e_s = exp(m_s - max m); runs without a visible key (m = -inf) weigh 0. Two query vectors per
+// e_s = 2^(m_s - max m) (m in base-2 units); runs without a visible key (m = -inf) weigh 0. Two query vectors per
 // workgroup of 256 threads (one per dim); all U >= runs run loads are issued at once.
 template <int U>
 __global__ __launch_bounds__(256) void k_attn_merge_rows(const float* __restrict__ part, uint32_t runs,
@@ -1079,8 +1085,8 @@ __global__ __launch_bounds__(256) void k_attn_merge_rows(const float* __restrict
   for (int u = 0; u < U; u++) M = uint32_t(u) < runs ? fmaxf(M, mv[u]) : M;
   float L = 0.f, A = 0.f;
 #pragma unroll
-  for (int u = 0; u < U; u++) {
-    const float e = (uint32_t(u) < runs && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
+  for (int u = 0; u < U; u++) {  // m in base-2 units (k_attn_causal_bf)
+    const float e = (uint32_t(u) < runs && mv[u] != -INFINITY) ? exp2f(mv[u] - M) : 0.f;
     L += e * lv[u];
     A += e * av[u];
   }
