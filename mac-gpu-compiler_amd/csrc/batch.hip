@@ -1196,8 +1196,27 @@ constexpr int kTileDepth = 2;
 bool rows_kernel(uint32_t M, uint32_t K) { return M > kGemmTileMinM && M <= kGemmRowsMaxM && K % 64 == 0; }
 
 // k_gemm_rows8 over `splits` K splits (K % (64 splits) == 0, checked by the callers)
+// Column tile of k_gemm_rows8 for an unsplit launch. The kernel is bound by what a CU pulls from
+// L2 (A 16 KB and W BN x 128 B per 64-deep step), so the tile is the one with the fewest bytes
+// on the busiest CU: rounds of 256 workgroups x bytes per step. For gate|up at 512 rows
+// (N = 6144) 192 columns give 256 workgroups at 40 KB a step against 384 at 32 KB (half the CUs
+// running two).
+uint32_t rows_bn(uint32_t M, uint32_t N, uint32_t splits) {
+  if (splits != 1 || N % 192) return 128;
+  const uint64_t rounds128 = ceil_div(ceil_div(N, 128) * ceil_div(M, 64), 256u);
+  const uint64_t rounds192 = ceil_div(ceil_div(N, 192) * ceil_div(M, 64), 256u);
+  return rounds192 * (16 + 24) < rounds128 * (16 + 16) ? 192 : 128;
+}
+
 template <bool NRM, int E>
 void launch_rows(const GemmParams& p, uint32_t splits, hipStream_t st) {
+  if constexpr (E == kGemmStore || E == kGemmSiluPair || E == kGemmResAdd) {
+    if (rows_bn(p.M, p.N, splits) == 192) {
+      const dim3 g(ceil_div(p.N, 192), ceil_div(p.M, 64), splits);
+      hipLaunchKernelGGL((k_gemm_rows8<NRM, E, 192, 1>), g, dim3(512), 0, st, p, BatchAttnParams{});
+      return;
+    }
+  }
   const dim3 g(ceil_div(p.N, 128), ceil_div(p.M, 64), splits);
   hipLaunchKernelGGL((k_gemm_rows8<NRM, E, 128, 1>), g, dim3(512), 0, st, p, BatchAttnParams{});
 }

@@ -26,13 +26,16 @@ def bf16_round(a: np.ndarray) -> np.ndarray:
 
 # m <= 32 runs the skinny (split over k) kernel: one m-tile on 16 or 8 waves, or two m-tiles;
 # m <= 64 the LDS-tiled 64 x 64 kernel (k % 64 == 0) or the register-only one (k = 96); larger m
-# the 128-row tile kernel with 64 columns per tile, or 128 once that gives 256 tiles (2048 x 6144);
+# the 64-row kernel up to 1024 rows (192-column tiles where that fills the CUs more evenly: 512 x
+# 6144, 1000 x 6144), then the 128-row tile kernel with 64 columns per tile, or 128 once that gives
+# 256 tiles (2048 x 6144);
 # odd stage counts (k = 32, 96), ragged rows and columns (n = 1000) included
 @pytest.mark.parametrize("m,n,k", [(1, 64, 32), (5, 128, 64), (64, 1024, 1024), (100, 4096, 1024),
                                    (512, 1024, 3072), (37, 6144, 1024), (4, 32768, 1024), (3, 1000, 256),
                                    (16, 2048, 1024), (8, 4096, 3072), (17, 6144, 1024), (32, 1024, 3072),
                                    (2, 4096, 160), (40, 512, 96), (65, 64, 32), (128, 128, 32),
-                                   (200, 4096, 1024), (300, 1000, 96), (513, 6144, 1024), (2048, 6144, 1024)])
+                                   (200, 4096, 1024), (300, 1000, 96), (513, 6144, 1024), (2048, 6144, 1024),
+                                   (512, 6144, 1024), (1000, 6144, 64)])
 def test_gemm_matches_float64(gpu, m, n, k):
     import torch
     rng = np.random.default_rng(m * 7 + n + k)
