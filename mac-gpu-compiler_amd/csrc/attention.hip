@@ -453,9 +453,15 @@ hipError_t launch_split(const AttnParams& pin, uint32_t splits, uint32_t chunk, 
 
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, hipStream_t s) {
   if (!attn_args_ok(p, splits, ceil_div(p.max_seq, max(splits, 1u)), p.max_seq) ||
-      splits > uint32_t(kAttnMaxMergeSplits) || !p.state || !p.rope_cur || !p.q_norm || !p.k_norm || !p.err)
+      splits > uint32_t(kAttnMaxWideSplits) || !p.state || !p.rope_cur || !p.q_norm || !p.k_norm || !p.err)
     return hipErrorInvalidValue;
   return launch_split<true>(p, splits, 0, s);
+}
+
+hipError_t launch_attention_merge(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
+  if (!p.n_kv || p.n_heads % p.n_kv || !p.partial || !out || splits == 0 || splits > uint32_t(kAttnMaxSplits))
+    return hipErrorInvalidValue;
+  return launch_merge(p, splits, out, 0u, 0u, s);
 }
 
 hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {

@@ -157,6 +157,10 @@ struct qe_kv {
   uint32_t* host_tokens = nullptr;  // pinned, written by the argmax kernel
   uint32_t tok_cap = 0;
   uint32_t attn_splits = 1;     // the most attention runs per KV head a step uses
+  // past 64 kAttnMaxMergeSplits positions, up to kAttnMaxWideSplits runs per KV head, merged by a
+  // launch of their own before a plain o_proj (QE_WIDE_ATTN=0: kAttnMaxMergeSplits runs of more
+  // tiles, merged in the o_proj prologue)
+  bool wide_attn = true;
   // the attention shape enqueue_step records: runs per KV head and positions per run
   uint32_t step_splits = 1, step_run = 64;
   bool eager = false;           // launch the step kernel by kernel instead of replaying a graph
@@ -348,7 +352,7 @@ int qe_model_load(const char* path, qe_model** out) {
   auto stake = [&](size_t bytes) { size_t o = so; so = align_up(so + bytes, 256); return o; };
   const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
                s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
-               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxMergeSplits * G * qe::kPartStride * 4),
+               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxWideSplits * G * qe::kPartStride * 4),
                s_err = stake(4);
   HIP_TRY(hipMalloc(&m->scratch, so));
   HIP_TRY(hipMemset(m->scratch, 0, so));
@@ -448,10 +452,18 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     p.w = w.w_o; p.x = m->att; p.rows = H; p.cols = QD; p.out = m->x;
     a.run = kv->step_run;
     if (want("attention")) HIP_TRY(qe::launch_attention_split(a, kv->step_splits, s));
-    // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164)
-    p.attn_part = m->attn_part; p.attn_splits = kv->step_splits;
-    p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
-    if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
+    // merge the attention partials, then o_proj + residual (cpu_inference.rs:163-164): in the
+    // o_proj prologue, or for more runs than it takes, in a launch of its own
+    if (kv->step_splits > uint32_t(qe::kAttnMaxMergeSplits)) {
+      if (want("o_proj")) {
+        HIP_TRY(qe::launch_attention_merge(a, kv->step_splits, m->att, s));
+        HIP_TRY(qe::launch_matvec_wide(p, qe::kCopy, qe::kResAdd, s));
+      }
+    } else {
+      p.attn_part = m->attn_part; p.attn_splits = kv->step_splits;
+      p.attn_group = uint32_t(c.num_attention_heads / c.num_key_value_heads);
+      if (want("o_proj")) HIP_TRY(qe::launch_matvec_wide(p, qe::kAttnMerge, qe::kResAdd, s));
+    }
     // post_attention_layernorm + gate/up + silu*up (cpu_inference.rs:167-170)
     p = MatvecParams{};
     p.eps = c.rms_norm_eps;
@@ -674,6 +686,18 @@ int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
 // attention kernel starts its first K/V tile load at launch instead of after reading pos.
 void step_shape(const qe_kv* kv, uint64_t pos, uint32_t& splits, uint32_t& run) {
   const uint64_t n = pos + 1, S = kv->attn_splits;
+  if (kv->wide_attn && n > 64 * uint64_t(qe::kAttnMaxMergeSplits)) {
+    // long context: runs of whole tiles over up to kAttnMaxWideSplits workgroups per KV head,
+    // their count rounded up to a multiple of 8 (fewer step graphs; the extra runs are empty).
+    // Against 16 runs of 128..256 positions merged in o_proj, at 4096 steps from a 130-token
+    // prompt: 1288 vs 1218 tok/s (f32 cache; 1158 vs 1054 over the last 512 steps), 1339 vs
+    // 1306 (bf16 cache).
+    const uint64_t W = qe::kAttnMaxWideSplits;
+    run = uint32_t(64 * ((n + 64 * W - 1) / (64 * W)));
+    const uint64_t active = (n + run - 1) / run;
+    splits = uint32_t(std::min<uint64_t>(W, 8 * ((active + 7) / 8)));
+    return;
+  }
   run = uint32_t(64 * ((n + 64 * S - 1) / (64 * S)));
   const uint64_t active = (n + run - 1) / run;
   splits = uint32_t(run == 64 ? (active <= 4 ? std::min<uint64_t>(4, S) : active <= 8 ? std::min<uint64_t>(8, S) : S) : S);
@@ -795,6 +819,7 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
   // at most kAttnMaxMergeSplits (the o_proj prologue merges that many partials per q head);
   // step_shape picks each step's runs within this
   kv->attn_splits = uint32_t(std::min<uint64_t>((max_seq + 63) / 64, qe::kAttnMaxMergeSplits));
+  if (const char* e = getenv("QE_WIDE_ATTN")) kv->wide_attn = strcmp(e, "0") != 0;
 
   // QE_LAUNCH=eager launches each step kernel by kernel (for tools that do not follow graph
   // replays, such as counter collection); otherwise one decode step is captured and replayed
@@ -813,9 +838,11 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
     uint32_t splits, run;
     step_shape(kv.get(), pos, splits, run);
     if (shapes.empty() || shapes.back() != std::make_pair(splits, run)) shapes.push_back({splits, run});
-    // the next position whose shape can differ: the end of this run length's range, or for runs
-    // of 64 the next multiple of 64
-    pos = run == 64 ? (pos / 64 + 1) * 64 : uint64_t(run) * kv->attn_splits;
+    // the next position whose shape can differ: the end of this run length's range (runs merged
+    // in o_proj), else the next multiple of 64 (wide runs change their count every 8 runs and
+    // their length every 64 kAttnMaxWideSplits positions)
+    const bool wide = splits > uint32_t(qe::kAttnMaxMergeSplits);
+    pos = run == 64 || wide ? (pos / 64 + 1) * 64 : uint64_t(run) * kv->attn_splits;
   }
   if (shapes.size() <= 64) {
     for (const auto& sh : shapes) {

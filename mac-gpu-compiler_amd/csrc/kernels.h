@@ -111,11 +111,16 @@ hipError_t launch_matvec_wide(const MatvecParams& p, int prologue, int epilogue,
 // Decode-step attention: grid (n_kv, splits); at each step the n = pos + 1 cached positions are
 // cut into `splits` runs of a whole number of 64-position tiles, each workgroup writes its (m, l,
 // acc) partials (runs past pos write empty ones), and the o_proj matvec merges them in its
-// prologue (kAttnMerge).
+// prologue (kAttnMerge, up to kAttnMaxMergeSplits runs). Long contexts use up to
+// kAttnMaxWideSplits runs, merged by launch_attention_merge before a plain o_proj.
 constexpr int kAttnMaxMergeSplits = 16;
+constexpr int kAttnMaxWideSplits = 64;
 // one split partial per q head: m, l, 2 pad floats, acc[128] (16-byte aligned rows)
 constexpr int kPartStride = 4 + kHeadDim;
 hipError_t launch_attention_split(const AttnParams& p, uint32_t splits, hipStream_t s);
+// out [n_heads][128] = the merge of the `splits` partials per q head that launch_attention_split
+// wrote to p.partial (splits <= kAttnMaxSplits)
+hipError_t launch_attention_merge(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);
 // The L2 prefetch of a matrix that launch_matvec_wide(rows x cols, prologue, epilogue) will read.
 L2Prefetch l2_prefetch_target(const uint16_t* w, uint32_t rows, uint32_t cols, int prologue, int epilogue);
 // Prefetch workgroups per XCD for these targets (each loads at most 16 chunks per thread).

@@ -155,6 +155,33 @@ def test_switches_change_no_result(gpu, tiny_ckpt, env, monkeypatch):
     np.testing.assert_array_equal(logits1, logits0)
 
 
+# Past 1024 positions a decode step splits each KV head's positions over up to 64 runs and
+# merges them in a launch of its own; QE_WIDE_ATTN=0 keeps 16 longer runs merged in the o_proj
+# prologue. Creating the cache enumerates every step shape up to max_seq (a loop that must end);
+# the two paths agree to the rounding of their merge order.
+@pytest.mark.parametrize("max_seq", [1100, 4227, 9000, 33000])
+def test_wide_attention_matches_prologue_merge(gpu, tiny_ckpt, max_seq, monkeypatch):
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(41, max_seq - 4, TINY.vocab_size)
+
+    def run():
+        c = qe.KVCache(m, max_seq)  # QE_WIDE_ATTN is read here
+        first = oracle.argmax(m.prefill_batch(prompt, 0, c, chunk=2048))
+        return m.decode(first, len(prompt), 3, c, want_logits=True)
+
+    toks1, lg1 = run()
+    monkeypatch.setenv("QE_WIDE_ATTN", "0")
+    toks0, lg0 = run()
+    d = float(np.max(np.abs(lg1 - lg0)))
+    assert d < 1e-4, f"wide and prologue-merged attention differ by {d}"
+    for i in range(3):
+        top2 = np.sort(lg0[i])[-2:]
+        if top2[1] - top2[0] > 1e-3:
+            assert toks1[i] == toks0[i]
+        else:
+            break  # a near-tie: the two greedy continuations may part here
+
+
 def test_empty_inputs_do_nothing(gpu, tiny_ckpt):
     """an empty prompt and a zero-step decode leave the cache as it was; a one-position cache
     holds exactly one forward"""
