@@ -345,19 +345,20 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
 
 
 // ---------------------------------------------------------------------------------------------
-// The isolated op's merge: out[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s over the split
-// partials of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. One workgroup of
-// 8 x 128 threads per q head: group j (thread = dim) takes splits j, j+8, ..., j + 8(U-1), all of
-// its loads issued at once (indexes past the last split re-read it and weigh 0; the launch picks
-// the least U with 8U >= splits: at 33 splits, U = 16 instead of 5 cost 1.4 us per launch); the 8
-// groups meet in LDS.
+// The merge of the split partials: out[h*128 + d] = sum_s e_s acc_s[d] / sum_s e_s l_s over the
+// runs of q head h, e_s = exp(m_s - max m); empty runs (m = -inf) weigh 0. Workgroup (h, dim
+// slice y) of 8 x DW threads: group j (thread = dim y DW + t) takes runs j, j+8, ..., j + 8(U-1),
+// all of its loads issued at once (indexes past the last run re-read it and weigh 0; the launch
+// picks the least U with 8U >= splits: at 33 runs, U = 16 instead of 5 cost 1.4 us per launch);
+// the 8 groups meet in LDS.
 // ---------------------------------------------------------------------------------------------
-template <int U>
-__global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
-                                                             float* __restrict__ out, uint32_t tok_heads,
-                                                             uint32_t q_tok_stride) {
+template <int U, int DW>
+__global__ __launch_bounds__(8 * DW) void k_attn_merge(const float* __restrict__ part, uint32_t splits, uint32_t G,
+                                                      float* __restrict__ out, uint32_t tok_heads,
+                                                      uint32_t q_tok_stride) {
   constexpr int PS = kPartStride;
-  const uint32_t h = blockIdx.x, g = h / G, j = h % G, d = threadIdx.x & (kHeadDim - 1), grp = threadIdx.x >> 7;
+  const uint32_t h = blockIdx.x, g = h / G, j = h % G, t = threadIdx.x % DW, grp = threadIdx.x / DW;
+  const uint32_t d = blockIdx.y * DW + t;
   const float* base = part + (size_t(g) * splits * G + j) * PS;
   float mv[U], lv[U], av[U];
 #pragma unroll
@@ -378,9 +379,9 @@ __global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __rest
     L += e * lv[u];
     A += e * av[u];
   }
-  __shared__ float gm[8], gl[8], ga[8][kHeadDim];
-  if (d == 0) { gm[grp] = M; gl[grp] = L; }
-  ga[grp][d] = A;
+  __shared__ float gm[8], gl[8], ga[8][DW];
+  if (t == 0) { gm[grp] = M; gl[grp] = L; }
+  ga[grp][t] = A;
   __syncthreads();
   if (grp != 0) return;
   float MM = -INFINITY;
@@ -391,7 +392,7 @@ __global__ __launch_bounds__(8 * kHeadDim) void k_attn_merge(const float* __rest
   for (int k = 0; k < 8; k++) {
     const float e = gm[k] == -INFINITY ? 0.f : expf(gm[k] - MM);  // a group with no run adds 0
     LL += e * gl[k];
-    AA += e * ga[k][d];
+    AA += e * ga[k][t];
   }
   // rows of several tokens: row j of KV head g is token j / tok_heads, head g tok_heads + j % tok_heads
   const size_t o = tok_heads ? size_t(j / tok_heads) * q_tok_stride + (size_t(g) * tok_heads + j % tok_heads) * kHeadDim
@@ -407,14 +408,19 @@ bool attn_args_ok(const AttnParams& p, uint32_t splits, uint32_t chunk, uint32_t
   return (G == 1 || G == 2 || G == 4 || G == 8) && splits > 0 && chunk > 0 && uint64_t(splits) * chunk >= n;
 }
 
-// the merge over `splits` partials per q head (splits <= kAttnMaxSplits)
+// the merge over `splits` partials per q head (splits <= kAttnMaxSplits), in slices of
+// kMergeDims dims per workgroup: 8 workgroups per q head instead of 1 took a 4096-step decode
+// (64 runs per KV head past 1024 positions) from 1290 to 1314 tok/s and the k = 4 verify at 2048
+// positions from 1.202 to 1.188 ms; slices of 32 dims: 1310 tok/s
+constexpr int kMergeDims = 16;
 template <int U>
 hipError_t launch_merge_u(const AttnParams& p, uint32_t splits, float* out, uint32_t tok_heads, uint32_t q_tok_stride,
                           hipStream_t s) {
   if constexpr (U < kAttnMaxSplits / 8) {
     if (splits > 8u * U) return launch_merge_u<U + 1>(p, splits, out, tok_heads, q_tok_stride, s);
   }
-  hipLaunchKernelGGL(k_attn_merge<U>, dim3(p.n_heads), dim3(8 * kHeadDim), 0, s, p.partial, splits,
+  constexpr int DW = kMergeDims;
+  hipLaunchKernelGGL((k_attn_merge<U, DW>), dim3(p.n_heads, kHeadDim / DW), dim3(8 * DW), 0, s, p.partial, splits,
                      p.n_heads / p.n_kv, out, tok_heads, q_tok_stride);
   return hipGetLastError();
 }
