@@ -481,7 +481,7 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
 }
 
 hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* out, hipStream_t s) {
-  if (p.n_pos_fixed == 0 || p.n_pos_fixed > p.max_seq || splits == 0 || splits > uint32_t(kAttnMaxSplits) || !out ||
+  if (p.n_pos_fixed == 0 || p.n_pos_fixed > p.max_seq || splits == 0 || splits > uint32_t(kAttnMaxSplits) ||
       !p.n_kv || !p.tok_heads || (p.n_heads / p.n_kv) % p.tok_heads || !p.q_tok_stride)
     return hipErrorInvalidValue;
   const uint32_t tokens = p.n_heads / p.n_kv / p.tok_heads;
@@ -491,7 +491,7 @@ hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* ou
   const uint32_t chunk = ceil_div(p.n_pos_fixed, splits);
   if (!attn_args_ok(p, splits, chunk, p.n_pos_fixed)) return hipErrorInvalidValue;
   hipError_t e = launch_split<false>(p, splits, chunk, s);
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !out) return e;
   return launch_merge(p, splits, out, p.tok_heads, p.q_tok_stride, s);
 }
 

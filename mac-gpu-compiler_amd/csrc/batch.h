@@ -53,6 +53,11 @@ struct MvRowsParams {
   float* out;            // [M][ldo]
   uint32_t M, rows, cols, ldo;
   float eps;
+  // launch_mv_rows_merge only: x is the attention output merged from the split kernel's
+  // partials [n_kv][attn_splits][rows per KV head][kPartStride] (launch_attention_rows layout:
+  // row j of KV head g is token j / tok_heads, q head g tok_heads + j % tok_heads)
+  const float* attn_part = nullptr;
+  uint32_t attn_splits = 0, tok_heads = 0;
 };
 
 struct BatchAttnParams {
@@ -90,6 +95,14 @@ hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, 
 // x' = x, or RMSNorm(x_m) * gain with `norm`. f32 FMA on bf16 weights, as the decode matvec.
 // cols % 8 == 0, cols <= 4096, 1 <= M <= kMvRowsMaxM; out must not alias x.
 hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st);
+// o_proj + residual of a short pass with the attention merge in its prologue (as the decode step
+// does): x[m][h*128 + d] = sum_s e_s acc_s / sum_s e_s l_s over the attn_splits partials of
+// token m, q head h (every workgroup merges its chunks of every row). hipErrorNotSupported
+// unless mv_rows_merge_fits(M, splits) and cols is whole heads of 128 with cols / 8 <= 256.
+hipError_t launch_mv_rows_merge(const MvRowsParams& p, hipStream_t st);
+// the merge slots a thread loads per token row (4, 8 or 16 for up to 4, 8, 16 runs) times the
+// token rows stay within 16
+bool mv_rows_merge_fits(uint32_t M, uint32_t splits);
 hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
 // The q|k|v GEMM of a chunk (A = x with the input RMSNorm, W = [q | k | v] rows, N = (n_heads +
 // 2 n_kv) 128) with k_qk_rope's work in its epilogue: q rows normalized and rotated to a.q, k and

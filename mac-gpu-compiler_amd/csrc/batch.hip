@@ -1254,7 +1254,7 @@ void launch_tile(const GemmParams& p, uint32_t splits, hipStream_t st) {
 // costs every wave its own products and lane reductions, so past a few rows the matrix cores
 // (k_gemm_skinny) are faster.
 // ---------------------------------------------------------------------------------------------
-template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI>
+template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI, int SM = 0>
 __global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
   constexpr int NG = 256 / TPR, WPG = TPR / 64, NS = NV * (RR + 1);
   __shared__ float red[4][NS];
@@ -1266,6 +1266,27 @@ __global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
 #pragma unroll
   for (int k = 0; k < CPT; k++) cc[k] = min(uint32_t(t) + uint32_t(TPR) * k, nch - 1);
 
+  // SM > 0: x is merged from the attention's partials (SM slots per chunk, the split kernel's
+  // layout), loaded before the weights as the decode step's o_proj does
+  float2 ml[SM > 0 ? NV : 1][CPT][SM > 0 ? SM : 1];
+  float4 a0[SM > 0 ? NV : 1][CPT][SM > 0 ? SM : 1], a1[SM > 0 ? NV : 1][CPT][SM > 0 ? SM : 1];
+  if constexpr (SM > 0) {
+    const uint32_t S = p.attn_splits, th = p.tok_heads, GT = uint32_t(NV) * th;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+#pragma unroll
+      for (int k = 0; k < CPT; k++) {
+        const uint32_t h = cc[k] >> 4, d0 = (cc[k] & 15) * 8, g = h / th, j = uint32_t(v) * th + h % th;
+#pragma unroll
+        for (int s = 0; s < SM; s++) {
+          const float* q = p.attn_part + ((size_t(g) * S + min(uint32_t(s), S - 1)) * GT + j) * kPartStride;
+          ml[v][k][s] = *reinterpret_cast<const float2*>(q);
+          a0[v][k][s] = *reinterpret_cast<const float4*>(q + 4 + d0);
+          a1[v][k][s] = *reinterpret_cast<const float4*>(q + 8 + d0);
+        }
+      }
+    }
+  }
   const uint4* W = reinterpret_cast<const uint4*>(p.w);
   uint4 wv[RR][CPT];
 #pragma unroll
@@ -1276,12 +1297,14 @@ __global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
   }
   const float4* X = reinterpret_cast<const float4*>(p.x);
   float4 xa[NV][CPT], xb[NV][CPT];
+  if constexpr (SM == 0) {
 #pragma unroll
-  for (int v = 0; v < NV; v++) {
+    for (int v = 0; v < NV; v++) {
 #pragma unroll
-    for (int k = 0; k < CPT; k++) {
-      xa[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k]];
-      xb[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k] + 1];
+      for (int k = 0; k < CPT; k++) {
+        xa[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k]];
+        xb[v][k] = X[size_t(v) * (p.cols >> 2) + 2 * cc[k] + 1];
+      }
     }
   }
   uint4 gains[CPT];
@@ -1297,6 +1320,32 @@ __global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
       for (int r = 0; r < RR; r++) res[v][r] = p.out[size_t(v) * p.ldo + min(row0 + uint32_t(r), p.rows - 1)];
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (SM > 0) {
+    // x = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m) (cpu_inference.rs:153-160 over
+    // the runs); empty runs (m = -inf) and slots past the last run weigh 0
+    const uint32_t S = p.attn_splits;
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+#pragma unroll
+      for (int k = 0; k < CPT; k++) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int s = 0; s < SM; s++) M = uint32_t(s) < S ? fmaxf(M, ml[v][k][s].x) : M;
+        float L = 0.f;
+        float4 A0 = make_float4(0.f, 0.f, 0.f, 0.f), A1 = A0;
+#pragma unroll
+        for (int s = 0; s < SM; s++) {
+          const float e = (uint32_t(s) < S && ml[v][k][s].x != -INFINITY) ? expf(ml[v][k][s].x - M) : 0.f;
+          L += e * ml[v][k][s].y;
+          A0.x += e * a0[v][k][s].x; A0.y += e * a0[v][k][s].y; A0.z += e * a0[v][k][s].z; A0.w += e * a0[v][k][s].w;
+          A1.x += e * a1[v][k][s].x; A1.y += e * a1[v][k][s].y; A1.z += e * a1[v][k][s].z; A1.w += e * a1[v][k][s].w;
+        }
+        const float inv = 1.0f / L;
+        xa[v][k] = make_float4(A0.x * inv, A0.y * inv, A0.z * inv, A0.w * inv);
+        xb[v][k] = make_float4(A1.x * inv, A1.y * inv, A1.z * inv, A1.w * inv);
+      }
+    }
+  }
 
   if (uint32_t(TPR) * CPT > nch) {  // chunks past the row end contribute 0
 #pragma unroll
@@ -1419,7 +1468,53 @@ hipError_t launch_mv_rows_nv(const MvRowsParams& p, bool norm, int epi, hipStrea
   return hipErrorInvalidValue;
 }
 
+// o_proj with the attention merge: four rows per workgroup amortize the merge, which every
+// workgroup repeats for all heads of its token rows
+template <int NV, int SM>
+hipError_t launch_mv_merge_t(const MvRowsParams& p, hipStream_t st) {
+  const uint32_t nch = p.cols / 8;
+  if (nch <= 128) {
+    hipLaunchKernelGGL((k_mv_rows<128, 1, 4, NV, false, kGemmResAdd, SM>), dim3(ceil_div(p.rows, 8u)), dim3(256), 0,
+                       st, p);
+  } else {
+    hipLaunchKernelGGL((k_mv_rows<256, 1, 4, NV, false, kGemmResAdd, SM>), dim3(ceil_div(p.rows, 4u)), dim3(256), 0,
+                       st, p);
+  }
+  return hipGetLastError();
+}
+
+uint32_t mv_merge_slots(uint32_t splits) { return splits <= 4 ? 4 : splits <= 8 ? 8 : 16; }
+
+template <int NV>
+hipError_t launch_mv_merge_nv(const MvRowsParams& p, hipStream_t st) {
+  const uint32_t sm = mv_merge_slots(p.attn_splits);
+  if (sm == 4) return launch_mv_merge_t<NV, 4>(p, st);
+  if constexpr (NV <= 2) {
+    if (sm == 8) return launch_mv_merge_t<NV, 8>(p, st);
+  }
+  if constexpr (NV == 1) return launch_mv_merge_t<NV, 16>(p, st);
+  return hipErrorNotSupported;
+}
+
 }  // namespace
+
+bool mv_rows_merge_fits(uint32_t M, uint32_t splits) {
+  return M >= 1 && M <= kMvRowsMaxM && splits >= 1 && splits <= uint32_t(kAttnMaxMergeSplits) &&
+         M * mv_merge_slots(splits) <= 16;
+}
+
+hipError_t launch_mv_rows_merge(const MvRowsParams& p, hipStream_t st) {
+  if (!p.w || !p.out || !p.attn_part || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||
+      p.ldo < p.rows || p.attn_splits == 0 || p.tok_heads == 0)
+    return hipErrorInvalidValue;
+  if (p.cols % kHeadDim || p.cols / 8 > 256 || !mv_rows_merge_fits(p.M, p.attn_splits)) return hipErrorNotSupported;
+  switch (p.M) {
+    case 1: return launch_mv_merge_nv<1>(p, st);
+    case 2: return launch_mv_merge_nv<2>(p, st);
+    case 3: return launch_mv_merge_nv<3>(p, st);
+    default: return launch_mv_merge_nv<4>(p, st);
+  }
+}
 
 hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st) {
   if (!p.w || !p.x || !p.out || (norm && !p.gain) || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||

@@ -120,6 +120,9 @@ struct qe_model {
   // decode step's split kernel, all their q heads of a KV head sharing one read of its K/V
   // (QE_ROWS_SPLIT_ATTN=0: on the causal matrix-core kernel)
   bool rows_split_attn = true;
+  // and their o_proj merges those runs in its prologue when they are few (QE_MV_MERGE=0: a
+  // merge launch of its own)
+  bool mv_merge = true;
   // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
@@ -230,6 +233,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* pf = getenv("QE_L2_PREFETCH")) m->l2_prefetch = strcmp(pf, "0") != 0;
   if (const char* mr = getenv("QE_MV_ROWS")) m->mv_rows = strcmp(mr, "0") != 0;
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
+  if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
   const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
@@ -620,6 +624,7 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       HIP_TRY(qe::launch_qk_rope(a, s));
     }
     const uint32_t rows_per_kv = (a.n_heads / a.n_kv) * M;
+    uint32_t merge_splits = 0;  // > 0: o_proj merges this many attention runs in its prologue
     if (m->rows_split_attn && (rows_per_kv == 1 || rows_per_kv == 2 || rows_per_kv == 4 || rows_per_kv == 8)) {
       // few tokens: the split kernel, the q heads of all M tokens of a KV head over one read of
       // its K/V, each token causal (positions up to its own), runs of 64 positions
@@ -641,13 +646,22 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
         r.pf_slots = qe::l2_prefetch_slots(r.pf, qe::kMaxPrefetch);
       }
       const uint32_t splits = std::min<uint32_t>(qe::kAttnMaxSplits, (start + M + 63) / 64);
-      HIP_TRY(qe::launch_attention_rows(r, splits, m->batt, s));
+      // with few runs the multi-row o_proj merges them in its prologue, as the decode step's does
+      if (mv && m->mv_merge && qe::mv_rows_merge_fits(M, splits) && QD % D == 0 && QD / 8 <= 256)
+        merge_splits = splits;
+      HIP_TRY(qe::launch_attention_rows(r, splits, merge_splits ? nullptr : m->batt, s));
     } else {
       a.part = m->bpart;
       HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
     }
     // o_proj + residual (cpu_inference.rs:163-164)
-    if ((rc = gemm_resadd(m->batt, QD, w.w_o, QD))) return rc;
+    if (merge_splits) {
+      qe::MvRowsParams r{w.w_o, nullptr, nullptr, m->bx, M, H, QD, H, eps};
+      r.attn_part = m->bpart; r.attn_splits = merge_splits; r.tok_heads = a.n_heads / a.n_kv;
+      HIP_TRY(qe::launch_mv_rows_merge(r, s));
+    } else if ((rc = gemm_resadd(m->batt, QD, w.w_o, QD))) {
+      return rc;
+    }
     // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)
     if ((rc = gemm(m->bx, H, w.w_post, w.w_gu, 2 * I, H, m->bh, I, qe::kGemmSiluPair))) return rc;
     if ((rc = gemm_resadd(m->bh, I, w.w_down, I))) return rc;

@@ -133,6 +133,7 @@ hipError_t launch_attention_op(const AttnParams& p, uint32_t splits, float* out,
 // the same kernels: q [T][heads][128] final (normalized, rotated), out [T][heads][128]. The T
 // tokens' q heads of a KV head share one read of its K/V: p.n_heads = n_kv * T * tok_heads must
 // give 1, 2, 4 or 8 rows per KV head. partial: n_kv * splits * (rows per KV head) * kPartStride floats.
+// out = nullptr: the partials only (a consumer merges them, launch_mv_rows_merge).
 hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* out, hipStream_t s);
 // Greedy token from the lm_head candidates; advances the step state and, with `rope`, copies the
 // RoPE row of the next position ([half] (cos, sin) pairs) to rope_cur for the next step.
