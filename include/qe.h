@@ -148,7 +148,8 @@ uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, ui
 
 /* ---- per-stage kernel timing: runs `token` at `pos` like qe_forward, then times each stage
  *      of the step (qkv, attention, o_proj, gate_up, down, lm_head, argmax) as a graph of that
- *      stage's launches only (28 per-layer launches, or one), replayed 8 times between two HIP
+ *      stage's launches only (28 per-layer launches, or one; past 1024 positions o_proj is 56:
+ *      the attention merge and o_proj), replayed 8 times between two HIP
  *      events, each stage from the step state of `pos`. Writes, per stage, the mean duration of
  *      one launch in microseconds to us_out, the launches per decode step to launches_out
  *      (nullable) and the stage name (a static string) to names_out (nullable); *n_out = stages

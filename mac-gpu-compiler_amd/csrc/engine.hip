@@ -460,6 +460,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
     // o_proj prologue, or for more runs than it takes, in a launch of its own
     if (kv->step_splits > uint32_t(qe::kAttnMaxMergeSplits)) {
       if (want("o_proj")) {
+        if (launches) ++*launches;  // the stage is two launches here
         HIP_TRY(qe::launch_attention_merge(a, kv->step_splits, m->att, s));
         HIP_TRY(qe::launch_matvec_wide(p, qe::kCopy, qe::kResAdd, s));
       }
