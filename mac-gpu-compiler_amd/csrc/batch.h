@@ -95,6 +95,10 @@ hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, 
 // x' = x, or RMSNorm(x_m) * gain with `norm`. f32 FMA on bf16 weights, as the decode matvec.
 // cols % 8 == 0, cols <= 4096, 1 <= M <= kMvRowsMaxM; out must not alias x.
 hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st);
+// final RMSNorm (gain) + lm_head of M <= kMvRowsMaxM token rows: out[m][row], each row's logits
+// equal to the decode step's lm_head's for that hidden state (its layout and summation order).
+// hipErrorNotSupported past 1024 columns.
+hipError_t launch_lm_head_rows(const MvRowsParams& p, hipStream_t st);
 // o_proj + residual of a short pass with the attention merge in its prologue (as the decode step
 // does): x[m][h*128 + d] = sum_s e_s acc_s / sum_s e_s l_s over the attn_splits partials of
 // token m, q head h (every workgroup merges its chunks of every row). hipErrorNotSupported

@@ -1435,6 +1435,83 @@ __global__ __launch_bounds__(256) void k_mv_rows(MvRowsParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// final RMSNorm + lm_head over the NV token rows of a short verify pass: the decode step's lm_head
+// matvec (k_matvec<R, CPL, kNorm, ..>: each wave R rows, lane l the 16-byte chunks l, l + 64, ..)
+// with the NV normalized rows staged in LDS, so the 311 MB of weights stream once for all rows.
+// Each row's norm and dot products are summed in the decode step's order, so a row's logits equal
+// that step's bit for bit. out[v][row] = logits, ldo per token row.
+// ---------------------------------------------------------------------------------------------
+template <int R, int CPL, int NV>
+__global__ __launch_bounds__(256) void k_lm_head_rows(MvRowsParams p) {
+  extern __shared__ __align__(16) float xs[];  // [NV][cols]
+  __shared__ float red[NV][4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t nch = p.cols >> 3;
+  const uint32_t row0 = (blockIdx.x * 4u + uint32_t(wave)) * R;
+  const uint4* W = reinterpret_cast<const uint4*>(p.w);
+  uint4 wv[R][CPL];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);  // past the end: re-read the last row
+    const uint4* wr = W + size_t(row) * nch;
+#pragma unroll
+    for (int k = 0; k < CPL; k++) wv[r][k] = wr[min(uint32_t(lane) + 64u * k, nch - 1)];
+  }
+  const float4* x4 = reinterpret_cast<const float4*>(p.x);
+  float4* xs4 = reinterpret_cast<float4*>(xs);
+  const uint32_t c4 = p.cols / 4;
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    float ss = 0.f;
+    for (uint32_t i = tid; i < c4; i += 256) {
+      const float4 a = x4[size_t(v) * c4 + i];
+      xs4[v * c4 + i] = a;
+      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) red[v][wave] = ss;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int v = 0; v < NV; v++) {
+    const float tot = (red[v][0] + red[v][1]) + (red[v][2] + red[v][3]);
+    const float sc = 1.0f / sqrtf(tot / float(p.cols) + p.eps);
+    for (uint32_t i = tid; i < p.cols; i += 256) xs[v * p.cols + i] = xs[v * p.cols + i] * sc * bf16f(p.gain[i]);
+  }
+  __syncthreads();
+  float acc[NV][R];
+#pragma unroll
+  for (int v = 0; v < NV; v++)
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[v][r] = 0.f;
+#pragma unroll
+  for (int k = 0; k < CPL; k++) {
+    const uint32_t c = uint32_t(lane) + 64u * k;
+    if (c < nch) {
+#pragma unroll
+      for (int v = 0; v < NV; v++) {
+        const float4 a = xs4[v * c4 + 2 * c], b = xs4[v * c4 + 2 * c + 1];
+#pragma unroll
+        for (int r = 0; r < R; r++) acc[v][r] = dot8(wv[r][k], a, b, acc[v][r]);
+      }
+    }
+  }
+#pragma unroll
+  for (int v = 0; v < NV; v++)
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[v][r] = wave_sum(acc[v][r]);
+  if (lane == 0) {
+#pragma unroll
+    for (int v = 0; v < NV; v++)
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t row = row0 + uint32_t(r);
+        if (row < p.rows) p.out[size_t(v) * p.ldo + row] = acc[v][r];
+      }
+  }
+}
+
 template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI>
 hipError_t launch_mv_rows_t(const MvRowsParams& p, hipStream_t st) {
   constexpr int rows_per_block = (256 / TPR) * RR;
@@ -1514,6 +1591,23 @@ hipError_t launch_mv_rows_merge(const MvRowsParams& p, hipStream_t st) {
     case 3: return launch_mv_merge_nv<3>(p, st);
     default: return launch_mv_merge_nv<4>(p, st);
   }
+}
+
+hipError_t launch_lm_head_rows(const MvRowsParams& p, hipStream_t st) {
+  if (!p.w || !p.x || !p.gain || !p.out || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||
+      p.cols % 8 || p.ldo < p.rows)
+    return hipErrorInvalidValue;
+  if (p.cols / 8 > 128) return hipErrorNotSupported;  // the decode lm_head's shape: 2 chunks per lane
+  constexpr int CPL = 2, R = 4;
+  const dim3 grid(ceil_div(p.rows, 4u * R));
+  const size_t lds = size_t(p.M) * p.cols * 4;
+  switch (p.M) {
+    case 1: hipLaunchKernelGGL((k_lm_head_rows<R, CPL, 1>), grid, dim3(256), lds, st, p); break;
+    case 2: hipLaunchKernelGGL((k_lm_head_rows<R, CPL, 2>), grid, dim3(256), lds, st, p); break;
+    case 3: hipLaunchKernelGGL((k_lm_head_rows<R, CPL, 3>), grid, dim3(256), lds, st, p); break;
+    default: hipLaunchKernelGGL((k_lm_head_rows<R, CPL, 4>), grid, dim3(256), lds, st, p); break;
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_mv_rows(const MvRowsParams& p, bool norm, int epi, hipStream_t st) {
