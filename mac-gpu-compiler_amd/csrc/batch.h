@@ -60,6 +60,13 @@ struct MvRowsParams {
   uint32_t attn_splits = 0, tok_heads = 0;
 };
 
+// Weights of the next GEMM that a short launch loads into the L2 of the XCDs that will read them
+// (8 x slots extra workgroups; slots = 0: none)
+struct TilePrefetch {
+  L2Prefetch pf[kMaxPrefetch];
+  uint32_t slots;
+};
+
 struct BatchAttnParams {
   const float* qkv;        // [M][n_heads + 2 n_kv][128] raw projections
   float* q;                // [M][n_heads][128] normalized + rotated q
@@ -74,6 +81,8 @@ struct BatchAttnParams {
   uint32_t key_run;        // positions per key run (set by launch_attn_causal)
   float eps, scale;
   int kv_bf16;
+  uint32_t runs;           // key runs (set by launch_attn_causal)
+  TilePrefetch pf;         // launch_attn_causal: weights its launch also loads into L2
 };
 
 hipError_t launch_rownorm(const float* x, uint32_t M, uint32_t K, float eps, float* s, hipStream_t st);
@@ -86,6 +95,13 @@ hipError_t launch_gemm(const GemmParams& p, bool norm, int epi, hipStream_t st);
 uint32_t gemm_splits(uint32_t M, uint32_t N, uint32_t K);
 // partial sums of `splits` K ranges (no norm): C[z][m][n], z < splits, ldc = N
 hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t st);
+// The prefetch target of the weights of launch_gemm / launch_gemm_qk_rope (epi) or
+// launch_gemm_split (kGemmPartial) at M rows on the 64-row kernel: column tile j, every row tile
+// and K split of which runs on XCD j % 8, reads W rows [bn j, bn (j + 1)). w = nullptr where
+// another kernel serves the shape or a column tile's workgroups do not stay on one XCD.
+L2Prefetch gemm_prefetch_target(const uint16_t* W, uint32_t M, uint32_t N, uint32_t K, int epi);
+// the slots that cover these targets (at most 64)
+uint32_t tile_prefetch_slots(const L2Prefetch* pf, int n);
 // x[m][n] += sum_z part[z][m][n] (z in order), then s[m] = 1 / sqrt(mean_n x[m][n]^2 + eps):
 // the residual add of a split GEMM fused with the next RMSNorm's row scale. N % 4 == 0.
 hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, uint32_t M, uint32_t N, float eps,
@@ -114,7 +130,8 @@ hipError_t launch_qk_rope(const BatchAttnParams& p, hipStream_t st);
 // hipErrorNotSupported where the 64-row kernel does not serve the shape (the caller then runs
 // launch_gemm and launch_qk_rope).
 hipError_t launch_gemm_qk_rope(const GemmParams& g, const BatchAttnParams& a, hipStream_t st);
-// causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att
+// causal attention of a chunk over `runs` (1..kBatchMaxRuns) key runs, merged into att; p.pf:
+// weights the launch also loads into L2 (whole planes of workgroups after the runs')
 hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream_t st);
 // key runs for a chunk of M tokens at positions start.. : at least 4, more while the chunk has
 // under 512 workgroups, and at most one per 128 keys

@@ -19,6 +19,7 @@
 #include <type_traits>
 
 #include "device_common.h"
+#include "l2_prefetch.h"
 
 namespace qe {
 namespace {
@@ -851,7 +852,12 @@ __global__ __launch_bounds__(256) void k_attn_causal_bf(BatchAttnParams p) {
   __shared__ __align__(16) uint16_t ks[NL][BK][KP];  // [hi, lo][key][dim]
   __shared__ __align__(16) uint16_t vt[NL][D][VP];   // [hi, lo][dim][key slot]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, li = lane & 15, kg = lane >> 4;
-  const uint32_t g = blockIdx.x, mb = blockIdx.y * TOK, run = blockIdx.z, runs = gridDim.z;
+  const uint32_t g = blockIdx.x, mb = blockIdx.y * TOK, run = blockIdx.z, runs = p.runs;
+  if (run >= runs) {  // a prefetch workgroup (whole workgroup, before any load)
+    l2_prefetch_tiles(p.pf.pf, (run - runs) * gridDim.x * gridDim.y + blockIdx.y * gridDim.x + g,
+                      reinterpret_cast<uint32_t*>(p.att));
+    return;
+  }
   uint32_t tok[RB], head[RB], my_pos[RB];
 #pragma unroll
   for (int b = 0; b < RB; b++) {
@@ -1729,6 +1735,23 @@ hipError_t launch_gemm_split(const GemmParams& p, uint32_t splits, hipStream_t s
   return hipGetLastError();
 }
 
+L2Prefetch gemm_prefetch_target(const uint16_t* W, uint32_t M, uint32_t N, uint32_t K, int epi) {
+  if (!W || !rows_kernel(M, K)) return L2Prefetch{};
+  const uint32_t bn = epi == kGemmQkRope || epi == kGemmPartial ? 128 : rows_bn(M, N, 1);
+  const uint32_t tiles = ceil_div(N, bn);
+  // workgroup (j, y, z) runs on XCD (j + tiles (y + gridDim.y z)) % 8: j % 8 when tiles is a
+  // multiple of 8 or the grid is one row of tiles
+  if (tiles % 8 && (ceil_div(M, 64) > 1 || epi == kGemmPartial)) return L2Prefetch{};
+  return L2Prefetch{W, N * (K / 8), bn * (K / 8), tiles};
+}
+
+uint32_t tile_prefetch_slots(const L2Prefetch* pf, int n) {
+  uint64_t tot = 0;  // XCD 0 has the most consumers
+  for (int i = 0; i < n; i++)
+    if (pf[i].w && pf[i].n_cwg) tot += uint64_t(ceil_div(pf[i].n_cwg, 8u)) * pf[i].cw_chunks;
+  return uint32_t(std::min<uint64_t>(64, (tot + 4095) / 4096));
+}
+
 hipError_t launch_resadd_partials(float* x, const float* part, uint32_t splits, uint32_t M, uint32_t N, float eps,
                                   float* s, hipStream_t st) {
   if (!M || N % 4 || !splits) return hipErrorInvalidValue;
@@ -1766,8 +1789,13 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
   const uint32_t tiles = ceil_div(p.start + p.M, 64), per_run = ceil_div(tiles, runs);
   runs = ceil_div(tiles, per_run);
   q.key_run = 64 * per_run;
+  q.runs = runs;
+  if (q.pf.slots > 64) return hipErrorInvalidValue;
   constexpr uint32_t RB = kAttnCausalRB;
-  const dim3 grid(p.n_kv, ceil_div(p.M, 64 * RB / G), runs);
+  const uint32_t gy = ceil_div(p.M, 64 * RB / G);
+  // prefetch workgroups: whole planes after the runs' (8 x slots of them at consecutive ids)
+  const uint32_t planes = q.pf.slots ? ceil_div(8 * q.pf.slots, p.n_kv * gy) : 0;
+  const dim3 grid(p.n_kv, gy, runs + planes);
   hipError_t e = hipErrorInvalidValue;
 #define QE_ATT(GG)                                                                                         \
   if (G == GG) {                                                                                           \

@@ -123,6 +123,9 @@ struct qe_model {
   // and their o_proj merges those runs in its prologue when they are few (QE_MV_MERGE=0: a
   // merge launch of its own)
   bool mv_merge = true;
+  // chunks on the 64-row GEMM: the causal attention launch also loads o_proj's weights into the
+  // L2 of the XCDs that will read them (QE_PREFILL_PREFETCH=0 turns it off)
+  bool prefill_prefetch = true;
   // ... and their lm_head is the decode step's matvec over all their rows, each row's logits
   // equal to a decode step's (QE_LM_HEAD_ROWS=0: the skinny GEMM; a 2-row pass 0.83 -> 0.80 ms)
   bool lm_head_rows = true;
@@ -238,6 +241,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
+  if (const char* pp = getenv("QE_PREFILL_PREFETCH")) m->prefill_prefetch = strcmp(pp, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
   const uint64_t D = c.head_dim, QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
@@ -657,6 +661,12 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       HIP_TRY(qe::launch_attention_rows(r, splits, merge_splits ? nullptr : m->batt, s));
     } else {
       a.part = m->bpart;
+      if (m->prefill_prefetch && !skinny) {
+        // the attention is latency-bound: extra workgroups load o_proj's weights (a split GEMM)
+        // into L2
+        a.pf.pf[0] = qe::gemm_prefetch_target(w.w_o, M, H, QD, qe::kGemmPartial);
+        a.pf.slots = qe::tile_prefetch_slots(a.pf.pf, qe::kMaxPrefetch);
+      }
       HIP_TRY(qe::launch_attn_causal(a, qe::attn_causal_runs(M, start, a.n_heads, a.n_kv), s));
     }
     // o_proj + residual (cpu_inference.rs:163-164)

@@ -203,3 +203,19 @@ def test_prefill_2048_token_by_token_matches_chunked(gpu, real_ckpt):
     logits = m.prefill(prompt, 0, cache)
     assert oracle.argmax(logits) == int(g["tokens"][0])
     check_row(g, 0, logits, 0)
+
+
+def test_prefill_prefetch_changes_no_result(gpu, real_ckpt, monkeypatch):
+    """the causal attention launch's L2 prefetch of o_proj's weights (chunks of 65..1024 tokens)
+    only loads: bit-identical last-token logits with QE_PREFILL_PREFETCH=0"""
+    g = load("qwen3_0_6b_prefill2048.npz")
+    prompt = g["prompt"].astype(np.uint32)
+
+    def run():
+        m = qe.Model.load_model(real_ckpt)  # QE_PREFILL_PREFETCH is read here
+        return m.prefill_batch(prompt, 0, qe.KVCache(m, len(prompt) + 1), chunk=512)
+
+    on = run()
+    monkeypatch.setenv("QE_PREFILL_PREFETCH", "0")
+    off = run()
+    np.testing.assert_array_equal(on, off)
