@@ -135,6 +135,20 @@ struct qe_model {
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
   float* bpart = nullptr;   // causal attention partials
   float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
+  // a chunked prefill on two streams (QE_PREFILL_STREAMS=1: one): the second stream, the
+  // second set of chunk buffers and, per set, one event per layer recorded once the chunk's K/V
+  // rows of that layer are in the cache. 2048 tokens in chunks of 512: 10.8-11.2 vs 12.5-12.8 ms.
+  // Once the process has the second stream, eager launches on the first are slightly slower (a
+  // k = 4 verify 1.22-1.23 vs 1.195-1.205 ms; 1.21 with the stream created but never used;
+  // destroying it after each prefill does not help); graph-replayed decode steps are not.
+  int prefill_streams = 2;
+  hipStream_t stream2 = nullptr;
+  uint8_t* batch_mem2 = nullptr;
+  uint32_t batch_cap2 = 0;
+  float *bx2 = nullptr, *bs2 = nullptr, *bqkv2 = nullptr, *bq2 = nullptr, *batt2 = nullptr, *bh2 = nullptr;
+  float *bpart2 = nullptr, *bsplit2 = nullptr;
+  std::vector<hipEvent_t> kv_ev[2];
+  hipEvent_t start_ev = nullptr;
   ArgCand* bcand = nullptr;  // row argmax candidates of a verify pass [kVerifyMaxTokens][kArgParts]
   float* blogits = nullptr;
   uint32_t* ids_dev = nullptr;  // the token ids of one qe_prefill_batch / qe_verify call
@@ -144,7 +158,13 @@ struct qe_model {
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
     if (scratch) (void)hipFree(scratch);
+    if (stream2) (void)hipStreamSynchronize(stream2);
     if (batch_mem) (void)hipFree(batch_mem);
+    if (batch_mem2) (void)hipFree(batch_mem2);
+    for (auto& v : kv_ev)
+      for (hipEvent_t e : v) (void)hipEventDestroy(e);
+    if (start_ev) (void)hipEventDestroy(start_ev);
+    if (stream2) (void)hipStreamDestroy(stream2);
     if (ids_dev) (void)hipFree(ids_dev);
     if (h_logits) (void)hipHostFree(h_logits);
     if (h_small) (void)hipHostFree(h_small);
@@ -241,6 +261,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
+  if (const char* ps = getenv("QE_PREFILL_STREAMS")) m->prefill_streams = strcmp(ps, "1") == 0 ? 1 : 2;
   if (const char* pp = getenv("QE_PREFILL_PREFETCH")) m->prefill_prefetch = strcmp(pp, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
@@ -541,6 +562,50 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   return QE_OK;
 }
 
+// The second stream of a chunked prefill: its chunk buffers for up to `cap` tokens (those of
+// ensure_batch without the logit rows), the stream, and the per-layer K/V events of both sets.
+int ensure_batch2(qe_model* m, uint32_t cap) {
+  const qe_config& c = m->cfg;
+  const size_t L = c.num_hidden_layers;
+  if (!m->stream2) HIP_TRY(hipStreamCreateWithFlags(&m->stream2, hipStreamNonBlocking));
+  if (!m->start_ev) HIP_TRY(hipEventCreateWithFlags(&m->start_ev, hipEventDisableTiming));
+  for (auto& v : m->kv_ev)
+    while (v.size() < L) {
+      hipEvent_t e;
+      HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+      v.push_back(e);
+    }
+  if (m->batch_mem2 && cap <= m->batch_cap2) return QE_OK;
+  cap = std::max(cap, m->batch_cap2);
+  const size_t H = c.hidden_size, I = c.intermediate_size, D = c.head_dim;
+  const size_t QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
+  size_t off = 0;
+  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
+  const size_t ox = take(cap * H * 4), os = take(cap * 4), oqkv = take(cap * (QD + 2 * KD) * 4),
+               oq = take(cap * QD * 4), oatt = take(cap * QD * 4), oh = take(cap * I * 4);
+  size_t part_rows = 0;
+  for (uint32_t M = 1; M <= cap; M++)
+    part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
+                                                                     uint32_t(c.num_key_value_heads)));
+  part_rows = std::max(part_rows, size_t(std::min<uint32_t>(cap, 8)) * qe::kAttnMaxSplits);
+  const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
+  const size_t osplit = take(size_t(8) * cap * H * 4);
+  HIP_TRY(hipStreamSynchronize(m->stream2));
+  if (m->batch_mem2) HIP_TRY(hipFree(m->batch_mem2));
+  m->batch_mem2 = nullptr;
+  HIP_TRY(hipMalloc(&m->batch_mem2, off));
+  m->batch_cap2 = cap;
+  m->bx2 = reinterpret_cast<float*>(m->batch_mem2 + ox);
+  m->bs2 = reinterpret_cast<float*>(m->batch_mem2 + os);
+  m->bqkv2 = reinterpret_cast<float*>(m->batch_mem2 + oqkv);
+  m->bq2 = reinterpret_cast<float*>(m->batch_mem2 + oq);
+  m->batt2 = reinterpret_cast<float*>(m->batch_mem2 + oatt);
+  m->bh2 = reinterpret_cast<float*>(m->batch_mem2 + oh);
+  m->bpart2 = reinterpret_cast<float*>(m->batch_mem2 + opart);
+  m->bsplit2 = reinterpret_cast<float*>(m->batch_mem2 + osplit);
+  return QE_OK;
+}
+
 // Copies n token ids to the device (in stream order, before the kernels that read them).
 int upload_ids(qe_model* m, const uint32_t* ids, uint64_t n) {
   if (n > m->ids_cap) {
@@ -561,17 +626,35 @@ enum BatchLogits { kNoLogits, kLastLogits, kAllLogits };
 // The ids are device memory (ids), or for a short pass the kernel argument ids_v (ids null).
 // kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the last row's logits to
 // m->logits (the decode step's buffer); kNoLogits: none (an inner chunk).
+// A chunk on the second stream (set 1) or, with events, on either stream of a two-stream prefill:
+// kv_done[l] is recorded once the chunk's layer-l K/V rows are in the cache, and the chunk's
+// layer-l attention waits for wait_kv[l] (the previous chunk's, on the other stream).
+struct ChunkStream {
+  int set;
+  hipEvent_t* kv_done;
+  hipEvent_t* wait_kv;
+};
+
 int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint32_t* ids, BatchLogits logits,
-                  const qe::TokenIds* ids_v = nullptr) {
+                  const qe::TokenIds* ids_v = nullptr, const ChunkStream* cs = nullptr) {
+  const bool set2 = cs && cs->set == 1;
+  float* const bx = set2 ? m->bx2 : m->bx;
+  float* const bs = set2 ? m->bs2 : m->bs;
+  float* const bqkv = set2 ? m->bqkv2 : m->bqkv;
+  float* const bq = set2 ? m->bq2 : m->bq;
+  float* const batt = set2 ? m->batt2 : m->batt;
+  float* const bh = set2 ? m->bh2 : m->bh;
+  float* const bpart = set2 ? m->bpart2 : m->bpart;
+  float* const bsplit = set2 ? m->bsplit2 : m->bsplit;
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
-  hipStream_t s = m->stream;
+  hipStream_t s = set2 ? m->stream2 : m->stream;
   const float eps = c.rms_norm_eps;
   // Up to kGemmSkinnyMaxM rows the skinny GEMM computes each norm's row scales itself and adds
-  // residuals in its epilogue. Past that, m->bs holds the row scales of the current norm input:
+  // residuals in its epilogue. Past that, bs holds the row scales of the current norm input:
   // from a rownorm launch for layer 0, then from the reduction that finishes each split o_proj /
   // down (residual add + the next norm's scales in one pass).
   // Up to kMvRowsMaxM rows the projections are matvecs over the M token rows: each weight is
@@ -588,33 +671,33 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       HIP_TRY(qe::launch_mv_rows(r, gain != nullptr, epi, s));
       return QE_OK;
     }
-    qe::GemmParams g{A, lda, m->bs, gain, W, M, N, K, C, ldc, eps};
+    qe::GemmParams g{A, lda, bs, gain, W, M, N, K, C, ldc, eps};
     HIP_TRY(qe::launch_gemm(g, gain != nullptr, epi, s));
     return QE_OK;
   };
-  // x += A W^T, then m->bs = the row scales of the updated x
+  // x += A W^T, then bs = the row scales of the updated x
   auto gemm_resadd = [&](const float* A, uint32_t lda, const uint16_t* W, uint32_t K) -> int {
-    if (mv || (skinny && qe::gemm_splits(M, H, K) == 1)) return gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd);
+    if (mv || (skinny && qe::gemm_splits(M, H, K) == 1)) return gemm(A, lda, nullptr, W, H, K, bx, H, qe::kGemmResAdd);
     if (!skinny && K % 64) {  // no split: residual epilogue, then the row scales
-      if (int rc2 = gemm(A, lda, nullptr, W, H, K, m->bx, H, qe::kGemmResAdd)) return rc2;
-      HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
+      if (int rc2 = gemm(A, lda, nullptr, W, H, K, bx, H, qe::kGemmResAdd)) return rc2;
+      HIP_TRY(qe::launch_rownorm(bx, M, H, eps, bs, s));
       return QE_OK;
     }
     const uint32_t z = qe::gemm_splits(M, H, K);
-    qe::GemmParams g{A, lda, nullptr, nullptr, W, M, H, K, m->bsplit, H, eps};
+    qe::GemmParams g{A, lda, nullptr, nullptr, W, M, H, K, bsplit, H, eps};
     HIP_TRY(qe::launch_gemm_split(g, z, s));
-    HIP_TRY(qe::launch_resadd_partials(m->bx, m->bsplit, z, M, H, eps, m->bs, s));
+    HIP_TRY(qe::launch_resadd_partials(bx, bsplit, z, M, H, eps, bs, s));
     return QE_OK;
   };
   int rc;
-  if (ids_v) HIP_TRY(qe::launch_embed_rows(m->embed, *ids_v, M, H, m->bx, s));
-  else HIP_TRY(qe::launch_embed_rows(m->embed, ids, M, H, m->bx, s));
-  if (!skinny) HIP_TRY(qe::launch_rownorm(m->bx, M, H, eps, m->bs, s));
+  if (ids_v) HIP_TRY(qe::launch_embed_rows(m->embed, *ids_v, M, H, bx, s));
+  else HIP_TRY(qe::launch_embed_rows(m->embed, ids, M, H, bx, s));
+  if (!skinny) HIP_TRY(qe::launch_rownorm(bx, M, H, eps, bs, s));
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     // q/k norm + RoPE, K/V append, causal attention (cpu_inference.rs:134-162)
     qe::BatchAttnParams a{};
-    a.qkv = m->bqkv; a.q = m->bq; a.att = m->batt; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
+    a.qkv = bqkv; a.q = bq; a.att = batt; a.q_norm = w.q_norm; a.k_norm = w.k_norm; a.rope = kv->rope;
     a.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
     a.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
     a.M = M; a.start = start; a.max_seq = uint32_t(kv->max_seq);
@@ -624,21 +707,25 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
     // norm, RoPE and K/V append in its epilogue, the others in k_qk_rope
     hipError_t fused = hipErrorNotSupported;
     if (!mv && !skinny) {
-      const qe::GemmParams g{m->bx, H, m->bs, w.w_in, w.w_qkv, M, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, eps};
+      const qe::GemmParams g{bx, H, bs, w.w_in, w.w_qkv, M, QD + 2 * KD, H, bqkv, QD + 2 * KD, eps};
       fused = qe::launch_gemm_qk_rope(g, a, s);
       if (fused != hipSuccess && fused != hipErrorNotSupported) HIP_TRY(fused);
     }
     if (fused != hipSuccess) {
-      if ((rc = gemm(m->bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, m->bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
+      if ((rc = gemm(bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
       HIP_TRY(qe::launch_qk_rope(a, s));
     }
+    // two-stream prefill: this layer's K/V rows are in the cache; the attention reads the
+    // previous chunk's, appended on the other stream
+    if (cs && cs->kv_done) HIP_TRY(hipEventRecord(cs->kv_done[l], s));
+    if (cs && cs->wait_kv) HIP_TRY(hipStreamWaitEvent(s, cs->wait_kv[l], 0));
     const uint32_t rows_per_kv = (a.n_heads / a.n_kv) * M;
     uint32_t merge_splits = 0;  // > 0: o_proj merges this many attention runs in its prologue
     if (m->rows_split_attn && (rows_per_kv == 1 || rows_per_kv == 2 || rows_per_kv == 4 || rows_per_kv == 8)) {
       // few tokens: the split kernel, the q heads of all M tokens of a KV head over one read of
       // its K/V, each token causal (positions up to its own), runs of 64 positions
       AttnParams r{};
-      r.qkv = m->bq; r.k_cache = a.k_cache; r.v_cache = a.v_cache; r.partial = m->bpart;
+      r.qkv = bq; r.k_cache = a.k_cache; r.v_cache = a.v_cache; r.partial = bpart;
       r.n_kv = a.n_kv; r.n_heads = a.n_kv * rows_per_kv; r.max_seq = a.max_seq; r.scale = a.scale;
       r.kv_bf16 = a.kv_bf16; r.n_pos_fixed = start + M; r.tok_heads = a.n_heads / a.n_kv; r.q_tok_stride = QD;
       // 8 rows (4 tokens): two workgroups of 4 rows per KV head halve each one's score and
@@ -658,9 +745,9 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       // with few runs the multi-row o_proj merges them in its prologue, as the decode step's does
       if (mv && m->mv_merge && qe::mv_rows_merge_fits(M, splits) && QD % D == 0 && QD / 8 <= 256)
         merge_splits = splits;
-      HIP_TRY(qe::launch_attention_rows(r, splits, merge_splits ? nullptr : m->batt, s));
+      HIP_TRY(qe::launch_attention_rows(r, splits, merge_splits ? nullptr : batt, s));
     } else {
-      a.part = m->bpart;
+      a.part = bpart;
       if (m->prefill_prefetch && !skinny) {
         // the attention is latency-bound: extra workgroups load o_proj's weights (a split GEMM)
         // into L2
@@ -671,30 +758,30 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
     }
     // o_proj + residual (cpu_inference.rs:163-164)
     if (merge_splits) {
-      qe::MvRowsParams r{w.w_o, nullptr, nullptr, m->bx, M, H, QD, H, eps};
-      r.attn_part = m->bpart; r.attn_splits = merge_splits; r.tok_heads = a.n_heads / a.n_kv;
+      qe::MvRowsParams r{w.w_o, nullptr, nullptr, bx, M, H, QD, H, eps};
+      r.attn_part = bpart; r.attn_splits = merge_splits; r.tok_heads = a.n_heads / a.n_kv;
       HIP_TRY(qe::launch_mv_rows_merge(r, s));
-    } else if ((rc = gemm_resadd(m->batt, QD, w.w_o, QD))) {
+    } else if ((rc = gemm_resadd(batt, QD, w.w_o, QD))) {
       return rc;
     }
     // post_attention_layernorm + gate/up + silu*up, down + residual (cpu_inference.rs:167-172)
-    if ((rc = gemm(m->bx, H, w.w_post, w.w_gu, 2 * I, H, m->bh, I, qe::kGemmSiluPair))) return rc;
-    if ((rc = gemm_resadd(m->bh, I, w.w_down, I))) return rc;
+    if ((rc = gemm(bx, H, w.w_post, w.w_gu, 2 * I, H, bh, I, qe::kGemmSiluPair))) return rc;
+    if ((rc = gemm_resadd(bh, I, w.w_down, I))) return rc;
   }
   // final norm + lm_head (cpu_inference.rs:175-178)
   if (logits == kAllLogits) {
     hipError_t lh = hipErrorNotSupported;
     if (mv && m->lm_head_rows) {
-      const qe::MvRowsParams r{m->lm_head, m->bx, m->final_norm, m->blogits, M, V, H, V, eps};
+      const qe::MvRowsParams r{m->lm_head, bx, m->final_norm, m->blogits, M, V, H, V, eps};
       lh = qe::launch_lm_head_rows(r, s);
       if (lh != hipSuccess && lh != hipErrorNotSupported) HIP_TRY(lh);
     }
     if (lh != hipSuccess &&
-        (rc = gemm(m->bx, H, m->final_norm, m->lm_head, V, H, m->blogits, V, qe::kGemmStore)))
+        (rc = gemm(bx, H, m->final_norm, m->lm_head, V, H, m->blogits, V, qe::kGemmStore)))
       return rc;
   } else if (logits == kLastLogits) {
     MatvecParams p{};
-    p.eps = eps; p.w = m->lm_head; p.x = m->bx + size_t(M - 1) * H; p.nw = m->final_norm;
+    p.eps = eps; p.w = m->lm_head; p.x = bx + size_t(M - 1) * H; p.nw = m->final_norm;
     p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
     HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
   }
@@ -1036,15 +1123,36 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
     if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
   int rc = ensure_batch(model, chunk, 0);
   if (rc) return rc;
+  // chunks of more than kGemmSkinnyMaxM tokens alternate between two streams and buffer sets:
+  // chunk i's layer-l attention waits for chunk i-1's layer-l K/V rows, and otherwise the two
+  // chunks' launches overlap (each chunk runs the same kernels as on one stream)
+  const bool two = model->prefill_streams == 2 && n > chunk && chunk > qe::kGemmSkinnyMaxM;
+  if (two && (rc = ensure_batch2(model, chunk))) return rc;
   if ((rc = upload_ids(model, ids, n))) return rc;
-  for (uint64_t done = 0; done < n;) {
+  uint32_t last_set = 0;
+  if (two) {  // the second stream starts after everything queued so far (ids, earlier steps)
+    HIP_TRY(hipEventRecord(model->start_ev, model->stream));
+    HIP_TRY(hipStreamWaitEvent(model->stream2, model->start_ev, 0));
+  }
+  for (uint64_t done = 0, i = 0; done < n; i++) {
     const uint32_t M = uint32_t(std::min<uint64_t>(chunk, n - done));
     const BatchLogits lg = done + M == n && last_logits ? kLastLogits : kNoLogits;
-    if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), model->ids_dev + done, lg))) return rc;
+    ChunkStream cs{int(i % 2), nullptr, nullptr};
+    if (two) {
+      cs.kv_done = model->kv_ev[i % 2].data();
+      cs.wait_kv = i > 0 ? model->kv_ev[1 - i % 2].data() : nullptr;
+    }
+    last_set = two ? uint32_t(i % 2) : 0u;
+    if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), model->ids_dev + done, lg, nullptr,
+                            two ? &cs : nullptr)))
+      return rc;
     done += M;
   }
+  if (two) HIP_TRY(hipStreamSynchronize(model->stream2));
   if (last_logits) {
-    HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost, model->stream));
+    HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
+                           last_set ? model->stream2 : model->stream));
+    HIP_TRY(hipStreamSynchronize(last_set ? model->stream2 : model->stream));
   }
   HIP_TRY(hipStreamSynchronize(model->stream));
   if (last_logits) memcpy(last_logits, model->h_logits, model->cfg.vocab_size * 4);
