@@ -113,9 +113,9 @@ int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t step
  * cache and the chunk. Appends the K/V of every position and writes the last token's logits
  * (nullable). Same position contract as qe_prefill; logits agree with it within 1e-2, not bit for
  * bit. The model's chunk buffers are allocated on first use. Consecutive chunks of more than 32
- * tokens run on two streams (the model's and a second one it creates on first use, with a second
- * set of chunk buffers), each chunk's attention ordered after the previous chunk's K/V rows of the
- * same layer; the call returns once both streams are done. n = 0 does nothing. */
+ * tokens run on two streams (the model's and one it creates on first use, with a second set of
+ * chunk buffers), each chunk's attention ordered after the earlier chunks' K/V rows of the same
+ * layer; the call returns once every stream is done. n = 0 does nothing. */
 int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t start_pos, qe_kv* kv,
                      uint32_t chunk, float* last_logits);
 /* Verify k (1..64) tokens at positions start_pos.. in one pass (the k-token check of speculative

@@ -85,6 +85,18 @@ static_assert(kVerifyMaxTokens <= qe::kIdsByValue, "verify ids travel in a kerne
 
 }  // namespace
 
+// The chunk buffers, stream and per-layer K/V events of one of the extra streams of a chunked
+// prefill (the first stream is the model's own, with its batch buffers).
+struct ChunkBufs {
+  uint8_t* mem = nullptr;
+  uint32_t cap = 0;
+  hipStream_t stream = nullptr;
+  float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
+  float *bpart = nullptr, *bsplit = nullptr;
+  std::vector<hipEvent_t> kv_ev;
+};
+constexpr int kMaxPrefillStreams = 4;
+
 struct qe_model {
   qe::Checkpoint ckpt;
   qe_config cfg{};
@@ -135,19 +147,16 @@ struct qe_model {
   float *bx = nullptr, *bs = nullptr, *bqkv = nullptr, *bq = nullptr, *batt = nullptr, *bh = nullptr;
   float* bpart = nullptr;   // causal attention partials
   float* bsplit = nullptr;  // split GEMM partial sums [splits][cap][hidden]
-  // a chunked prefill on two streams (QE_PREFILL_STREAMS=1: one): the second stream, the
-  // second set of chunk buffers and, per set, one event per layer recorded once the chunk's K/V
-  // rows of that layer are in the cache. 2048 tokens in chunks of 512: 10.8-11.2 vs 12.5-12.8 ms.
-  // Once the process has the second stream, eager launches on the first are slightly slower (a
-  // k = 4 verify 1.22-1.23 vs 1.195-1.205 ms; 1.21 with the stream created but never used;
-  // destroying it after each prefill does not help); graph-replayed decode steps are not.
+  // a chunked prefill on prefill_streams streams (QE_PREFILL_STREAMS, 1 to 4): the extra streams
+  // with their chunk buffers and, per stream, one event per layer recorded once the chunk's K/V
+  // rows of that layer are in the cache. 2048 tokens in chunks of 512: 10.8-11.2 ms on two
+  // streams vs 12.5-12.8 on one (three streams: the same as two; four: slower). Once the process
+  // has a second stream, eager launches on the first are slightly slower (a k = 4 verify
+  // 1.22-1.23 vs 1.195-1.205 ms; 1.21 with the stream created but never used; destroying it
+  // after each prefill does not help); graph-replayed decode steps are not.
   int prefill_streams = 2;
-  hipStream_t stream2 = nullptr;
-  uint8_t* batch_mem2 = nullptr;
-  uint32_t batch_cap2 = 0;
-  float *bx2 = nullptr, *bs2 = nullptr, *bqkv2 = nullptr, *bq2 = nullptr, *batt2 = nullptr, *bh2 = nullptr;
-  float *bpart2 = nullptr, *bsplit2 = nullptr;
-  std::vector<hipEvent_t> kv_ev[2];
+  ChunkBufs extra[kMaxPrefillStreams - 1];
+  std::vector<hipEvent_t> kv_ev0;  // the first stream's per-layer K/V events
   hipEvent_t start_ev = nullptr;
   ArgCand* bcand = nullptr;  // row argmax candidates of a verify pass [kVerifyMaxTokens][kArgParts]
   float* blogits = nullptr;
@@ -158,13 +167,15 @@ struct qe_model {
     if (stream) (void)hipStreamSynchronize(stream);
     if (arena) (void)hipFree(arena);
     if (scratch) (void)hipFree(scratch);
-    if (stream2) (void)hipStreamSynchronize(stream2);
     if (batch_mem) (void)hipFree(batch_mem);
-    if (batch_mem2) (void)hipFree(batch_mem2);
-    for (auto& v : kv_ev)
-      for (hipEvent_t e : v) (void)hipEventDestroy(e);
+    for (ChunkBufs& b : extra) {
+      if (b.stream) (void)hipStreamSynchronize(b.stream);
+      if (b.mem) (void)hipFree(b.mem);
+      for (hipEvent_t e : b.kv_ev) (void)hipEventDestroy(e);
+      if (b.stream) (void)hipStreamDestroy(b.stream);
+    }
+    for (hipEvent_t e : kv_ev0) (void)hipEventDestroy(e);
     if (start_ev) (void)hipEventDestroy(start_ev);
-    if (stream2) (void)hipStreamDestroy(stream2);
     if (ids_dev) (void)hipFree(ids_dev);
     if (h_logits) (void)hipHostFree(h_logits);
     if (h_small) (void)hipHostFree(h_small);
@@ -261,7 +272,8 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
-  if (const char* ps = getenv("QE_PREFILL_STREAMS")) m->prefill_streams = strcmp(ps, "1") == 0 ? 1 : 2;
+  if (const char* ps = getenv("QE_PREFILL_STREAMS"))
+    m->prefill_streams = std::min(std::max(atoi(ps), 1), kMaxPrefillStreams);
   if (const char* pp = getenv("QE_PREFILL_PREFETCH")) m->prefill_prefetch = strcmp(pp, "0") != 0;
   const qe_config& c = m->cfg;
   const uint64_t H = c.hidden_size, I = c.intermediate_size, L = c.num_hidden_layers, V = c.vocab_size;
@@ -562,47 +574,54 @@ int ensure_batch(qe_model* m, uint32_t cap, uint32_t logit_rows) {
   return QE_OK;
 }
 
-// The second stream of a chunked prefill: its chunk buffers for up to `cap` tokens (those of
-// ensure_batch without the logit rows), the stream, and the per-layer K/V events of both sets.
-int ensure_batch2(qe_model* m, uint32_t cap) {
+// The extra streams of a chunked prefill on `streams` streams: their chunk buffers for up to
+// `cap` tokens (those of ensure_batch without the logit rows), and the per-layer K/V events.
+int ensure_streams(qe_model* m, uint32_t cap, int streams) {
   const qe_config& c = m->cfg;
   const size_t L = c.num_hidden_layers;
-  if (!m->stream2) HIP_TRY(hipStreamCreateWithFlags(&m->stream2, hipStreamNonBlocking));
-  if (!m->start_ev) HIP_TRY(hipEventCreateWithFlags(&m->start_ev, hipEventDisableTiming));
-  for (auto& v : m->kv_ev)
+  auto events = [&](std::vector<hipEvent_t>& v) -> int {
     while (v.size() < L) {
       hipEvent_t e;
       HIP_TRY(hipEventCreateWithFlags(&e, hipEventDisableTiming));
       v.push_back(e);
     }
-  if (m->batch_mem2 && cap <= m->batch_cap2) return QE_OK;
-  cap = std::max(cap, m->batch_cap2);
+    return QE_OK;
+  };
+  if (!m->start_ev) HIP_TRY(hipEventCreateWithFlags(&m->start_ev, hipEventDisableTiming));
+  if (int rc = events(m->kv_ev0)) return rc;
   const size_t H = c.hidden_size, I = c.intermediate_size, D = c.head_dim;
   const size_t QD = c.num_attention_heads * D, KD = c.num_key_value_heads * D;
-  size_t off = 0;
-  auto take = [&](size_t b) { size_t o = off; off = align_up(off + b, 256); return o; };
-  const size_t ox = take(cap * H * 4), os = take(cap * 4), oqkv = take(cap * (QD + 2 * KD) * 4),
-               oq = take(cap * QD * 4), oatt = take(cap * QD * 4), oh = take(cap * I * 4);
-  size_t part_rows = 0;
-  for (uint32_t M = 1; M <= cap; M++)
-    part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
-                                                                     uint32_t(c.num_key_value_heads)));
-  part_rows = std::max(part_rows, size_t(std::min<uint32_t>(cap, 8)) * qe::kAttnMaxSplits);
-  const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
-  const size_t osplit = take(size_t(8) * cap * H * 4);
-  HIP_TRY(hipStreamSynchronize(m->stream2));
-  if (m->batch_mem2) HIP_TRY(hipFree(m->batch_mem2));
-  m->batch_mem2 = nullptr;
-  HIP_TRY(hipMalloc(&m->batch_mem2, off));
-  m->batch_cap2 = cap;
-  m->bx2 = reinterpret_cast<float*>(m->batch_mem2 + ox);
-  m->bs2 = reinterpret_cast<float*>(m->batch_mem2 + os);
-  m->bqkv2 = reinterpret_cast<float*>(m->batch_mem2 + oqkv);
-  m->bq2 = reinterpret_cast<float*>(m->batch_mem2 + oq);
-  m->batt2 = reinterpret_cast<float*>(m->batch_mem2 + oatt);
-  m->bh2 = reinterpret_cast<float*>(m->batch_mem2 + oh);
-  m->bpart2 = reinterpret_cast<float*>(m->batch_mem2 + opart);
-  m->bsplit2 = reinterpret_cast<float*>(m->batch_mem2 + osplit);
+  for (int i = 0; i + 1 < streams; i++) {
+    ChunkBufs& b = m->extra[i];
+    if (!b.stream) HIP_TRY(hipStreamCreateWithFlags(&b.stream, hipStreamNonBlocking));
+    if (int rc = events(b.kv_ev)) return rc;
+    if (b.mem && cap <= b.cap) continue;
+    const uint32_t bcap = std::max(cap, b.cap);
+    size_t off = 0;
+    auto take = [&](size_t n) { size_t o = off; off = align_up(off + n, 256); return o; };
+    const size_t ox = take(bcap * H * 4), os = take(bcap * 4), oqkv = take(bcap * (QD + 2 * KD) * 4),
+                 oq = take(bcap * QD * 4), oatt = take(bcap * QD * 4), oh = take(bcap * I * 4);
+    size_t part_rows = 0;
+    for (uint32_t M = 1; M <= bcap; M++)
+      part_rows = std::max(part_rows, size_t(M) * qe::attn_causal_runs(M, 1u << 30, uint32_t(c.num_attention_heads),
+                                                                       uint32_t(c.num_key_value_heads)));
+    part_rows = std::max(part_rows, size_t(std::min<uint32_t>(bcap, 8)) * qe::kAttnMaxSplits);
+    const size_t opart = take(part_rows * c.num_attention_heads * qe::kPartStride * 4);
+    const size_t osplit = take(size_t(8) * bcap * H * 4);
+    HIP_TRY(hipStreamSynchronize(b.stream));
+    if (b.mem) HIP_TRY(hipFree(b.mem));
+    b.mem = nullptr;
+    HIP_TRY(hipMalloc(&b.mem, off));
+    b.cap = bcap;
+    b.bx = reinterpret_cast<float*>(b.mem + ox);
+    b.bs = reinterpret_cast<float*>(b.mem + os);
+    b.bqkv = reinterpret_cast<float*>(b.mem + oqkv);
+    b.bq = reinterpret_cast<float*>(b.mem + oq);
+    b.batt = reinterpret_cast<float*>(b.mem + oatt);
+    b.bh = reinterpret_cast<float*>(b.mem + oh);
+    b.bpart = reinterpret_cast<float*>(b.mem + opart);
+    b.bsplit = reinterpret_cast<float*>(b.mem + osplit);
+  }
   return QE_OK;
 }
 
@@ -622,36 +641,37 @@ int upload_ids(qe_model* m, const uint32_t* ids, uint64_t n) {
 
 enum BatchLogits { kNoLogits, kLastLogits, kAllLogits };
 
-// One chunk of M tokens at positions start..start+M-1 through every layer, appending their K/V.
-// The ids are device memory (ids), or for a short pass the kernel argument ids_v (ids null).
-// kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the last row's logits to
-// m->logits (the decode step's buffer); kNoLogits: none (an inner chunk).
-// A chunk on the second stream (set 1) or, with events, on either stream of a two-stream prefill:
-// kv_done[l] is recorded once the chunk's layer-l K/V rows are in the cache, and the chunk's
-// layer-l attention waits for wait_kv[l] (the previous chunk's, on the other stream).
+// A chunk of a multi-stream prefill, on stream `set` (0: the model's, with its batch buffers; i > 0:
+// extra[i - 1]): its layer-l attention waits for wait_kv[l] (the previous chunk's event, on another
+// stream), and kv_done[l] is recorded after that wait and this chunk's layer-l K/V rows.
 struct ChunkStream {
   int set;
   hipEvent_t* kv_done;
   hipEvent_t* wait_kv;
 };
 
+// One chunk of M tokens at positions start..start+M-1 through every layer, appending their K/V.
+// The ids are device memory (ids), or for a short pass the kernel argument ids_v (ids null).
+// kAllLogits: logits of every row to m->blogits [M][V]; kLastLogits: the last row's logits to
+// m->logits (the decode step's buffer); kNoLogits: none (an inner chunk). cs: a chunk of a
+// multi-stream prefill (its buffers, stream and events), else the model's stream and buffers.
 int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint32_t* ids, BatchLogits logits,
                   const qe::TokenIds* ids_v = nullptr, const ChunkStream* cs = nullptr) {
-  const bool set2 = cs && cs->set == 1;
-  float* const bx = set2 ? m->bx2 : m->bx;
-  float* const bs = set2 ? m->bs2 : m->bs;
-  float* const bqkv = set2 ? m->bqkv2 : m->bqkv;
-  float* const bq = set2 ? m->bq2 : m->bq;
-  float* const batt = set2 ? m->batt2 : m->batt;
-  float* const bh = set2 ? m->bh2 : m->bh;
-  float* const bpart = set2 ? m->bpart2 : m->bpart;
-  float* const bsplit = set2 ? m->bsplit2 : m->bsplit;
+  const ChunkBufs* xb = cs && cs->set > 0 ? &m->extra[cs->set - 1] : nullptr;
+  float* const bx = xb ? xb->bx : m->bx;
+  float* const bs = xb ? xb->bs : m->bs;
+  float* const bqkv = xb ? xb->bqkv : m->bqkv;
+  float* const bq = xb ? xb->bq : m->bq;
+  float* const batt = xb ? xb->batt : m->batt;
+  float* const bh = xb ? xb->bh : m->bh;
+  float* const bpart = xb ? xb->bpart : m->bpart;
+  float* const bsplit = xb ? xb->bsplit : m->bsplit;
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
   const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
-  hipStream_t s = set2 ? m->stream2 : m->stream;
+  hipStream_t s = xb ? xb->stream : m->stream;
   const float eps = c.rms_norm_eps;
   // Up to kGemmSkinnyMaxM rows the skinny GEMM computes each norm's row scales itself and adds
   // residuals in its epilogue. Past that, bs holds the row scales of the current norm input:
@@ -715,10 +735,12 @@ int enqueue_batch(qe_model* m, qe_kv* kv, uint32_t M, uint32_t start, const uint
       if ((rc = gemm(bx, H, w.w_in, w.w_qkv, QD + 2 * KD, H, bqkv, QD + 2 * KD, qe::kGemmStore))) return rc;
       HIP_TRY(qe::launch_qk_rope(a, s));
     }
-    // two-stream prefill: this layer's K/V rows are in the cache; the attention reads the
-    // previous chunk's, appended on the other stream
-    if (cs && cs->kv_done) HIP_TRY(hipEventRecord(cs->kv_done[l], s));
+    // multi-stream prefill: the attention reads the previous chunks' K/V rows of this layer,
+    // appended on other streams. The event is recorded after this chunk's own wait, so that it
+    // stands for the K/V rows of this chunk and of every chunk before it (chunk i waits for
+    // chunk i-1 only, whatever the number of streams).
     if (cs && cs->wait_kv) HIP_TRY(hipStreamWaitEvent(s, cs->wait_kv[l], 0));
+    if (cs && cs->kv_done) HIP_TRY(hipEventRecord(cs->kv_done[l], s));
     const uint32_t rows_per_kv = (a.n_heads / a.n_kv) * M;
     uint32_t merge_splits = 0;  // > 0: o_proj merges this many attention runs in its prologue
     if (m->rows_split_attn && (rows_per_kv == 1 || rows_per_kv == 2 || rows_per_kv == 4 || rows_per_kv == 8)) {
@@ -1123,36 +1145,40 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
     if (ids[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u at %llu >= vocab", ids[i], (unsigned long long)i);
   int rc = ensure_batch(model, chunk, 0);
   if (rc) return rc;
-  // chunks of more than kGemmSkinnyMaxM tokens alternate between two streams and buffer sets:
-  // chunk i's layer-l attention waits for chunk i-1's layer-l K/V rows, and otherwise the two
-  // chunks' launches overlap (each chunk runs the same kernels as on one stream)
-  const bool two = model->prefill_streams == 2 && n > chunk && chunk > qe::kGemmSkinnyMaxM;
-  if (two && (rc = ensure_batch2(model, chunk))) return rc;
+  // chunks of more than kGemmSkinnyMaxM tokens go round-robin over up to prefill_streams streams
+  // and buffer sets: chunk i's layer-l attention waits for chunk i-1's layer-l K/V rows, and
+  // otherwise the chunks' launches overlap (each chunk runs the same kernels as on one stream)
+  const uint64_t n_chunks = (n + chunk - 1) / chunk;
+  const int S = chunk > qe::kGemmSkinnyMaxM ? int(std::min<uint64_t>(model->prefill_streams, n_chunks)) : 1;
+  if (S > 1 && (rc = ensure_streams(model, chunk, S))) return rc;
   if ((rc = upload_ids(model, ids, n))) return rc;
-  uint32_t last_set = 0;
-  if (two) {  // the second stream starts after everything queued so far (ids, earlier steps)
+  auto stream_of = [&](int set) { return set ? model->extra[set - 1].stream : model->stream; };
+  auto events_of = [&](int set) { return set ? model->extra[set - 1].kv_ev.data() : model->kv_ev0.data(); };
+  if (S > 1) {  // the extra streams start after everything queued so far (ids, earlier steps)
     HIP_TRY(hipEventRecord(model->start_ev, model->stream));
-    HIP_TRY(hipStreamWaitEvent(model->stream2, model->start_ev, 0));
+    for (int j = 1; j < S; j++) HIP_TRY(hipStreamWaitEvent(stream_of(j), model->start_ev, 0));
   }
+  int last_set = 0;
   for (uint64_t done = 0, i = 0; done < n; i++) {
     const uint32_t M = uint32_t(std::min<uint64_t>(chunk, n - done));
     const BatchLogits lg = done + M == n && last_logits ? kLastLogits : kNoLogits;
-    ChunkStream cs{int(i % 2), nullptr, nullptr};
-    if (two) {
-      cs.kv_done = model->kv_ev[i % 2].data();
-      cs.wait_kv = i > 0 ? model->kv_ev[1 - i % 2].data() : nullptr;
+    const int set = int(i % uint64_t(S));
+    ChunkStream cs{set, nullptr, nullptr};
+    if (S > 1) {
+      cs.kv_done = events_of(set);
+      cs.wait_kv = i > 0 ? events_of(int((i - 1) % uint64_t(S))) : nullptr;
     }
-    last_set = two ? uint32_t(i % 2) : 0u;
+    last_set = set;
     if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), model->ids_dev + done, lg, nullptr,
-                            two ? &cs : nullptr)))
+                            S > 1 ? &cs : nullptr)))
       return rc;
     done += M;
   }
-  if (two) HIP_TRY(hipStreamSynchronize(model->stream2));
+  for (int j = 1; j < S; j++) HIP_TRY(hipStreamSynchronize(stream_of(j)));
   if (last_logits) {
     HIP_TRY(hipMemcpyAsync(model->h_logits, model->logits, model->cfg.vocab_size * 4, hipMemcpyDeviceToHost,
-                           last_set ? model->stream2 : model->stream));
-    HIP_TRY(hipStreamSynchronize(last_set ? model->stream2 : model->stream));
+                           stream_of(last_set)));
+    HIP_TRY(hipStreamSynchronize(stream_of(last_set)));
   }
   HIP_TRY(hipStreamSynchronize(model->stream));
   if (last_logits) memcpy(last_logits, model->h_logits, model->cfg.vocab_size * 4);
