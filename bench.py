@@ -369,43 +369,44 @@ def lookup_bench(qe, model, cfg, args):
 
     # The random-init model's greedy output repeats itself far more than text does, so lookup
     # drafts are accepted more often than on text (the reference's MLX replay saw 1.22-1.32
-    # tokens per pass, README.md:109-111). To time the speculative loop at those rates, the
-    # drafts are made from the known greedy continuation: on a fraction a of the passes the first
-    # draft token is the true next token (accepted), every other draft token is wrong (rejected),
-    # so a pass emits 1 + a tokens on average; each pass is a qe_verify_greedy of 1 + kd rows,
-    # driven from Python. The emitted tokens are checked against the plain decode.
+    # tokens per pass, README.md:109-111). To time the speculative loop at those rates, a draft
+    # source (qe_decode_drafted) makes its drafts from the known greedy continuation: on a
+    # fraction a of its drafts the first token is the true next token (accepted), every other
+    # draft token is wrong (rejected), so a pass emits 1 + a tokens on average. The loop is the
+    # engine's own, with its adaptive rule (plain blocks while passes do not pay) and without it;
+    # the emitted tokens are checked against the plain decode.
     seq = [first] + list(plain)
 
-    def emulate(accept: float, kd: int):
+    def emulate(accept: float, kd: int, adaptive: bool):
         best, stats = float("inf"), None
         for _ in range(3):
             c = qe.KVCache(model, P + K + 1)
             model.prefill(prompt, 0, c, want_logits=False)
-            pos, i, credit, passes, out = P, 0, 0.0, 0, []
+            credit = [0.0]
+
+            def draft(hist, k):
+                i = len(hist) - P - 1  # index of the last token in seq
+                credit[0] += accept
+                a = 1 if credit[0] >= 1.0 else 0
+                credit[0] -= a
+                return seq[i + 1:i + 1 + a] + [(seq[i + 1 + j] + 1) % cfg.vocab_size for j in range(a, min(kd, k))]
+
             t0 = time.perf_counter()
-            while len(out) < K:
-                nd = min(kd, K - len(out) - 1)
-                credit += accept
-                a = 1 if credit >= 1.0 and nd > 0 else 0
-                credit -= a
-                draft = seq[i + 1:i + 1 + a] + [(seq[i + 1 + j] + 1) % cfg.vocab_size for j in range(a, nd)]
-                g = model.verify_greedy(np.array([seq[i]] + draft, dtype=np.uint32), pos, c).tolist()
-                n = 0
-                while n < nd and draft[n] == g[n]:
-                    n += 1
-                out += g[:n + 1]
-                i, pos, passes = i + n + 1, pos + n + 1, passes + 1
+            out, st = model.decode_drafted(first, P, K, c, draft, context=prompt, k_max=kd, adaptive=adaptive)
             dt = time.perf_counter() - t0
-            if out[:K] != list(plain):
-                raise RuntimeError("emulated-acceptance lookup left the greedy sequence")
+            if out != list(plain):
+                raise RuntimeError("drafted decode left the greedy sequence")
             if dt < best:
-                best, stats = dt, {"tok_s": round(K / dt, 1), "tokens_per_pass": round(K / passes, 3),
-                                   "passes": passes, "ms_per_pass": round(dt / passes * 1e3, 3),
-                                   "speedup": round(t_plain / dt, 3)}
+                passes = st["passes"] + st["single_steps"]
+                best, stats = dt, {"tok_s": round(K / dt, 1), "speedup": round(t_plain / dt, 3),
+                                   "tokens_per_pass": round((K - st["plain_steps"]) / max(passes, 1), 3),
+                                   "ms_per_pass": round(dt / max(passes, 1) * 1e3, 3) if not st["plain_steps"] else None,
+                                   **st}
         return stats
 
     res["emulated_text_acceptance"] = {
-        f"{1 + a:.2f}_tokens_per_pass_k{kd}": emulate(a, kd) for a in (0.22, 0.32) for kd in (1, 3)}
+        f"{1 + a:.2f}_tokens_per_pass_k{kd}" + ("" if ad else "_always_draft"): emulate(a, kd, ad)
+        for a in (0.22, 0.32) for kd in (1, 3) for ad in (True, False)}
     return res
 
 

@@ -141,10 +141,23 @@ typedef struct {
   uint64_t drafted;       /* draft tokens checked */
   uint64_t accepted;      /* draft tokens accepted */
   uint64_t single_steps;  /* decode steps taken when no draft was found */
+  uint64_t plain_steps;   /* decode steps taken in plain blocks while drafting did not pay */
 } qe_lookup_stats;
+/* Adaptive (on unless QE_LOOKUP_ADAPTIVE=0 when the model was loaded): the host times the passes
+ * as they run; once they average under 2 tokens each it also times one block of 16 pipelined
+ * decode steps, and while the passes emit fewer tokens per second than those steps, it decodes
+ * plain blocks of 16 steps with one pass after each (plain_steps). The tokens do not change. */
 int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
                      uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
                      qe_lookup_stats* stats);
+/* A draft source: writes up to k_max tokens that are to follow history[0..n) (context, first and
+ * the tokens emitted so far) to draft_out and returns their count (0: no draft). */
+typedef uint32_t (*qe_draft_fn)(void* user, const uint32_t* history, uint64_t n, uint32_t k_max, uint32_t* draft_out);
+/* qe_decode_lookup with the drafts of `draft` (a draft model, another lookup rule, ...) instead
+ * of prompt lookup, and the adaptive rule on when adaptive != 0. No reference counterpart. */
+int qe_decode_drafted(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                      uint64_t steps, qe_kv* kv, uint32_t k_max, qe_draft_fn draft, void* draft_user, int adaptive,
+                      qe_on_token on_token, void* user, qe_lookup_stats* stats);
 /* The draft rule alone (host code, no device): writes the draft qe_decode_lookup would check
  * after history[0..n) (at most k_max tokens) to draft_out and returns its length. */
 uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, uint32_t k_max, uint32_t* draft_out);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <chrono>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -141,6 +142,12 @@ struct qe_model {
   // ... and their lm_head is the decode step's matvec over all their rows, each row's logits
   // equal to a decode step's (QE_LM_HEAD_ROWS=0: the skinny GEMM; a 2-row pass 0.83 -> 0.80 ms)
   bool lm_head_rows = true;
+  // qe_decode_lookup decodes plain blocks while its verify passes emit tokens more slowly than
+  // plain steps (QE_LOOKUP_ADAPTIVE=0: always drafts)
+  bool lookup_adaptive = true;
+  // its last timing of a plain decode step (seconds per step) and the position it was taken at
+  double plain_step_s = 0;
+  uint64_t plain_step_pos = 0;
   // multi-token (chunked prefill / verify) buffers, grown on first use: up to batch_cap tokens
   uint8_t* batch_mem = nullptr;
   uint32_t batch_cap = 0, batch_logit_rows = 0;
@@ -272,6 +279,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
+  if (const char* la = getenv("QE_LOOKUP_ADAPTIVE")) m->lookup_adaptive = strcmp(la, "0") != 0;
   if (const char* ps = getenv("QE_PREFILL_STREAMS"))
     m->prefill_streams = std::min(std::max(atoi(ps), 1), kMaxPrefillStreams);
   if (const char* pp = getenv("QE_PREFILL_PREFETCH")) m->prefill_prefetch = strcmp(pp, "0") != 0;
@@ -1272,61 +1280,153 @@ int qe_verify_greedy(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t 
   return verify_greedy(model, ids, uint32_t(k), start_pos, kv, tokens_out);
 }
 
-int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
-                     uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
-                     qe_lookup_stats* stats) {
+}  // extern "C"
+
+namespace {
+
+// The speculative loop of qe_decode_lookup / qe_decode_drafted. Each pass asks `draft` for up to
+// k tokens after the history and checks them with one verify pass (accepted while they equal the
+// greedy token of the row before, plus that pass's own token); with no draft it takes one decode
+// step. Adaptive: the host times the passes as they run (their mean seconds and tokens so far).
+// Once kAdaptMinPasses passes average under kAdaptMarginal tokens, one pipelined block of plain
+// decode steps is timed as well, unless the model holds such a timing from within
+// kAdaptStepReuse positions of this one; from then on, while even the passes' optimistic rate (mean
+// tokens plus one standard error, over their mean seconds) is below the plain steps' rate, the
+// loop decodes plain blocks of kAdaptBlock steps and tries one pass after each. The tokens are
+// the greedy ones whatever the loop does.
+constexpr double kAdaptMarginal = 2.0;
+constexpr uint64_t kAdaptBlock = 16;
+constexpr int kAdaptMinPasses = 6;
+constexpr uint64_t kAdaptStepReuse = 1024;
+
+template <class Draft>
+int decode_drafted(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                   uint64_t steps, qe_kv* kv, uint32_t k_max, Draft&& draft, bool adaptive, qe_on_token on_token,
+                   void* user, qe_lookup_stats* stats) {
   if (!model || !kv || (!context && n_context)) return fail(QE_ERR_ARG, "null argument");
   if (kv->model != model) return fail(QE_ERR_ARG, "cache belongs to another model");
   if (k_max == 0 || k_max >= kVerifyMaxTokens) return fail(QE_ERR_ARG, "k_max must be 1..%u", kVerifyMaxTokens - 1);
-  if (ngram == 0) return fail(QE_ERR_ARG, "ngram must be >= 1");
   if (start_pos > kv->len) return fail(QE_ERR_POS, "start_pos %llu is past the %llu cached positions", (unsigned long long)start_pos, (unsigned long long)kv->len);
   if (start_pos + steps > kv->max_seq) return fail(QE_ERR_POS, "decode end %llu exceeds KV cache size %llu", (unsigned long long)(start_pos + steps), (unsigned long long)kv->max_seq);
   if (first >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "token %u >= vocab", first);
   for (uint64_t i = 0; i < n_context; i++)
     if (context[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "context token %u at %llu >= vocab", context[i], (unsigned long long)i);
+  using clock = std::chrono::steady_clock;
+  auto secs = [](clock::time_point a, clock::time_point b) { return std::chrono::duration<double>(b - a).count(); };
   qe_lookup_stats st{};
-  std::vector<uint32_t> h(context, context + n_context), draft, ids, got(kVerifyMaxTokens);
+  std::vector<uint32_t> h(context, context + n_context), d(kVerifyMaxTokens), ids, got(kVerifyMaxTokens), blk;
   h.push_back(first);
   uint32_t cur = first;
   uint64_t pos = start_pos, emitted = 0;
+  // sums over the timed passes (seconds, tokens, tokens^2); the mean seconds of a plain step
+  double sum_s = 0, sum_tok = 0, sum_tok2 = 0, step_s = 0;
+  int passes_seen = 0;
+  if (adaptive && model->plain_step_s > 0 &&
+      std::max(start_pos, model->plain_step_pos) - std::min(start_pos, model->plain_step_pos) <= kAdaptStepReuse)
+    step_s = model->plain_step_s;
+  bool plain = false;  // the next iteration decodes a plain block
+  auto emit = [&](uint32_t tok) {
+    h.push_back(tok);
+    if (on_token) on_token(user, tok);
+  };
   int rc;
   while (emitted < steps) {
+    if (plain) {
+      const uint64_t nb = std::min(kAdaptBlock, steps - emitted);
+      blk.clear();
+      auto keep = [](void* u, uint32_t t) { static_cast<std::vector<uint32_t>*>(u)->push_back(t); };
+      const auto t0 = clock::now();
+      if ((rc = qe_decode(model, cur, pos, nb, kv, keep, &blk, nullptr))) return rc;
+      const double per = secs(t0, clock::now()) / double(nb);
+      step_s = step_s > 0 ? 0.5 * (step_s + per) : per;
+      model->plain_step_s = step_s;
+      model->plain_step_pos = pos;
+      for (uint32_t t : blk) emit(t);
+      st.plain_steps += nb;
+      cur = blk.back();
+      pos += nb;
+      emitted += nb;
+      plain = false;  // then one pass, which decides again
+      continue;
+    }
     // a pass emits accepted drafts + 1 token, so it never runs past `steps`
-    lookup_draft(h, ngram, uint32_t(std::min<uint64_t>(k_max, steps - emitted - 1)), draft);
-    if (draft.empty()) {  // nothing to verify: one decode step
+    const uint32_t kk = uint32_t(std::min<uint64_t>(k_max, steps - emitted - 1));
+    const uint32_t nd = kk ? std::min(draft(h, kk, d.data()), kk) : 0u;
+    if (nd == 0) {  // nothing to verify: one decode step
       uint32_t tok = 0;
       auto keep = [](void* u, uint32_t t) { *static_cast<uint32_t*>(u) = t; };
       if ((rc = qe_decode(model, cur, pos, 1, kv, keep, &tok, nullptr))) return rc;
       st.single_steps++;
-      h.push_back(tok);
-      if (on_token) on_token(user, tok);
+      emit(tok);
       cur = tok;
       pos++;
       emitted++;
       continue;
     }
+    for (uint32_t i = 0; i < nd; i++)
+      if (d[i] >= model->cfg.vocab_size) return fail(QE_ERR_ARG, "draft token %u >= vocab", d[i]);
     ids.assign(1, cur);
-    ids.insert(ids.end(), draft.begin(), draft.end());
+    ids.insert(ids.end(), d.begin(), d.begin() + nd);
+    const auto t0 = clock::now();
     if ((rc = verify_greedy(model, ids.data(), uint32_t(ids.size()), pos, kv, got.data()))) return rc;
     // row i is the greedy token after ids[i]: drafts are accepted while they equal it, and the
     // row after the last accepted one adds a token of its own
-    size_t j = 0;
-    while (j < draft.size() && got[j] == draft[j]) j++;
+    uint32_t j = 0;
+    while (j < nd && got[j] == d[j]) j++;
     st.passes++;
-    st.drafted += draft.size();
+    st.drafted += nd;
     st.accepted += j;
-    for (size_t i = 0; i <= j; i++) {
-      const uint32_t tok = i < j ? draft[i] : got[j];
-      h.push_back(tok);
-      if (on_token) on_token(user, tok);
-    }
+    for (uint32_t i = 0; i <= j; i++) emit(i < j ? d[i] : got[j]);
     cur = got[j];
     pos += j + 1;
     emitted += j + 1;
+    if (adaptive) {
+      sum_s += secs(t0, clock::now());
+      sum_tok += double(j + 1);
+      sum_tok2 += double(j + 1) * double(j + 1);
+      if (++passes_seen >= kAdaptMinPasses) {
+        const double n = passes_seen, mean = sum_tok / n;
+        if (step_s > 0) {
+          const double upper = mean + std::sqrt(std::max(0.0, sum_tok2 / n - mean * mean) / n);
+          plain = upper / (sum_s / n) < 1.0 / step_s;
+        } else {
+          plain = mean < kAdaptMarginal;  // time a plain block to compare
+        }
+      }
+    }
   }
   kv->len = start_pos + steps;  // positions past the accepted tokens hold rejected drafts
   if (stats) *stats = st;
   return QE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                     uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
+                     qe_lookup_stats* stats) {
+  if (ngram == 0) return fail(QE_ERR_ARG, "ngram must be >= 1");
+  std::vector<uint32_t> tmp;
+  auto lookup = [&](const std::vector<uint32_t>& h, uint32_t k, uint32_t* out) -> uint32_t {
+    lookup_draft(h, ngram, k, tmp);
+    std::copy(tmp.begin(), tmp.end(), out);
+    return uint32_t(tmp.size());
+  };
+  return decode_drafted(model, context, n_context, first, start_pos, steps, kv, k_max, lookup,
+                        model && model->lookup_adaptive, on_token, user, stats);
+}
+
+int qe_decode_drafted(qe_model* model, const uint32_t* context, uint64_t n_context, uint32_t first, uint64_t start_pos,
+                      uint64_t steps, qe_kv* kv, uint32_t k_max, qe_draft_fn draft, void* draft_user, int adaptive,
+                      qe_on_token on_token, void* user, qe_lookup_stats* stats) {
+  if (!draft) return fail(QE_ERR_ARG, "null draft function");
+  auto source = [&](const std::vector<uint32_t>& h, uint32_t k, uint32_t* out) -> uint32_t {
+    return draft(draft_user, h.data(), h.size(), k, out);
+  };
+  return decode_drafted(model, context, n_context, first, start_pos, steps, kv, k_max, source, adaptive != 0,
+                        on_token, user, stats);
 }
 
 int qe_decode(qe_model* model, uint32_t first, uint64_t start_pos, uint64_t steps, qe_kv* kv, qe_on_token on_token,

@@ -92,6 +92,9 @@ class Config:
 QWEN3_0_6B = Config(1024, 3072, 28, 16, 8, 128, 151936, 1e-6, 1e6, 151645)
 
 ON_TOKEN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_uint32)
+# qe_draft_fn: (user, history, n, k_max, draft_out) -> draft length
+DRAFT_FN = ctypes.CFUNCTYPE(ctypes.c_uint32, ctypes.c_void_p, ctypes.POINTER(ctypes.c_uint32), ctypes.c_uint64,
+                            ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint32))
 
 
 def lookup_draft(history, ngram: int = 3, k_max: int = 4) -> list:
@@ -105,7 +108,7 @@ def lookup_draft(history, ngram: int = 3, k_max: int = 4) -> list:
 
 class _LookupStats(ctypes.Structure):
     _fields_ = [("passes", ctypes.c_uint64), ("drafted", ctypes.c_uint64), ("accepted", ctypes.c_uint64),
-                ("single_steps", ctypes.c_uint64)]
+                ("single_steps", ctypes.c_uint64), ("plain_steps", ctypes.c_uint64)]
 
 _lib = None
 
@@ -189,6 +192,8 @@ def lib() -> ctypes.CDLL:
         "qe_lookup_draft": (u64, [ctypes.POINTER(u32), u64, u32, u32, ctypes.POINTER(u32)]),
         "qe_decode_lookup": (i32, [vp, ctypes.POINTER(u32), u64, u32, u64, u64, vp, u32, u32, ON_TOKEN, vp,
                                    ctypes.POINTER(_LookupStats)]),
+        "qe_decode_drafted": (i32, [vp, ctypes.POINTER(u32), u64, u32, u64, u64, vp, u32, DRAFT_FN, vp, ctypes.c_int,
+                                    ON_TOKEN, vp, ctypes.POINTER(_LookupStats)]),
         "qe_op_gemm_bf16": (i32, [vp, vp, vp, u64, u64, u64, vp]),
         "qe_write_random_checkpoint": (i32, [ctypes.c_char_p, u64, ctypes.POINTER(_CConfig)]),
         "qe_random_prompt": (None, [u64, u64, u32, ctypes.POINTER(u32)]),
@@ -298,7 +303,7 @@ class Model:
                       k_max: int = 4, ngram: int = 3, on_token: Optional[Callable[[int], None]] = None):
         """Greedy decode with prompt-lookup drafts checked by verify passes (qe_decode_lookup): the
         same tokens as decode(). context: the ids before `first` (the prompt). Returns (tokens,
-        stats) with stats = {passes, drafted, accepted, single_steps}."""
+        stats) with stats = {passes, drafted, accepted, single_steps, plain_steps}."""
         toks = []
 
         def cb(_user, tok):
@@ -312,6 +317,39 @@ class Model:
         _check(lib().qe_decode_lookup(self._h, ctx.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ctx),
                                       int(first), int(start_pos), int(steps), cache._h, int(k_max), int(ngram), ccb,
                                       None, ctypes.byref(st)))
+        return toks, {f: int(getattr(st, f)) for f, _ in _LookupStats._fields_}
+
+    def decode_drafted(self, first: int, start_pos: int, steps: int, cache: "KVCache",
+                       draft: Callable[[list, int], list], context=(), k_max: int = 4, adaptive: bool = True,
+                       on_token: Optional[Callable[[int], None]] = None):
+        """decode_lookup with the drafts of draft(history, k_max) -> list of at most k_max tokens
+        (qe_decode_drafted); adaptive: the same rule as decode_lookup's. Returns (tokens, stats)."""
+        toks = []
+        err = []
+
+        def cb(_user, tok):
+            toks.append(int(tok))
+            if on_token is not None:
+                on_token(int(tok))
+
+        def dcb(_user, hist, n, k, out):
+            try:
+                d = [int(t) for t in draft(np.ctypeslib.as_array(hist, shape=(n,)).tolist(), int(k))][:int(k)]
+            except Exception as e:  # an exception cannot cross the C frames: report it afterwards
+                err.append(e)
+                return 0
+            for i, t in enumerate(d):
+                out[i] = t
+            return len(d)
+
+        ccb, cdraft = ON_TOKEN(cb), DRAFT_FN(dcb)
+        ctx = np.ascontiguousarray(context, dtype=np.uint32)
+        st = _LookupStats()
+        _check(lib().qe_decode_drafted(self._h, ctx.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ctx),
+                                       int(first), int(start_pos), int(steps), cache._h, int(k_max), cdraft, None,
+                                       int(bool(adaptive)), ccb, None, ctypes.byref(st)))
+        if err:
+            raise err[0]
         return toks, {f: int(getattr(st, f)) for f, _ in _LookupStats._fields_}
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",

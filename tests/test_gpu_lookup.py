@@ -46,13 +46,67 @@ def test_tiny_lookup_decode_matches_oracle(gpu, tiny_ckpt, k_max, ngram):
         want.append(tok)
     assert got == want
     assert st["accepted"] <= st["drafted"] and st["passes"] + st["single_steps"] >= 1
-    assert st["passes"] + st["single_steps"] + st["accepted"] == steps
+    assert st["passes"] + st["single_steps"] + st["accepted"] + st["plain_steps"] == steps
     assert len(c) == P + steps
     # the cache continues like the oracle's after the rejected drafts
     more, _ = m.decode(got[-1], P + steps, 5, c)
     for i in range(5):
         tok = oracle.argmax(om.forward(tok, P + steps + i, oc))
         assert more[i] == tok
+
+
+@pytest.mark.parametrize("adaptive", [True, False])
+@pytest.mark.parametrize("quality", ["right", "wrong", "every_third"])
+def test_tiny_drafted_decode_matches_plain(gpu, tiny_ckpt, adaptive, quality):
+    """qe_decode_drafted with a caller's draft source: the tokens of plain decode whatever the
+    drafts; with drafts that never pay (always wrong) the adaptive rule decodes plain blocks"""
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(61, 20, TINY.vocab_size)
+    P, steps, k_max = len(prompt), 80, 3
+    c = qe.KVCache(m, P + steps + 8)
+    first = oracle.argmax(m.prefill(prompt, 0, c))
+    want, _ = m.decode(first, P, steps, c)
+    seq = [first] + want
+    calls = [0]
+
+    def draft(hist, k):
+        i = len(hist) - P - 1  # seq index of the last token
+        assert list(hist[P:]) == seq[:i + 1]
+        calls[0] += 1
+        good = quality == "right" or (quality == "every_third" and calls[0] % 3 == 0)
+        return [seq[i + 1 + j] if good else (seq[i + 1 + j] + 1) % TINY.vocab_size for j in range(k)]
+
+    got, st = m.decode_drafted(first, P, steps, c, draft, context=prompt, k_max=k_max, adaptive=adaptive)
+    assert got == want
+    assert st["passes"] + st["single_steps"] + st["accepted"] + st["plain_steps"] == steps
+    assert len(c) == P + steps
+    if quality == "right":
+        assert st["accepted"] == st["drafted"] > 0
+    if quality == "wrong":
+        assert st["accepted"] == 0
+        assert (st["plain_steps"] > 0) == adaptive
+    if not adaptive:
+        assert st["plain_steps"] == 0
+    more, _ = m.decode(got[-1], P + steps, 3, c)  # the cache continues after rejected drafts
+    c2 = qe.KVCache(m, P + steps + 8)
+    m.prefill(prompt, 0, c2, want_logits=False)
+    ref, _ = m.decode(first, P, steps + 3, c2)
+    assert more == ref[steps:]
+
+
+def test_drafted_decode_reports_a_draft_source_error(gpu, tiny_ckpt):
+    m = qe.Model.load_model(tiny_ckpt)
+    prompt = qe.random_prompt(63, 10, TINY.vocab_size)
+    c = qe.KVCache(m, 40)
+    first = oracle.argmax(m.prefill(prompt, 0, c))
+
+    def bad(hist, k):
+        raise ValueError("draft source failed")
+
+    with pytest.raises(ValueError, match="draft source failed"):
+        m.decode_drafted(first, len(prompt), 5, c, bad, context=prompt, k_max=2)
+    with pytest.raises(qe.QeError):  # a draft token outside the vocabulary
+        m.decode_drafted(first, len(prompt), 5, c, lambda h, k: [TINY.vocab_size] * k, context=prompt, k_max=2)
 
 
 @pytest.mark.slow
