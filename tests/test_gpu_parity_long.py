@@ -221,22 +221,24 @@ def test_prefill_prefetch_changes_no_result(gpu, real_ckpt, monkeypatch):
     np.testing.assert_array_equal(on, off)
 
 
-def test_prefill_two_streams_change_no_result(gpu, real_ckpt, monkeypatch):
-    """consecutive chunks alternate between two streams, each chunk's attention ordered after the
-    previous chunk's K/V rows of the same layer: bit-identical logits and cache to one stream
-    (QE_PREFILL_STREAMS=1), here for a prompt that ends in a short chunk"""
+@pytest.mark.parametrize("streams", ["2", "3"])
+def test_prefill_two_streams_change_no_result(gpu, real_ckpt, monkeypatch, streams):
+    """consecutive chunks go round-robin over 2 (the default) or 3 streams, each chunk's attention
+    ordered after the earlier chunks' K/V rows of the same layer: bit-identical logits and cache to
+    one stream (QE_PREFILL_STREAMS=1), here for a prompt that ends in a short chunk"""
     g = load("qwen3_0_6b_prefill2048.npz")
     prompt = g["prompt"].astype(np.uint32)[:1800]
 
     def run():
         m = qe.Model.load_model(real_ckpt)  # QE_PREFILL_STREAMS is read here
         c = qe.KVCache(m, len(prompt) + 4)
-        lg = m.prefill_batch(prompt, 0, c, chunk=512)
+        lg = m.prefill_batch(prompt, 0, c, chunk=256)
         toks, _ = m.decode(oracle.argmax(lg), len(prompt), 4, c)
         return lg, toks
 
-    lg2, t2 = run()
+    monkeypatch.setenv("QE_PREFILL_STREAMS", streams)
+    lgn, tn = run()
     monkeypatch.setenv("QE_PREFILL_STREAMS", "1")
     lg1, t1 = run()
-    np.testing.assert_array_equal(lg2, lg1)
-    assert t2 == t1
+    np.testing.assert_array_equal(lgn, lg1)
+    assert tn == t1
