@@ -1178,8 +1178,11 @@ int qe_prefill_batch(qe_model* model, const uint32_t* ids, uint64_t n, uint64_t 
     }
     last_set = set;
     if ((rc = enqueue_batch(model, kv, M, uint32_t(start_pos + done), model->ids_dev + done, lg, nullptr,
-                            S > 1 ? &cs : nullptr)))
+                            S > 1 ? &cs : nullptr))) {
+      // nothing queued may outlive the call (the caller may free the cache next)
+      for (int j = 0; j < S; j++) (void)hipStreamSynchronize(stream_of(j));
       return rc;
+    }
     done += M;
   }
   for (int j = 1; j < S; j++) HIP_TRY(hipStreamSynchronize(stream_of(j)));
