@@ -10,7 +10,11 @@
 //                         3 launches at each of M x N x K = 2048 x 4096 x 1024 (q|k|v of a
 //                         2048-token chunk: k_gemm_tile), 512 x 6144 x 1024 and 512 x 4096 x 1024
 //                         (gate|up and q|k|v of a 512-token chunk: k_gemm_rows8), for the
-//                         matrix-core counters (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, ...)
+//                         matrix-core counters (SQ_INSTS_MFMA, SQ_VALU_MFMA_BUSY_CYCLES, ...);
+//                         --reps R launches per shape instead of 3, --random fills A and W with
+//                         hashed values in [-1, 1) and [-1/64, 1/64) instead of constants (the
+//                         same work; what changes is how many bits the operands toggle)
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -47,6 +51,23 @@ __global__ void k_fill_f32(float* p, size_t n, float v) {
   for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) p[i] = v;
 }
 
+// p[i] = scale x (a hash of i mapped to [-1, 1)); bf16: the upper halves of such floats
+__device__ __forceinline__ float hash_unit(uint32_t i) {
+  uint32_t h = i * 2654435761u;
+  h ^= h >> 16;
+  h *= 2246822519u;
+  h ^= h >> 13;
+  return float(h >> 8) * (2.0f / 16777216.0f) - 1.0f;
+}
+__global__ void k_fill_hash_f32(float* p, size_t n, float scale) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+    p[i] = scale * hash_unit(uint32_t(i));
+}
+__global__ void k_fill_hash_bf16(uint16_t* p, size_t n, float scale) {
+  for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256)
+    p[i] = uint16_t(__float_as_uint(scale * hash_unit(uint32_t(i) ^ 0x9E3779B9u)) >> 16);
+}
+
 template <typename T>
 T* dalloc(size_t n) {
   T* p = nullptr;
@@ -58,11 +79,14 @@ T* dalloc(size_t n) {
 
 int main(int argc, char** argv) {
   uint32_t pos = 193;
-  bool prefetch = true, gemm = false;
+  bool prefetch = true, gemm = false, random = false;
+  int reps = 3;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
     else if (!strcmp(argv[i], "--no-prefetch")) prefetch = false;
     else if (!strcmp(argv[i], "--gemm")) gemm = true;
+    else if (!strcmp(argv[i], "--random")) random = true;
+    else if (!strcmp(argv[i], "--reps") && i + 1 < argc) reps = std::max(1, atoi(argv[++i]));
   }
   if (gemm) {
     CK(hipSetDevice(0));
@@ -74,16 +98,21 @@ int main(int argc, char** argv) {
       float* A = dalloc<float>(size_t(M) * K);
       uint16_t* W = dalloc<uint16_t>(size_t(N) * K);
       float* C = dalloc<float>(size_t(M) * N);
-      k_fill_f32<<<1024, 256, 0, gs>>>(A, size_t(M) * K, 0.5f);
-      // bf16 pairs (0, 0.0078125): any finite values give the same matrix-core work
-      k_fill_f32<<<1024, 256, 0, gs>>>(reinterpret_cast<float*>(W), size_t(N) * K / 2, 0.0078125f);
+      if (random) {
+        k_fill_hash_f32<<<1024, 256, 0, gs>>>(A, size_t(M) * K, 1.0f);
+        k_fill_hash_bf16<<<1024, 256, 0, gs>>>(W, size_t(N) * K, 1.0f / 64);
+      } else {
+        k_fill_f32<<<1024, 256, 0, gs>>>(A, size_t(M) * K, 0.5f);
+        // bf16 pairs (0, 0.0078125): any finite values give the same matrix-core work
+        k_fill_f32<<<1024, 256, 0, gs>>>(reinterpret_cast<float*>(W), size_t(N) * K / 2, 0.0078125f);
+      }
       const qe::GemmParams g{A, K, nullptr, nullptr, W, M, N, K, C, N, 1e-6f};
-      for (int r = 0; r < 3; r++) CK(qe::launch_gemm(g, false, qe::kGemmStore, gs));
+      for (int r = 0; r < reps; r++) CK(qe::launch_gemm(g, false, qe::kGemmStore, gs));
       CK(hipStreamSynchronize(gs));
       CK(hipFree(A));
       CK(hipFree(W));
       CK(hipFree(C));
-      std::printf("gemm %u x %u x %u: 3 launches\n", M, N, K);
+      std::printf("gemm %u x %u x %u: %d launches%s\n", M, N, K, reps, random ? " (hashed operands)" : "");
     }
     return 0;
   }
