@@ -11,6 +11,7 @@
 
 #include <cmath>
 
+#include "attn_tile.h"
 #include "device_common.h"
 #include "l2_prefetch.h"
 
@@ -36,83 +37,6 @@ namespace {
 // The workgroup writes its (m, l, acc) partial per q head; a run past the last position writes
 // an empty one (m = -inf, l = 0, acc = 0).
 // ---------------------------------------------------------------------------------------------
-template <bool KV_BF16>
-struct KVTile;
-template <>
-struct KVTile<false> {
-  float4 k[2][4];  // scores layout: 2 positions x 16 dims
-  float4 v[8];     // PV layout: 8 positions x 4 dims
-};
-template <>
-struct KVTile<true> {
-  uint4 k[2][2];
-  uint2 v[8];
-};
-
-// component-wise select (a ternary on float4 objects selects between their addresses, which
-// keeps them out of registers)
-__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
-  return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
-}
-
-__device__ __forceinline__ float4 bf16x4(uint32_t a, uint32_t b) {
-  return make_float4(__uint_as_float(a << 16), __uint_as_float(a & 0xFFFF0000u), __uint_as_float(b << 16),
-                     __uint_as_float(b & 0xFFFF0000u));
-}
-
-// K/V rows of positions tile.. in this thread's two layouts; rows past the cache end are clamped
-template <bool KV_BF16>
-__device__ __forceinline__ void load_tile(KVTile<KV_BF16>& X, const AttnParams& p, size_t head_base, uint32_t tile,
-                                          int tid) {
-  constexpr int D = kHeadDim;
-  const uint32_t last = p.max_seq - 1;
-  const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
-#pragma unroll
-  for (int u = 0; u < 2; u++) {
-    const size_t row = head_base + size_t(min(tile + uint32_t(pg + 32 * u), last)) * D + 16 * dc;
-    if constexpr (KV_BF16) {
-      const uint4* src = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.k_cache) + row);
-      X.k[u][0] = src[0];
-      X.k[u][1] = src[1];
-    } else {
-      const float4* src = reinterpret_cast<const float4*>(static_cast<const float*>(p.k_cache) + row);
-#pragma unroll
-      for (int i = 0; i < 4; i++) X.k[u][i] = src[i];
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const size_t row = head_base + size_t(min(tile + uint32_t(8 * pp + i), last)) * D + 4 * dg;
-    if constexpr (KV_BF16) {
-      X.v[i] = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(p.v_cache) + row);
-    } else {
-      X.v[i] = *reinterpret_cast<const float4*>(static_cast<const float*>(p.v_cache) + row);
-    }
-  }
-}
-
-template <bool KV_BF16>
-__device__ __forceinline__ void tile_k(const KVTile<KV_BF16>& X, int u, float4 (&k4)[4]) {
-  if constexpr (KV_BF16) {
-    k4[0] = bf16x4(X.k[u][0].x, X.k[u][0].y);
-    k4[1] = bf16x4(X.k[u][0].z, X.k[u][0].w);
-    k4[2] = bf16x4(X.k[u][1].x, X.k[u][1].y);
-    k4[3] = bf16x4(X.k[u][1].z, X.k[u][1].w);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; i++) k4[i] = X.k[u][i];
-  }
-}
-
-template <bool KV_BF16>
-__device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16>& X, int i) {
-  if constexpr (KV_BF16) {
-    return bf16x4(X.v[i].x, X.v[i].y);
-  } else {
-    return X.v[i];
-  }
-}
-
 template <int G, bool KV_BF16, bool DECODE>
 __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk) {
   if (blockIdx.y >= p.splits) {  // a prefetch workgroup (whole workgroup, before any load)
@@ -168,7 +92,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
   }
   KVTile<KV_BF16> A, B;
-  load_tile<KV_BF16>(A, p, head_base, t0_first, tid);
+  load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, t0_first, tid);
   __builtin_amdgcn_sched_barrier(0);  // keep the scheduler from sinking these loads to their uses
 
   // a run with no cached position (t1 <= t0) goes through one all-masked tile and writes the
@@ -193,7 +117,7 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
     }
     t0 = s * run;
     owns_new = n != 0 && pos >= t0 && pos < t0 + run;
-    if (!p.run && run != T) load_tile<KV_BF16>(A, p, head_base, t0, tid);  // longer runs start elsewhere
+    if (!p.run && run != T) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, t0, tid);  // longer runs start elsewhere
   } else {
     n = p.n_pos_fixed;
     pos = n - 1;
@@ -318,12 +242,12 @@ __global__ __launch_bounds__(256) void k_attn_split(AttnParams p, uint32_t chunk
   // this one is computed (sc / pes / Cs are only rewritten after the next tile's first barrier)
   for (uint32_t tile = t0;; tile += 2 * T) {
     const bool more = tile + T < t1;
-    if (more) load_tile<KV_BF16>(B, p, head_base, tile + T, tid);
+    if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
     __builtin_amdgcn_sched_barrier(0);
     process(A, tile);
     if (!more) break;
     const bool more2 = tile + 2 * T < t1;
-    if (more2) load_tile<KV_BF16>(A, p, head_base, tile + 2 * T, tid);
+    if (more2) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, tile + 2 * T, tid);
     __builtin_amdgcn_sched_barrier(0);
     process(B, tile + T);
     if (!more2) break;

@@ -24,6 +24,7 @@
 
 using qe::ArgCand;
 using qe::AttnParams;
+using qe::FusedLayerParams;
 using qe::MatvecParams;
 using qe::StepState;
 
@@ -119,6 +120,14 @@ struct qe_model {
   uint32_t n_cand = 0;
   float* attn_part = nullptr;
   uint32_t* err = nullptr;  // device error word
+  // two launches per layer (fused.hip) for the Qwen3-0.6B shape, when a launch deals its
+  // workgroups to the XCDs round-robin (checked at load; QE_FUSED=0 keeps one launch per
+  // stage): residual stream
+  // ping-pong buffers, the 8 per-XCD partials of o_proj and of down, and the XCD sync words
+  bool fused = false;
+  float *res0 = nullptr, *res1 = nullptr, *part_attn = nullptr, *part_mlp = nullptr;
+  uint32_t* fsync = nullptr;
+  uint32_t* place_word = nullptr;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -406,7 +415,10 @@ int qe_model_load(const char* path, qe_model** out) {
   const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
                s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
                s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxWideSplits * G * qe::kPartStride * 4),
-               s_err = stake(4);
+               s_err = stake(4), s_res0 = stake(H * 4), s_res1 = stake(H * 4),
+               s_pa = stake(qe::kFusedXcds * H * 4), s_pm = stake(qe::kFusedXcds * H * 4),
+               s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4);
+  static_assert(size_t(qe::kAttnMaxWideSplits) >= qe::kFusedMaxRuns, "fused attention partials fit attn_part");
   HIP_TRY(hipMalloc(&m->scratch, so));
   HIP_TRY(hipMemset(m->scratch, 0, so));
   m->x = reinterpret_cast<float*>(m->scratch + s_x);
@@ -417,6 +429,28 @@ int qe_model_load(const char* path, qe_model** out) {
   m->cand = reinterpret_cast<ArgCand*>(m->scratch + s_cand);
   m->attn_part = reinterpret_cast<float*>(m->scratch + s_part);
   m->err = reinterpret_cast<uint32_t*>(m->scratch + s_err);
+  m->res0 = reinterpret_cast<float*>(m->scratch + s_res0);
+  m->res1 = reinterpret_cast<float*>(m->scratch + s_res1);
+  m->part_attn = reinterpret_cast<float*>(m->scratch + s_pa);
+  m->part_mlp = reinterpret_cast<float*>(m->scratch + s_pm);
+  m->fsync = reinterpret_cast<uint32_t*>(m->scratch + s_sync);
+  m->place_word = reinterpret_cast<uint32_t*>(m->scratch + s_place);
+  const char* fz = getenv("QE_FUSED");
+  if ((!fz || strcmp(fz, "0") != 0) && H == qe::kFusedH && I == qe::kFusedI && D == qe::kHeadDim &&
+      c.num_attention_heads == qe::kFusedHeads && c.num_key_value_heads == qe::kFusedKv) {
+    bool ok = false;
+    uint32_t* host_ids = nullptr;
+    HIP_TRY(hipHostMalloc(&host_ids, qe::kFusedXcds * qe::kFusedSlots * 4, hipHostMallocDefault));
+    hipError_t pe = qe::fused_placement_check(m->place_word, host_ids, &ok, m->stream);
+    if (getenv("QE_FUSED_DEBUG")) {
+      fprintf(stderr, "qe: workgroup -> XCD placement (%s):", ok ? "round-robin" : "NOT round-robin");
+      for (uint32_t i = 0; i < qe::kFusedXcds * qe::kFusedSlots; i++) fprintf(stderr, " %u", host_ids[i]);
+      fprintf(stderr, "\n");
+    }
+    (void)hipHostFree(host_ids);
+    HIP_TRY(pe);
+    m->fused = ok;
+  }
   HIP_TRY(hipHostMalloc(&m->h_logits, V * 4, hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(&m->h_small, 64, hipHostMallocDefault));
   *out = m.release();
@@ -432,6 +466,8 @@ int qe_model_config(const qe_model* model, qe_config* out) {
 }
 
 uint64_t qe_weight_bytes_per_token(const qe_model* model) { return model ? model->weight_bytes : 0; }
+
+int qe_model_fused_layers(const qe_model* model) { return model && model->fused ? 1 : 0; }
 
 void* qe_model_stream(const qe_model* model) { return model ? static_cast<void*>(model->stream) : nullptr; }
 
@@ -451,7 +487,10 @@ namespace {
 // the last), with the stage name of the kernel that follows it.
 // Enqueues one decode step on the model's stream. With `only` set, just the kernels of that
 // stage are enqueued (qe_profile_step times each stage this way); `launches` counts them.
+int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
+
 int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* launches = nullptr) {
+  if (m->fused) return enqueue_step_fused(m, kv, only, launches);
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -532,6 +571,57 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = H; p.out = m->logits; p.cand = m->cand;
+  if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  if (want("argmax")) {
+    HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err,
+                              kv->rope, kv->rope_cur, D / 2, s));
+  }
+  return QE_OK;
+}
+
+// The decode step as two launches per layer (fused.hip): each layer's attention block, then its
+// MLP block; the final reduction of the last layer's partials, the lm_head and the argmax.
+// `only` / `launches` as in enqueue_step, with the stages attn_block, mlp_block, final_reduce,
+// lm_head and argmax.
+int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches) {
+  const qe_config& c = m->cfg;
+  const uint32_t V = uint32_t(c.vocab_size), D = uint32_t(c.head_dim);
+  const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
+  const size_t layer_kv = size_t(c.num_key_value_heads) * kv->max_seq * D * el;
+  hipStream_t s = m->stream;
+  auto want = [&](const char* name) {
+    bool w = !only;
+    const size_t n = strlen(name);
+    for (const char* t = only; t && !w; t = strchr(t, '+') ? strchr(t, '+') + 1 : nullptr)
+      w = strncmp(t, name, n) == 0 && (t[n] == '+' || t[n] == '\0');
+    if (w && launches) ++*launches;
+    return w;
+  };
+  FusedLayerParams f{};
+  f.qkv = m->qkv; f.attn_part = m->attn_part; f.h = m->h;
+  f.embed = m->embed; f.tokens = kv->tokens; f.vocab = V; f.state = kv->state;
+  f.kv_bf16 = kv->dtype == QE_KV_BF16; f.max_seq = uint32_t(kv->max_seq); f.rope_cur = kv->rope_cur;
+  f.splits = kv->step_splits; f.run = kv->step_run;
+  f.eps = c.rms_norm_eps; f.scale = 1.0f / sqrtf(float(D));
+  f.sync = m->fsync; f.err = m->err;
+  for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
+    const Layer& w = m->layers[l];
+    f.w_in = w.w_in; f.w_qkv = w.w_qkv; f.q_norm = w.q_norm; f.k_norm = w.k_norm; f.w_o = w.w_o;
+    f.w_post = w.w_post; f.w_gu = w.w_gu; f.w_down = w.w_down;
+    f.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
+    f.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
+    // attention block: x = res0 + the previous layer's down partials (layer 0: the embedding)
+    f.res_in = m->res0; f.part_in = m->part_mlp; f.res_out = m->res1; f.part_out = m->part_attn;
+    if (want("attn_block")) HIP_TRY(qe::launch_fused_attn(f, l == 0, s));
+    // MLP block: x = res1 + the o_proj partials
+    f.res_in = m->res1; f.part_in = m->part_attn; f.res_out = m->res0; f.part_out = m->part_mlp;
+    if (want("mlp_block")) HIP_TRY(qe::launch_fused_mlp(f, s));
+  }
+  if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, s));
+  MatvecParams p{};
+  p.eps = c.rms_norm_eps;
+  p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = uint32_t(c.hidden_size);
+  p.out = m->logits; p.cand = m->cand;
   if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
   if (want("argmax")) {
     HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err,
@@ -840,6 +930,15 @@ int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
 // attention kernel starts its first K/V tile load at launch instead of after reading pos.
 void step_shape(const qe_kv* kv, uint64_t pos, uint32_t& splits, uint32_t& run) {
   const uint64_t n = pos + 1, S = kv->attn_splits;
+  if (kv->model->fused) {
+    // one run per slot of an XCD: runs of 64 in 4, 8, 16 or 32 up to 64 x 32 positions, then 32
+    // runs of a whole number of tiles
+    const uint64_t R = qe::kFusedMaxRuns;
+    run = uint32_t(64 * ((n + 64 * R - 1) / (64 * R)));
+    const uint64_t active = (n + run - 1) / run;
+    splits = uint32_t(run > 64 ? R : active <= 4 ? 4 : active <= 8 ? 8 : active <= 16 ? 16 : R);
+    return;
+  }
   if (kv->wide_attn && n > 64 * uint64_t(qe::kAttnMaxMergeSplits)) {
     // long context: runs of whole tiles over up to kAttnMaxWideSplits workgroups per KV head,
     // their count rounded up to a multiple of 8 (fewer step graphs; the extra runs are empty).
@@ -996,7 +1095,7 @@ int qe_kv_new(qe_model* model, uint64_t max_seq, int kv_dtype, qe_kv** out) {
     // in o_proj), else the next multiple of 64 (wide runs change their count every 8 runs and
     // their length every 64 kAttnMaxWideSplits positions)
     const bool wide = splits > uint32_t(qe::kAttnMaxMergeSplits);
-    pos = run == 64 || wide ? (pos / 64 + 1) * 64 : uint64_t(run) * kv->attn_splits;
+    pos = run == 64 || wide || model->fused ? (pos / 64 + 1) * 64 : uint64_t(run) * kv->attn_splits;
   }
   if (shapes.size() <= 64) {
     for (const auto& sh : shapes) {
@@ -1051,18 +1150,31 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   // them) up to the lm_head, whose differences are the stages' in-step costs. The argmax, the
   // step's last launch, is not in a prefix: it advances the step state, which the attention
   // launches of a replayed prefix would then follow past the captured position.
-  static const char* const kStages[] = {"qkv",
-                                        "attention",
-                                        "qkv+attention",
-                                        "o_proj",
-                                        "gate_up",
-                                        "down",
-                                        "lm_head",
-                                        "argmax",
-                                        "qkv+attention+o_proj",
-                                        "qkv+attention+o_proj+gate_up",
-                                        "qkv+attention+o_proj+gate_up+down",
-                                        "qkv+attention+o_proj+gate_up+down+lm_head"};
+  static const char* const kStageList[] = {"qkv",
+                                           "attention",
+                                           "qkv+attention",
+                                           "o_proj",
+                                           "gate_up",
+                                           "down",
+                                           "lm_head",
+                                           "argmax",
+                                           "qkv+attention+o_proj",
+                                           "qkv+attention+o_proj+gate_up",
+                                           "qkv+attention+o_proj+gate_up+down",
+                                           "qkv+attention+o_proj+gate_up+down+lm_head",
+                                           nullptr};
+  // the two-launch layers (fused.hip): per layer an attention block and an MLP block
+  static const char* const kFusedStageList[] = {"attn_block",
+                                                "mlp_block",
+                                                "final_reduce",
+                                                "lm_head",
+                                                "argmax",
+                                                "attn_block+mlp_block",
+                                                "attn_block+mlp_block+final_reduce",
+                                                "attn_block+mlp_block+final_reduce+lm_head",
+                                                nullptr};
+  std::vector<const char*> kStages;
+  for (const char* const* st = model->fused ? kFusedStageList : kStageList; *st; st++) kStages.push_back(*st);
   constexpr int kReps = 8;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   HIP_TRY(hipEventCreate(&e0));

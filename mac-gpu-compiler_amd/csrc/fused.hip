@@ -1,0 +1,645 @@
+// Fused decode layer for the Qwen3-0.6B shape (hidden 1024, 16 q heads over 8 KV heads of 128,
+// SwiGLU 3072): two launches per layer instead of one per dependent stage.
+//
+// Reference: cpu_inference.rs:126-172 (one layer of Model::forward), inference.metal:113-346.
+//
+// The MI355X has 8 XCDs, each with its own L2. The workgroups of a launch are dealt to the XCDs
+// round-robin, starting where the previous dispatch left off: workgroup i runs on XCD
+// (start + i) % 8 with a start that varies from launch to launch. So a workgroup takes its XCD x
+// from HW_REG_XCC_ID and its slot from i / 8, which gives each XCD the slots 0..31 whatever the
+// start. The model has 8 KV heads, so XCD x serves KV head x and the slices of the other
+// projections that go with it. Inside one launch the stages of an XCD hand their outputs to each other
+// through that XCD's L2 only:
+//   - a producer stores its outputs (the vector L1 writes through to L2), waits for the stores
+//     (s_waitcnt vmcnt(0)), and stores its flag word (one 128-byte line per workgroup);
+//   - a consumer polls the flags of the workgroups it needs with device-scope loads (sc1, which
+//     miss the vector L1 and read the XCD's L2), then reads the outputs with sc1 loads too.
+// A flag holds the launch's generation tag: every launch reads its XCD's generation word at
+// the start and writes tag = generation + 1, and slot 0 stores tag as the new generation once
+// every workgroup of the XCD has arrived at the first wait (so after all of them read it). Flags
+// are compared for equality, so no reset is needed and the count can wrap.
+// Every wait is bounded: past kSpinMax polls it sets kErrSync and goes on, so no wave waits for
+// ever (a host check at model load runs this path only if a launch deals its workgroups
+// round-robin, and the 256 workgroups of a launch, one per CU, are all resident at once). A
+// placement that broke the slot assignment would leave a slot empty, and the waits for it would
+// end in kErrSync, so it cannot pass silently.
+//
+// What crosses XCDs goes through a launch boundary: o_proj and down are split over the XCDs by
+// input columns (XCD x owns attention heads 2x, 2x+1 and h[384x .. 384x+383]), each XCD writes a
+// partial output vector, and the next launch adds the 8 partials to the residual stream in a
+// fixed order.
+//
+//   attention block (k_fused_attn), workgroup (x, s = slot 0..31):
+//     x = res + sum partials (layer 0: the embedding row) -> RMSNorm -> 16 of XCD x's 512 q|k|v rows
+//     -> [wait: all 32 slots] -> run s of the split attention of KV head x (q/k RMSNorm, RoPE,
+//     K/V append by the run that holds pos) -> [wait: the attention runs] -> merge of the runs
+//     -> 32 rows of o_proj over columns [256x, 256x+256) -> partial x
+//   MLP block (k_fused_mlp):
+//     x = res + sum partials -> RMSNorm -> 24 of XCD x's 768 gate|up rows, silu * up -> 12 of
+//     h[384x..] -> [wait: all 32 slots] -> 32 rows of down over columns [384x, 384x+384) -> partial x
+// Every workgroup issues all of its weight loads (and its first K/V tile) at the start, so HBM
+// streams the whole launch's weights while the dependent chain runs.
+#include <cmath>
+
+#include "attn_tile.h"
+#include "device_common.h"
+#include "kernels.h"
+#include "l2_prefetch.h"
+
+namespace qe {
+namespace {
+
+constexpr uint32_t H = kFusedH, I = kFusedI, D = kHeadDim, NKV = kFusedKv, G = kFusedHeads / kFusedKv;
+constexpr uint32_t QD = kFusedHeads * D, KD = NKV * D;
+constexpr uint32_t NX = kFusedXcds, NS = kFusedSlots;
+constexpr uint32_t kSpinMax = 1u << 16;
+constexpr int kSc1 = 16;  // buffer-load cache policy: device scope (sc1), misses the vector L1
+
+static_assert(NKV == NX, "one KV head per XCD");
+static_assert(G == 2 && H == 1024 && I == 3072, "the launch layouts below are written for these sizes");
+static_assert((G * D + 2 * D) == 16 * NS, "16 q|k|v rows per workgroup");
+static_assert(2 * I / NX == 24 * NS && H == 32 * NS, "24 gate|up rows and 32 o_proj / down rows per workgroup");
+
+__device__ __forceinline__ uint32_t* gen_word(uint32_t* sync, uint32_t x) { return sync + x * kFusedLineWords; }
+__device__ __forceinline__ uint32_t* flag_word(uint32_t* sync, uint32_t phase, uint32_t x, uint32_t slot) {
+  return sync + (NX + (phase * NX + x) * NS + slot) * kFusedLineWords;
+}
+
+// This workgroup's stores that other workgroups of the XCD will read are complete in the L2,
+// then its flag says so.
+__device__ __forceinline__ void arrive(uint32_t* flag, uint32_t tag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until the flags of slots 0..n-1 of XCD x hold tag: lane i of wave 0 polls slot i.
+// Once any wait of the step has run out of spins (kErrSync in the error word, checked every
+// 1024 polls) the others stop waiting too, so a failing step ends within milliseconds.
+__device__ __forceinline__ void wait_flags(uint32_t* sync, uint32_t phase, uint32_t x, uint32_t n, uint32_t tag,
+                                           uint32_t* err) {
+  if (threadIdx.x < 64) {
+    const uint32_t* f = flag_word(sync, phase, x, min(uint32_t(threadIdx.x), n - 1));
+    for (uint32_t spins = 0;; spins++) {
+      const bool ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
+      if (__all(ok)) break;
+      if ((spins & 1023) == 1023 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync))
+        break;
+      if (spins >= kSpinMax) {
+        if (threadIdx.x == 0) atomicOr(err, kErrSync);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// L1-bypassing loads of data another workgroup of this XCD wrote during the launch
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), short(0), int(bytes), 0x00020000);
+}
+__device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, int(byte_off), 0, kSc1));
+}
+__device__ __forceinline__ float4 ld4_l2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, kSc1));
+}
+
+// sum over each aligned group of 16 lanes, returned to all 16
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  v += dpp<0x140>(v);  // row mirror
+  return v;
+}
+
+__device__ __forceinline__ float4 add4(float4 a, float4 b) {
+  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+}
+
+// x[4 tid .. 4 tid + 3] = xin + part[0] + ... + part[7] (a fixed order) into xs; workgroup 0
+// also stores it to res_out. Returns the RMSNorm scale 1 / sqrt(mean(x^2) + eps) of all of x.
+__device__ __forceinline__ float residual_and_scale(float4 xin, const float4 (&xp)[NX], bool add_parts, float* xs,
+                                                    float* res_out, float eps, float* red4) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float4 v = xin;
+  if (add_parts) {
+#pragma unroll
+    for (uint32_t g = 0; g < NX; g++) v = add4(v, xp[g]);
+  }
+  reinterpret_cast<float4*>(xs)[tid] = v;
+  if (blockIdx.x == 0) reinterpret_cast<float4*>(res_out)[tid] = v;
+  const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+  if (lane == 0) red4[wave] = ss;
+  __syncthreads();
+  const float tot = (red4[0] + red4[1]) + (red4[2] + red4[3]);
+  return 1.0f / sqrtf(tot / float(H) + eps);
+}
+
+// the XCD this workgroup runs on (wave-uniform); an id past the 8 XCDs is an error
+__device__ __forceinline__ uint32_t fused_xcd(uint32_t* err) {
+  const uint32_t x = xcc_id();
+  if (x >= NX) {
+    if (threadIdx.x == 0) atomicOr(err, kErrPlace);
+    return x % NX;
+  }
+  return x;
+}
+
+// first q|k|v row of slot s of KV head x: slots 0-15 take 16 rows each of q heads 2x, 2x+1,
+// slots 16-23 of k head x, slots 24-31 of v head x (a slot's 16 rows are consecutive)
+__device__ __forceinline__ uint32_t qkv_row0(uint32_t x, uint32_t s) {
+  return s < 16 ? x * G * D + 16 * s : s < 24 ? QD + x * D + 16 * (s - 16) : QD + KD + x * D + 16 * (s - 24);
+}
+
+// ---------------------------------------------------------------------------------------------
+// attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type.
+// ---------------------------------------------------------------------------------------------
+template <bool FIRST, bool KV_BF16, int SM>
+__global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
+  constexpr uint32_t T = 64;
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t x = fused_xcd(p.err), s = blockIdx.x / NX;
+  const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
+  const uint32_t splits = max(p.splits, 1u);
+  const bool attn = s < splits;  // this workgroup also runs attention run s of KV head x
+
+  __shared__ __align__(16) float xs[H];
+  __shared__ float red4[4];
+  __shared__ __align__(16) float qs[G][D];
+  __shared__ __align__(16) float knew[D];
+  __shared__ __align__(16) float vnew[D];
+  __shared__ float sc[G][T], pes[G][T];
+  __shared__ float Ms[G], Ls[G], Cs[G];
+  __shared__ __align__(16) float red[8][G][D];
+  __shared__ __align__(16) float att[G * D];
+
+  const uint32_t tag = *gen_word(p.sync, x) + 1;
+
+  // ---- every load that does not depend on another workgroup, issued before any use ----
+  // the residual stream (from the previous launch) or the embedding row
+  float4 xin;
+  float4 xp[NX];
+  if constexpr (FIRST) {
+    uint32_t tok = p.tokens[p.state->tok_idx];
+    if (tok >= p.vocab) {
+      if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
+      tok = 0;
+    }
+    const uint2 e = reinterpret_cast<const uint2*>(p.embed + size_t(tok) * H)[tid];
+    xin = bf16x4(e.x, e.y);
+#pragma unroll
+    for (uint32_t g = 0; g < NX; g++) xp[g] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    xin = reinterpret_cast<const float4*>(p.res_in)[tid];
+#pragma unroll
+    for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(p.part_in + g * H)[tid];
+  }
+  // q|k|v: row group = wave, 4 rows of 1024 columns, lane l holds chunks l and l + 64
+  const uint4* Wq = reinterpret_cast<const uint4*>(p.w_qkv);
+  const uint32_t qrow0 = __builtin_amdgcn_readfirstlane(qkv_row0(x, s) + 4 * wave);
+  uint4 wq[4][2];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const uint32_t row = qrow0 + r;
+#pragma unroll
+    for (int k = 0; k < 2; k++) wq[r][k] = Wq[size_t(row) * (H / 8) + lane + 64 * k];
+  }
+  uint4 gin[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) gin[k] = reinterpret_cast<const uint4*>(p.w_in)[lane + 64 * k];
+  // o_proj rows 32 s + 2 rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
+  // t16 and t16 + 16 of the slice
+  const uint32_t rg = tid >> 4, t16 = tid & 15;
+  const uint4* Wo = reinterpret_cast<const uint4*>(p.w_o);
+  uint4 wo[2][2];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) wo[r][k] = Wo[size_t(32 * s + 2 * rg + r) * (QD / 8) + 32 * x + t16 + 16 * k];
+  }
+  // attention inputs: the first K/V tile of the run (the row at pos is not read from it: the
+  // run that holds pos substitutes the new row from LDS), the norm gains, this position's RoPE row
+  const size_t head_base = size_t(x) * p.max_seq * D;
+  KVTile<KV_BF16> A, B;
+  float gqa = 0.f, gqb = 0.f, gka = 0.f, gkb = 0.f;
+  float2 cs = make_float2(0.f, 0.f);
+  if (attn) {
+    load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, s * p.run, tid);
+    gqa = bf16f(p.q_norm[lane]);
+    gqb = bf16f(p.q_norm[lane + 64]);
+    gka = bf16f(p.k_norm[lane]);
+    gkb = bf16f(p.k_norm[lane + 64]);
+    cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- input RMSNorm + this workgroup's 16 q|k|v rows (cpu_inference.rs:129-132) ----
+  {
+    const float rs = residual_and_scale(xin, xp, !FIRST, xs, p.res_out, p.eps, red4);
+    const float4* xs4 = reinterpret_cast<const float4*>(xs);
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t c = lane + 64 * k;
+      float4 a = xs4[2 * c], b = xs4[2 * c + 1];
+      const uint4 g = gin[k];
+      a.x *= __uint_as_float(g.x << 16);
+      a.y *= __uint_as_float(g.x & 0xFFFF0000u);
+      a.z *= __uint_as_float(g.y << 16);
+      a.w *= __uint_as_float(g.y & 0xFFFF0000u);
+      b.x *= __uint_as_float(g.z << 16);
+      b.y *= __uint_as_float(g.z & 0xFFFF0000u);
+      b.z *= __uint_as_float(g.w << 16);
+      b.w *= __uint_as_float(g.w & 0xFFFF0000u);
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[r] = dot8(wq[r][k], a, b, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) acc[r] = wave_sum(acc[r]) * rs;
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < 4; r++) p.qkv[qrow0 + r] = acc[r];
+    }
+  }
+  arrive(flag_word(p.sync, 0, x, s), tag);
+
+  // ---- attention run s of KV head x (cpu_inference.rs:134-162) ----
+  if (attn) {
+    wait_flags(p.sync, 0, x, NS, tag, p.err);
+    // every workgroup of the XCD has read the generation word before arriving
+    if (s == 0 && tid == 0) __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v]; lane l holds dims l, l + 64
+    const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, (QD + 2 * KD) * 4);
+    const uint32_t off = wave < G ? (x * G + wave) * D : wave == G ? QD + x * D : QD + KD + x * D;
+    float a = ld_l2(rq, (off + lane) * 4), b = ld_l2(rq, (off + lane + 64) * 4);
+
+    const uint32_t pos = p.state->pos;
+    const bool bad = pos >= p.max_seq;
+    if (bad && x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
+    uint32_t n = bad ? 0u : pos + 1;
+    const uint32_t run = p.run;
+    if (n > splits * run) {  // the host's runs would skip positions
+      if (x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrShape);
+      n = 0;
+    }
+    const uint32_t t0 = s * run, t1 = min(n, t0 + run);
+    const bool owns_new = n != 0 && pos >= t0 && pos < t0 + run;
+
+    // q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215)
+    if (wave <= G) {
+      const float ss = wave_sum(a * a + b * b);
+      const float scl = 1.0f / sqrtf(ss / float(D) + p.eps);
+      a = a * scl * (wave < G ? gqa : gka);
+      b = b * scl * (wave < G ? gqb : gkb);
+      const float ar = a * cs.x - b * cs.y, br = b * cs.x + a * cs.y;
+      a = ar;
+      b = br;
+    }
+    if (KV_BF16 && wave >= G) {  // attend with the values later steps read back
+      a = bf16f(f32_to_bf16(a));
+      b = bf16f(f32_to_bf16(b));
+    }
+    float* dst = wave < G ? qs[wave] : (wave == G ? knew : vnew);
+    dst[lane] = a;
+    dst[lane + 64] = b;
+    if (tid < G) {
+      Ms[tid] = -INFINITY;
+      Ls[tid] = 0.f;
+    }
+    __syncthreads();
+    if (owns_new) {  // append the new K/V row (cpu_inference.rs:140-141)
+      const size_t slot = head_base + size_t(pos) * D + (tid & (D - 1));
+      const float val = tid < D ? knew[tid] : vnew[tid - D];
+      void* cache = tid < D ? p.k_cache : p.v_cache;
+      if (KV_BF16) static_cast<uint16_t*>(cache)[slot] = f32_to_bf16(val);
+      else static_cast<float*>(cache)[slot] = val;
+    }
+
+    float4 acc[G];
+#pragma unroll
+    for (uint32_t j = 0; j < G; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    auto process = [&](const KVTile<KV_BF16>& X, uint32_t tile) __attribute__((always_inline)) {
+      // scores s_t = (q . k_t) * scale (cpu_inference.rs:144-152); the new position's k is knew
+#pragma unroll
+      for (int u = 0; u < 2; u++) {
+        const uint32_t t = tile + uint32_t(pg + 32 * u);
+        float4 k4[4];
+        tile_k<KV_BF16>(X, u, k4);
+        const bool sub = owns_new && t == pos;
+        const float4* kn = reinterpret_cast<const float4*>(knew) + 4 * dc;
+#pragma unroll
+        for (int i = 0; i < 4; i++) k4[i] = sel4(sub, kn[i], k4[i]);
+        float sv[G];
+#pragma unroll
+        for (uint32_t j = 0; j < G; j++) {
+          const float4* qj = reinterpret_cast<const float4*>(qs[j]) + 4 * dc;
+          float d = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; i++) {
+            const float4 qv = qj[i];
+            d += k4[i].x * qv.x + k4[i].y * qv.y + k4[i].z * qv.z + k4[i].w * qv.w;
+          }
+          sv[j] = sum8(d);
+        }
+        if (dc == 0) {
+#pragma unroll
+          for (uint32_t j = 0; j < G; j++) sc[j][pg + 32 * u] = t < t1 ? sv[j] * p.scale : -INFINITY;
+        }
+      }
+      __syncthreads();
+      // softmax (cpu_inference.rs:217-223) as an online update: running max, rescaled sum
+      if (wave < G) {
+        const uint32_t j = wave;
+        const float xv = sc[j][lane];
+        const float m_old = Ms[j];
+        const float m_new = fmaxf(m_old, wave_max(xv));
+        const float pe = xv == -INFINITY ? 0.f : expf(xv - m_new);
+        const float c = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
+        const float tsum = wave_sum(pe);
+        pes[j][lane] = pe;
+        if (lane == 0) {
+          Ls[j] = Ls[j] * c + tsum;
+          Ms[j] = m_new;
+          Cs[j] = c;
+        }
+      }
+      __syncthreads();
+      // out += p_t * v_t (cpu_inference.rs:153-160); positions past the run add 0
+      float4 v4[8];
+      const float4 vn = reinterpret_cast<const float4*>(vnew)[dg];
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const uint32_t t = tile + uint32_t(8 * pp + i);
+        v4[i] = sel4(owns_new && t == pos, vn, tile_v<KV_BF16>(X, i));
+        v4[i] = sel4(t < t1, v4[i], make_float4(0.f, 0.f, 0.f, 0.f));
+      }
+#pragma unroll
+      for (uint32_t j = 0; j < G; j++) {
+        const float c = Cs[j];
+        float4 o = make_float4(acc[j].x * c, acc[j].y * c, acc[j].z * c, acc[j].w * c);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+          const float pe = pes[j][8 * pp + i];
+          o.x += pe * v4[i].x;
+          o.y += pe * v4[i].y;
+          o.z += pe * v4[i].z;
+          o.w += pe * v4[i].w;
+        }
+        acc[j] = o;
+      }
+    };
+
+    // runs of several tiles alternate between two register sets, so the next tile's loads are
+    // in flight while one is computed (sc / pes / Cs are rewritten only after the next barrier)
+    for (uint32_t tile = t0;; tile += 2 * T) {
+      const bool more = tile + T < t1;
+      if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
+      __builtin_amdgcn_sched_barrier(0);
+      process(A, tile);
+      if (!more) break;
+      const bool more2 = tile + 2 * T < t1;
+      if (more2) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, tile + 2 * T, tid);
+      __builtin_amdgcn_sched_barrier(0);
+      process(B, tile + T);
+      if (!more2) break;
+    }
+
+    // the 8 position groups meet; m and l are the softmax state
+#pragma unroll
+    for (uint32_t j = 0; j < G; j++) reinterpret_cast<float4*>(red[pp][j])[dg] = acc[j];
+    __syncthreads();
+    float* part = p.attn_part + (size_t(x) * kFusedMaxRuns + s) * G * kPartStride;
+    for (uint32_t o = tid; o < G * D; o += 256) {
+      const uint32_t j = o / D, d = o % D;
+      float v = 0.f;
+#pragma unroll
+      for (int q = 0; q < 8; q++) v += red[q][j][d];
+      part[j * kPartStride + 4 + d] = v;
+      if (d == 0) {
+        part[j * kPartStride] = Ms[j];
+        part[j * kPartStride + 1] = Ls[j];
+      }
+    }
+    arrive(flag_word(p.sync, 1, x, s), tag);
+  }
+
+  // ---- merge of the runs (thread: head 2x + (tid >> 7), dim tid & 127), then o_proj ----
+  wait_flags(p.sync, 1, x, splits, tag, p.err);
+  {
+    const __amdgpu_buffer_rsrc_t rp =
+        rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride, kFusedMaxRuns * G * kPartStride * 4);
+    const uint32_t j = tid >> 7, d = tid & 127;
+    float mv[SM], lv[SM], av[SM];
+#pragma unroll
+    for (int u = 0; u < SM; u++) {
+      const uint32_t base = (min(uint32_t(u), splits - 1) * G + j) * kPartStride;
+      mv[u] = ld_l2(rp, base * 4);
+      lv[u] = ld_l2(rp, (base + 1) * 4);
+      av[u] = ld_l2(rp, (base + 4 + d) * 4);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
+    // slots past the last run weigh 0
+    float M = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < SM; u++) M = uint32_t(u) < splits ? fmaxf(M, mv[u]) : M;
+    float L = 0.f, Av = 0.f;
+#pragma unroll
+    for (int u = 0; u < SM; u++) {
+      const float e = (uint32_t(u) < splits && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
+      L += e * lv[u];
+      Av += e * av[u];
+    }
+    att[tid] = Av * (1.0f / L);
+  }
+  __syncthreads();
+  {
+    // o_proj over this XCD's 256 columns (cpu_inference.rs:163-164): the partial of rows
+    // 32 s .. 32 s + 31; the next launch adds the 8 partials and the residual
+    const float4* at4 = reinterpret_cast<const float4*>(att);
+    float oa[2] = {0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t c = t16 + 16 * k;
+      const float4 a = at4[2 * c], b = at4[2 * c + 1];
+#pragma unroll
+      for (int r = 0; r < 2; r++) oa[r] = dot8(wo[r][k], a, b, oa[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) oa[r] = sum16(oa[r]);
+    if (t16 == 0) {
+#pragma unroll
+      for (int r = 0; r < 2; r++) p.part_out[x * H + 32 * s + 2 * rg + r] = oa[r];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// MLP block of one layer (cpu_inference.rs:166-172)
+// ---------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
+  const uint32_t tid = threadIdx.x, lane = tid & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const uint32_t x = fused_xcd(p.err), s = blockIdx.x / NX;
+  __shared__ __align__(16) float xs[H];
+  __shared__ float red4[4];
+
+  const uint32_t tag = *gen_word(p.sync, x) + 1;
+
+  const float4 xin = reinterpret_cast<const float4*>(p.res_in)[tid];
+  float4 xp[NX];
+#pragma unroll
+  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(p.part_in + g * H)[tid];
+  // gate|up: rows 768 x + 24 s + 6 wave + r (pairs (gate_i, up_i) interleaved), lane l holds
+  // chunks l and l + 64
+  const uint4* Wg = reinterpret_cast<const uint4*>(p.w_gu);
+  const uint32_t row0 = (2 * I / NX) * x + 24 * s + 6 * wave;
+  uint4 wg[6][2];
+#pragma unroll
+  for (int r = 0; r < 6; r++) {
+#pragma unroll
+    for (int k = 0; k < 2; k++) wg[r][k] = Wg[size_t(row0 + r) * (H / 8) + lane + 64 * k];
+  }
+  uint4 gp[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) gp[k] = reinterpret_cast<const uint4*>(p.w_post)[lane + 64 * k];
+  // down rows 32 s + 2 rg + r over columns [384 x, 384 x + 384): 16 threads per row, chunks
+  // t16, t16 + 16, t16 + 32 of the slice
+  const uint32_t rg = tid >> 4, t16 = tid & 15;
+  const uint4* Wd = reinterpret_cast<const uint4*>(p.w_down);
+  uint4 wd[2][3];
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+#pragma unroll
+    for (int k = 0; k < 3; k++) wd[r][k] = Wd[size_t(32 * s + 2 * rg + r) * (I / 8) + 48 * x + t16 + 16 * k];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // post_attention_layernorm + gate|up + silu * up (cpu_inference.rs:167-170)
+  {
+    const float rs = residual_and_scale(xin, xp, true, xs, p.res_out, p.eps, red4);
+    const float4* xs4 = reinterpret_cast<const float4*>(xs);
+    float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t c = lane + 64 * k;
+      float4 a = xs4[2 * c], b = xs4[2 * c + 1];
+      const uint4 g = gp[k];
+      a.x *= __uint_as_float(g.x << 16);
+      a.y *= __uint_as_float(g.x & 0xFFFF0000u);
+      a.z *= __uint_as_float(g.y << 16);
+      a.w *= __uint_as_float(g.y & 0xFFFF0000u);
+      b.x *= __uint_as_float(g.z << 16);
+      b.y *= __uint_as_float(g.z & 0xFFFF0000u);
+      b.z *= __uint_as_float(g.w << 16);
+      b.w *= __uint_as_float(g.w & 0xFFFF0000u);
+#pragma unroll
+      for (int r = 0; r < 6; r++) acc[r] = dot8(wg[r][k], a, b, acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 6; r++) acc[r] = wave_sum(acc[r]) * rs;
+    if (lane == 0) {
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        const float gt = acc[2 * i];
+        p.h[(row0 >> 1) + i] = gt / (1.0f + expf(-gt)) * acc[2 * i + 1];
+      }
+    }
+  }
+  arrive(flag_word(p.sync, 2, x, s), tag);
+  wait_flags(p.sync, 2, x, NS, tag, p.err);
+  if (s == 0 && tid == 0) __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+
+  // down over this XCD's 384 columns (cpu_inference.rs:171-172): the partial of rows 32 s ..
+  const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, (I / NX) * 4);
+  float4 ha[3], hb[3];
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+    const uint32_t c = t16 + 16 * k;
+    ha[k] = ld4_l2(rh, c * 32);
+    hb[k] = ld4_l2(rh, c * 32 + 16);
+  }
+  float da[2] = {0.f, 0.f};
+#pragma unroll
+  for (int k = 0; k < 3; k++) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha[k], hb[k], da[r]);
+  }
+#pragma unroll
+  for (int r = 0; r < 2; r++) da[r] = sum16(da[r]);
+  if (t16 == 0) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) p.part_out[x * H + 32 * s + 2 * rg + r] = da[r];
+  }
+}
+
+// x = res + part[0] + ... + part[7]
+__global__ __launch_bounds__(256) void k_fused_reduce(const float* __restrict__ res, const float* __restrict__ part,
+                                                      float* __restrict__ out) {
+  const uint32_t tid = threadIdx.x;
+  float4 v = reinterpret_cast<const float4*>(res)[tid];
+  float4 xp[NX];
+#pragma unroll
+  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part + g * H)[tid];
+#pragma unroll
+  for (uint32_t g = 0; g < NX; g++) v = add4(v, xp[g]);
+  reinterpret_cast<float4*>(out)[tid] = v;
+}
+
+// ids[i] = the XCD workgroup i runs on
+__global__ __launch_bounds__(256) void k_place_check(uint32_t* ids) {
+  if (threadIdx.x == 0) ids[blockIdx.x] = xcc_id();
+}
+
+template <bool FIRST, bool KV_BF16>
+hipError_t launch_attn_sm(const FusedLayerParams& p, hipStream_t s) {
+  const dim3 grid(NX * NS), block(256);
+  if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4>), grid, block, 0, s, p);
+  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8>), grid, block, 0, s, p);
+  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32>), grid, block, 0, s, p);
+  return hipGetLastError();
+}
+
+bool common_ok(const FusedLayerParams& p) { return p.res_out && p.part_out && p.sync && p.err; }
+
+}  // namespace
+
+hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s) {
+  if (!common_ok(p) || !p.w_in || !p.w_qkv || !p.q_norm || !p.k_norm || !p.w_o || !p.qkv || !p.attn_part ||
+      !p.state || !p.k_cache || !p.v_cache || !p.rope_cur || p.max_seq == 0 || p.splits == 0 ||
+      p.splits > kFusedMaxRuns || p.run == 0 || p.run % 64)
+    return hipErrorInvalidValue;
+  if (first_layer ? (!p.embed || !p.tokens || p.vocab == 0) : (!p.res_in || !p.part_in)) return hipErrorInvalidValue;
+  if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true>(p, s) : launch_attn_sm<true, false>(p, s);
+  return p.kv_bf16 ? launch_attn_sm<false, true>(p, s) : launch_attn_sm<false, false>(p, s);
+}
+
+hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s) {
+  if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * NS), dim3(256), 0, s, p);
+  return hipGetLastError();
+}
+
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s) {
+  if (!res || !part || !x) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_fused_reduce, dim3(1), dim3(256), 0, s, res, part, x);
+  return hipGetLastError();
+}
+
+hipError_t fused_placement_check(uint32_t* dev_ids, uint32_t* host_ids, bool* ok, hipStream_t s) {
+  *ok = false;
+  hipLaunchKernelGGL(k_place_check, dim3(NX * NS), dim3(256), 0, s, dev_ids);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpyAsync(host_ids, dev_ids, NX * NS * 4, hipMemcpyDeviceToHost, s);
+  if (e == hipSuccess) e = hipStreamSynchronize(s);
+  if (e != hipSuccess) return e;
+  bool good = host_ids[0] < NX;
+  for (uint32_t i = 0; i < NX * NS; i++) good = good && host_ids[i] == (host_ids[0] + i) % NX;
+  *ok = good;
+  return e;
+}
+
+}  // namespace qe

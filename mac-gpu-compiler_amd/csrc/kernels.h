@@ -26,6 +26,8 @@ enum : uint32_t {
   kErrToken = 2u,     // input token >= vocab
   kErrRing = 4u,      // token ring full
   kErrShape = 8u,     // the decode step's attention runs do not cover pos (a host-side mistake)
+  kErrSync = 16u,     // a fused layer's wait for the workgroups of its XCD ran out of spins
+  kErrPlace = 32u,    // a fused layer's workgroup read an XCD id past the 8 XCDs
 };
 
 // Per-workgroup greedy candidate (value, index); NaN is never a candidate.
@@ -141,5 +143,70 @@ hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logi
                          uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, const float* rope,
                          float* rope_cur, uint32_t half, hipStream_t s);
 hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, hipStream_t s);
+
+// ---- fused decode layer (fused.hip): two launches per layer for the Qwen3-0.6B shape ----
+// One KV head per XCD: the 256 workgroups of a launch are 8 XCDs x 32 slots (workgroup i runs
+// on XCD (start + i) % 8, the start varying from launch to launch; a workgroup reads its XCD from
+// HW_REG_XCC_ID and takes slot i / 8). The stages of a launch hand data to each other only inside one XCD, through its
+// L2 (plain stores, a flag per workgroup, L1-bypassing loads); what crosses XCDs (the o_proj and
+// down outputs, split over the XCDs' column slices) goes to the next launch as 8 partial vectors
+// that it adds to the residual stream.
+constexpr uint32_t kFusedXcds = 8;
+constexpr uint32_t kFusedSlots = 32;     // workgroups per XCD
+constexpr uint32_t kFusedMaxRuns = 32;   // attention runs per KV head (one per slot)
+constexpr uint32_t kFusedH = 1024, kFusedI = 3072, kFusedHeads = 16, kFusedKv = 8;
+// sync words: one generation word per XCD, then 3 flag arrays [phase][xcd][slot], each word on
+// its own 128-byte line
+constexpr uint32_t kFusedLineWords = 32;
+constexpr uint32_t kFusedPhases = 3;
+constexpr size_t kFusedSyncWords = size_t(kFusedXcds) * kFusedLineWords * (1 + kFusedPhases * kFusedSlots);
+
+struct FusedLayerParams {
+  // attention block
+  const uint16_t* w_in;     // input_layernorm gain [H]
+  const uint16_t* w_qkv;    // q_proj | k_proj | v_proj rows [QD + 2 KD][H]
+  const uint16_t* q_norm;   // [D]
+  const uint16_t* k_norm;   // [D]
+  const uint16_t* w_o;      // [H][QD]
+  // MLP block
+  const uint16_t* w_post;   // post_attention_layernorm gain [H]
+  const uint16_t* w_gu;     // gate/up rows interleaved [2I][H]
+  const uint16_t* w_down;   // [H][I]
+  // residual stream: x = res_in + sum_x part_in[x] (part_in null: x = res_in; layer 0 of the
+  // attention block: x = the embedding row of the step's token)
+  const float* res_in;
+  const float* part_in;     // [8][H]
+  float* res_out;           // x, written by workgroup 0 for the next launch
+  float* part_out;          // [8][H]: this launch's o_proj (or down) output, one slice per XCD
+  // exchanged inside one XCD during a launch
+  float* qkv;               // [QD + 2 KD] raw projections
+  float* attn_part;         // [8][kFusedMaxRuns][G][kPartStride]
+  float* h;                 // [I] silu(gate) * up
+  const uint16_t* embed;
+  const uint32_t* tokens;
+  uint32_t vocab;
+  const StepState* state;
+  void* k_cache;            // layer base [8][max_seq][D], f32 or bf16
+  void* v_cache;
+  int kv_bf16;
+  uint32_t max_seq;
+  const float* rope_cur;    // [D/2][2]
+  uint32_t splits, run;     // attention runs per KV head (<= 32) and positions per run
+  float eps, scale;
+  uint32_t* sync;           // kFusedSyncWords words, zeroed once
+  uint32_t* err;
+};
+
+// layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
+// q/k RMSNorm + RoPE + K/V append + attention (split runs) -> merge -> o_proj slice partial
+hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s);
+// layer l's MLP block: residual + partials -> RMSNorm -> gate|up + silu -> down slice partial
+hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
+// x = res + sum of the 8 partials (the last layer's output, before the final norm)
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s);
+// Runs a 256-workgroup kernel whose workgroup i writes the XCD it runs on to dev_ids[i] (256
+// words), copies them to host_ids (pinned, 256 words); *ok = the workgroups were dealt to the 8
+// XCDs round-robin (workgroup i on XCD (start + i) % 8 for some start).
+hipError_t fused_placement_check(uint32_t* dev_ids, uint32_t* host_ids, bool* ok, hipStream_t s);
 
 }  // namespace qe

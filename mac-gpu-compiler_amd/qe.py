@@ -175,6 +175,7 @@ def lib() -> ctypes.CDLL:
         "qe_model_free": (None, [vp]),
         "qe_model_config": (i32, [vp, ctypes.POINTER(_CConfig)]),
         "qe_weight_bytes_per_token": (u64, [vp]),
+        "qe_model_fused_layers": (i32, [vp]),
         "qe_model_stream": (vp, [vp]),
         "qe_kv_bytes_at": (u64, [vp, u64, i32]),
         "qe_kv_new": (i32, [vp, u64, i32, ctypes.POINTER(vp)]),
@@ -240,6 +241,11 @@ class Model:
 
     def weight_bytes_per_token(self) -> int:
         return int(lib().qe_weight_bytes_per_token(self._h))
+
+    def fused_layers(self) -> bool:
+        """True if the decode step runs two launches per layer (an attention block and an MLP
+        block, one KV head per XCD), False if one launch per stage."""
+        return bool(lib().qe_model_fused_layers(self._h))
 
     def stream_handle(self) -> int:
         """The hipStream_t all of this model's work runs on (for external timing events)."""

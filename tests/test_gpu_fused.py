@@ -1,0 +1,112 @@
+"""The two-launch decode layer (attention block + MLP block per layer, one KV head per XCD)
+against the one-launch-per-stage step on the same checkpoint, and against the oracle.
+
+The fused layer splits o_proj and down over the 8 XCDs by input columns and adds the 8 partial
+vectors to the residual stream in the next launch, so its sums are ordered differently from the
+per-stage step's: logits agree to float rounding (bound 1e-3 here, measured ~1e-5), greedy tokens
+exactly. QE_FUSED=0 at model load selects the per-stage step.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+import qe
+from conftest import PROMPT_LEN, PROMPT_SEED
+
+pytestmark = pytest.mark.gpu
+
+# a checkpoint with the real widths (hidden 1024, 16/8 heads of 128, SwiGLU 3072) but 2 layers
+# and a 4096-token vocabulary, so that the oracle runs it in seconds
+NARROW = qe.Config(1024, 3072, 2, 16, 8, 128, 4096, 1e-6, 1e6, 4095)
+NARROW_SEED = 4321
+
+
+@pytest.fixture(scope="module")
+def narrow_ckpt(workdir):
+    return qe.write_random_checkpoint(os.path.join(workdir, "narrow"), NARROW_SEED, NARROW)
+
+
+def load(path, fused: bool):
+    old = os.environ.get("QE_FUSED")
+    os.environ["QE_FUSED"] = "1" if fused else "0"
+    try:
+        return qe.Model.load_model(path)
+    finally:
+        if old is None:
+            del os.environ["QE_FUSED"]
+        else:
+            os.environ["QE_FUSED"] = old
+
+
+def test_fused_path_selected_for_the_qwen3_shape(gpu, narrow_ckpt, tiny_ckpt):
+    assert load(narrow_ckpt, True).fused_layers()
+    assert not load(narrow_ckpt, False).fused_layers()
+    assert not load(tiny_ckpt, True).fused_layers()  # other shapes keep the per-stage step
+
+
+@pytest.mark.parametrize("kv", [qe.QE_KV_F32, qe.QE_KV_BF16])
+def test_fused_decode_matches_oracle_lockstep(gpu, narrow_ckpt, kv):
+    m = load(narrow_ckpt, True)
+    assert m.fused_layers()
+    om = oracle.Model(narrow_ckpt)
+    V = NARROW.vocab_size
+    prompt = qe.random_prompt(5, 40, V)
+    cache = qe.KVCache(m, 400, kv)
+    oc = om.new_cache(bf16=kv == qe.QE_KV_BF16)
+    worst = 0.0
+    for pos, tok in enumerate(prompt):
+        a = om.forward(int(tok), pos, oc)
+        b = m.forward(int(tok), pos, cache)
+        worst = max(worst, float(np.max(np.abs(a - b))))
+        assert oracle.argmax(a) == oracle.argmax(b), f"pos {pos}"
+    first = oracle.argmax(a)
+    steps = 300  # past 256 positions: 4, 8 and 16 attention runs per KV head
+    toks, lg = m.decode(first, len(prompt), steps, cache, want_logits=True)
+    tok = first
+    for i in range(steps):
+        a = om.forward(tok, len(prompt) + i, oc)
+        worst = max(worst, float(np.max(np.abs(a - lg[i]))))
+        assert toks[i] == oracle.argmax(a), f"decode step {i}"
+        tok = toks[i]
+    assert worst < 1e-3, worst
+    print(f"fused lockstep kv={kv}: worst max-abs {worst:.2e}")
+
+
+def test_fused_matches_per_stage_step_long(gpu, narrow_ckpt):
+    """2600 positions: runs of 64 in 4..32 runs, then 32 runs of 128 (past 2048 positions)."""
+    mf, ms = load(narrow_ckpt, True), load(narrow_ckpt, False)
+    assert mf.fused_layers() and not ms.fused_layers()
+    V = NARROW.vocab_size
+    prompt = qe.random_prompt(9, 24, V)
+    out = []
+    for m in (mf, ms):
+        c = qe.KVCache(m, 2700)
+        lg = m.prefill(prompt, 0, c)
+        first = int(np.argmax(lg))
+        toks, _ = m.decode(first, len(prompt), 2600, c)
+        last = m.forward(toks[-1], len(prompt) + 2600, c)
+        out.append((toks, last))
+    assert out[0][0] == out[1][0]
+    assert float(np.max(np.abs(out[0][1] - out[1][1]))) < 1e-3
+
+
+def test_fused_real_model_matches_fixture_tokens(gpu, real_ckpt):
+    """The bench workload on the fused path: 130-token prompt + 128 greedy steps against the
+    oracle's committed run (the per-stage step's own test is test_gpu_parity_real)."""
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qwen3_0_6b_decode.npz"),
+                allow_pickle=False)
+    m = load(real_ckpt, True)
+    assert m.fused_layers()
+    prompt = qe.random_prompt(PROMPT_SEED, PROMPT_LEN, m.config().vocab_size)
+    cache = qe.KVCache(m, PROMPT_LEN + 129)
+    logits = m.prefill(prompt, 0, cache)
+    first = oracle.argmax(logits)
+    toks, lg = m.decode(first, PROMPT_LEN, 128, cache, want_logits=True)
+    got = [first] + toks
+    ref = [int(t) for t in g["tokens"]]
+    assert got == ref[:len(got)]
+    idx = g["sample_idx"]
+    worst = max(float(np.max(np.abs(l[idx] - g["sample_val"][i + 1]))) for i, l in enumerate(lg))
+    assert worst < 1e-2, worst
