@@ -565,22 +565,25 @@ def main():
             stages.setdefault(name, ([], launches))[0].append(us)
     mean_pos = sum(prof_positions) / n_prof
     stage_bytes = qe.stage_bytes(cfg, mean_pos, el)
-    # Each stage's cost inside the step: the step's prefixes (q|k|v; + attention; + o_proj; ...;
-    # + lm_head) are timed as graphs, and a stage costs the difference between the prefix that
-    # ends with it and the one before; the argmax, the step's last launch, is timed alone. The
-    # costs add up to the step, which `reconciliation` compares with the timed decode. The
-    # attention, for example, runs behind the q|k|v launch it reads, as in the step. Each stage
-    # replayed alone (its launches back to back, no producer in front) is reported beside it as
-    # isolated_mean_us.
-    order = ["qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"]
-    prefix_names = ["+".join(order[:i + 1]) for i in range(len(order) - 1)] + ["argmax"]
+    # Each stage's cost inside the step: the step's prefixes (for one launch per stage: q|k|v;
+    # + attention; + o_proj; ...; + lm_head) are timed as graphs, and a stage costs the difference
+    # between the prefix that ends with it and the one before; the argmax (the step's last launch,
+    # which advances the step state and so cannot end a shorter prefix) costs the whole step minus
+    # the prefix that ends with the lm_head. The costs add up to the step, which `reconciliation`
+    # compares with the timed decode. Each stage replayed alone (its launches back to back, no
+    # producer in front) is reported beside it as isolated_mean_us.
+    mode = model.fused_layers()
+    order = {2: ["layers", "lm_head", "argmax"],
+             1: ["attn_block", "mlp_block", "final_reduce", "lm_head", "argmax"]}.get(
+                 mode, ["qkv", "attention", "o_proj", "gate_up", "down", "lm_head", "argmax"])
+    prefix_names = ["+".join(order[:i + 1]) for i in range(len(order) - 1)] + ["step"]
     kernel_table, prev = {}, None
     for name, pref in zip(order, prefix_names):
         if pref not in stages or name not in stages:
             break
         durs, launches = stages[pref]
         tot = [us * launches for us in durs]  # µs per step of the prefix, per profiled position
-        inc = [t - p for t, p in zip(tot, prev)] if prev and name != "argmax" else tot
+        inc = [t - p for t, p in zip(tot, prev)] if prev else tot
         prev = tot
         per_step = stages[name][1]
         mean_us = sum(inc) / len(inc) / per_step
@@ -590,7 +593,7 @@ def main():
                               "us_per_step": round(mean_us * per_step, 2), "isolated_mean_us": round(iso, 3),
                               "bytes_per_launch": int(b),
                               "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
-    pf = qe.prefetch_bytes(cfg, mean_pos, el) if qe.l2_prefetch_enabled() else 0
+    pf = qe.prefetch_bytes(cfg, mean_pos, el) if qe.l2_prefetch_enabled() and mode == 0 else 0
     if "attention" in kernel_table:
         # the gate/up and down weights this launch also pulls into L2 (counted with those stages)
         kernel_table["attention"]["prefetch_bytes"] = int(pf)
@@ -662,6 +665,8 @@ def main():
         "median_ms_per_token": round(sorted(gaps)[len(gaps) // 2] * 1e3, 4) if gaps else None,
         "by_position": by_position(runs[0][1], P, 512) if DS >= 1024 else None,
         "gpu_ms_per_token": round(per_token_gpu_s * 1e3, 4),
+        # 2: one persistent launch for all layers, 1: two launches per layer, 0: one per stage
+        "layer_launches": {2: "persistent", 1: "two per layer", 0: "one per stage"}[mode],
         "weight_bytes_per_token": weight_bytes,
         "parity_vs_oracle_fixture": parity,
     }

@@ -76,10 +76,11 @@ void* qe_model_stream(const qe_model* model);
 uint64_t qe_weight_bytes_per_token(const qe_model* model);
 /* bench.rs:118-119: K and V bytes read at position pos (f32 as in the reference; bf16 halves) */
 uint64_t qe_kv_bytes_at(const qe_model* model, uint64_t pos, int kv_dtype);
-/* 1 if this model's decode step runs two launches per layer (attention block, MLP block, one KV
- * head per XCD; the Qwen3-0.6B shape on a device that deals a launch's workgroups to its XCDs
- * round-robin, unless QE_FUSED=0), 0 if it runs one launch per stage. No reference
- * counterpart: the Metal engine encodes one dispatch per stage (metal_inference.rs:318-387). */
+/* How this model's decode step runs its layers: 2 = all of them in one persistent launch, 1 = two
+ * launches per layer (attention block, MLP block), 0 = one launch per stage. 1 and 2 serve one KV
+ * head per XCD and need the Qwen3-0.6B shape on a device that deals a launch's workgroups to its
+ * XCDs round-robin; QE_FUSED=0, 1 or 2 at model load caps the choice. No reference counterpart:
+ * the Metal engine encodes one dispatch per stage (metal_inference.rs:318-387). */
 int qe_model_fused_layers(const qe_model* model);
 
 /* ---- KV cache: MetalKVCache::new (metal_inference.rs:129-137). One cache per sequence,

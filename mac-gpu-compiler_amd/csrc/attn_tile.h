@@ -66,6 +66,37 @@ __device__ __forceinline__ void load_tile(KVTile<KV_BF16>& X, const void* k_cach
   }
 }
 
+// load_tile through buffer descriptors over one head's K and V regions ([max_seq][D] each, so
+// rows past the cache end read as 0 instead of being clamped): two lane offsets, and the rows'
+// distances as scalar or immediate offsets
+template <bool KV_BF16>
+__device__ __forceinline__ void load_tile_buf(KVTile<KV_BF16>& X, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                              uint32_t tile, int tid) {
+  constexpr uint32_t D = kHeadDim, EL = KV_BF16 ? 2 : 4;
+  const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
+  const uint32_t koff = ((tile + pg) * D + 16 * dc) * EL, voff = ((tile + 8 * pp) * D + 4 * dg) * EL;
+#pragma unroll
+  for (int u = 0; u < 2; u++) {
+    if constexpr (KV_BF16) {
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+        X.k[u][i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, int(koff + 16 * i), int(u * 32 * D * EL), 0));
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        X.k[u][i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rk, int(koff + 16 * i), int(u * 32 * D * EL), 0));
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i++) {
+    if constexpr (KV_BF16) {
+      X.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, int(voff), int(i * D * EL), 0));
+    } else {
+      X.v[i] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rv, int(voff), int(i * D * EL), 0));
+    }
+  }
+}
+
 template <bool KV_BF16>
 __device__ __forceinline__ void tile_k(const KVTile<KV_BF16>& X, int u, float4 (&k4)[4]) {
   if constexpr (KV_BF16) {

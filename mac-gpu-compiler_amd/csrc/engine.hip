@@ -124,10 +124,20 @@ struct qe_model {
   // workgroups to the XCDs round-robin (checked at load; QE_FUSED=0 keeps one launch per
   // stage): residual stream
   // ping-pong buffers, the 8 per-XCD partials of o_proj and of down, and the XCD sync words
-  bool fused = false;
+  int fused = 0;  // 0: one launch per stage, 1: two launches per layer, 2: one persistent launch
   float *res0 = nullptr, *res1 = nullptr, *part_attn = nullptr, *part_mlp = nullptr;
+  // the persistent launch's exchange buffers (pairs): each XCD's gathered residual stream after
+  // the attention and after the MLP, and the per-XCD o_proj and down partials; its generation word
+  uint2 *pxa = nullptr, *pxm = nullptr, *ppa = nullptr, *ppm = nullptr;
+  uint32_t* pgen = nullptr;
+  uint64_t layer_stride = 0;  // bytes between consecutive layers' tensors in the arena
+  uint2 *fqkv = nullptr, *fh = nullptr;  // (value, tag) pairs exchanged inside an XCD
   uint32_t* fsync = nullptr;
   uint32_t* place_word = nullptr;
+  // extra workgroups per XCD of each attention block that load the layer's MLP weights into the
+  // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
+  // and o_proj weights (QE_FUSED_PF_MLP)
+  uint32_t fused_pf_attn = 0, fused_pf_mlp = 0;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -417,8 +427,12 @@ int qe_model_load(const char* path, qe_model** out) {
                s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxWideSplits * G * qe::kPartStride * 4),
                s_err = stake(4), s_res0 = stake(H * 4), s_res1 = stake(H * 4),
                s_pa = stake(qe::kFusedXcds * H * 4), s_pm = stake(qe::kFusedXcds * H * 4),
-               s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4);
-  static_assert(size_t(qe::kAttnMaxWideSplits) >= qe::kFusedMaxRuns, "fused attention partials fit attn_part");
+               s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4),
+               s_fqkv = stake(qe::kFusedQkvPairs * 8), s_fh = stake(qe::kFusedHPairs * 8),
+               s_pxa = stake(qe::kFusedXcds * H * 8), s_pxm = stake(qe::kFusedXcds * H * 8),
+               s_ppa = stake(qe::kFusedXcds * H * 8), s_ppm = stake(qe::kFusedXcds * H * 8), s_pgen = stake(256);
+  static_assert(qe::kFusedPartPairs * 8 <= size_t(qe::kFusedKv) * qe::kAttnMaxWideSplits * 2 * qe::kPartStride * 4,
+                "fused attention partial pairs fit attn_part");
   HIP_TRY(hipMalloc(&m->scratch, so));
   HIP_TRY(hipMemset(m->scratch, 0, so));
   m->x = reinterpret_cast<float*>(m->scratch + s_x);
@@ -435,8 +449,31 @@ int qe_model_load(const char* path, qe_model** out) {
   m->part_mlp = reinterpret_cast<float*>(m->scratch + s_pm);
   m->fsync = reinterpret_cast<uint32_t*>(m->scratch + s_sync);
   m->place_word = reinterpret_cast<uint32_t*>(m->scratch + s_place);
+  m->fqkv = reinterpret_cast<uint2*>(m->scratch + s_fqkv);
+  m->fh = reinterpret_cast<uint2*>(m->scratch + s_fh);
+  m->pxa = reinterpret_cast<uint2*>(m->scratch + s_pxa);
+  m->pxm = reinterpret_cast<uint2*>(m->scratch + s_pxm);
+  m->ppa = reinterpret_cast<uint2*>(m->scratch + s_ppa);
+  m->ppm = reinterpret_cast<uint2*>(m->scratch + s_ppm);
+  m->pgen = reinterpret_cast<uint32_t*>(m->scratch + s_pgen);
+  if (const char* v = getenv("QE_FUSED_PF_ATTN")) m->fused_pf_attn = uint32_t(std::min(std::max(atoi(v), 0), 64));
+  if (const char* v = getenv("QE_FUSED_PF_MLP")) m->fused_pf_mlp = uint32_t(std::min(std::max(atoi(v), 0), 64));
+  // the layers' tensors sit at one stride in the arena (the persistent launch finds layer l's from
+  // layer 0's)
+  m->layer_stride = L > 1 ? lo[1].in - lo[0].in : 0;
+  bool strided = true;
+  for (uint64_t l = 0; l < L; l++) {
+    const LOff& a = lo[l];
+    const size_t d = l * m->layer_stride;
+    strided = strided && a.in == lo[0].in + d && a.qkv == lo[0].qkv + d && a.qn == lo[0].qn + d &&
+              a.kn == lo[0].kn + d && a.o == lo[0].o + d && a.post == lo[0].post + d && a.gu == lo[0].gu + d &&
+              a.d == lo[0].d + d;
+  }
   const char* fz = getenv("QE_FUSED");
-  if ((!fz || strcmp(fz, "0") != 0) && H == qe::kFusedH && I == qe::kFusedI && D == qe::kHeadDim &&
+  // default: two launches per layer (measured 1781-1800 tok/s on the 128-step bench against
+  // 1766 for the persistent launch and 1598 for one launch per stage)
+  const int want_mode = fz ? std::min(std::max(atoi(fz), 0), 2) : 1;
+  if (want_mode > 0 && H == qe::kFusedH && I == qe::kFusedI && D == qe::kHeadDim &&
       c.num_attention_heads == qe::kFusedHeads && c.num_key_value_heads == qe::kFusedKv) {
     bool ok = false;
     uint32_t* host_ids = nullptr;
@@ -449,7 +486,7 @@ int qe_model_load(const char* path, qe_model** out) {
     }
     (void)hipHostFree(host_ids);
     HIP_TRY(pe);
-    m->fused = ok;
+    if (ok) m->fused = want_mode == 2 && strided && L <= 32 ? 2 : 1;
   }
   HIP_TRY(hipHostMalloc(&m->h_logits, V * 4, hipHostMallocDefault));
   HIP_TRY(hipHostMalloc(&m->h_small, 64, hipHostMallocDefault));
@@ -467,7 +504,7 @@ int qe_model_config(const qe_model* model, qe_config* out) {
 
 uint64_t qe_weight_bytes_per_token(const qe_model* model) { return model ? model->weight_bytes : 0; }
 
-int qe_model_fused_layers(const qe_model* model) { return model && model->fused ? 1 : 0; }
+int qe_model_fused_layers(const qe_model* model) { return model ? model->fused : 0; }
 
 void* qe_model_stream(const qe_model* model) { return model ? static_cast<void*>(model->stream) : nullptr; }
 
@@ -488,9 +525,13 @@ namespace {
 // Enqueues one decode step on the model's stream. With `only` set, just the kernels of that
 // stage are enqueued (qe_profile_step times each stage this way); `launches` counts them.
 int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
+int enqueue_step_persist(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
 
 int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* launches = nullptr) {
-  if (m->fused) return enqueue_step_fused(m, kv, only, launches);
+  // the persistent launch addresses a head's K/V region through 32-bit buffer offsets: caches of
+  // more than 2^22 positions take the two-launch step
+  if (m->fused == 2 && kv->max_seq <= (uint64_t(1) << 22)) return enqueue_step_persist(m, kv, only, launches);
+  if (m->fused == 1) return enqueue_step_fused(m, kv, only, launches);
   const qe_config& c = m->cfg;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), V = uint32_t(c.vocab_size);
   const uint32_t D = uint32_t(c.head_dim), QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
@@ -598,26 +639,90 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     return w;
   };
   FusedLayerParams f{};
-  f.qkv = m->qkv; f.attn_part = m->attn_part; f.h = m->h;
+  f.qkv = m->fqkv; f.attn_part = reinterpret_cast<uint2*>(m->attn_part); f.h = m->fh;
   f.embed = m->embed; f.tokens = kv->tokens; f.vocab = V; f.state = kv->state;
   f.kv_bf16 = kv->dtype == QE_KV_BF16; f.max_seq = uint32_t(kv->max_seq); f.rope_cur = kv->rope_cur;
   f.splits = kv->step_splits; f.run = kv->step_run;
   f.eps = c.rms_norm_eps; f.scale = 1.0f / sqrtf(float(D));
   f.sync = m->fsync; f.err = m->err;
+  const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), NX = qe::kFusedXcds;
+  const uint32_t QD = uint32_t(c.num_attention_heads) * D, KD = uint32_t(c.num_key_value_heads) * D;
+  auto bytes = [](const uint16_t* w) { return reinterpret_cast<const uint8_t*>(w); };
+  // prefetch only while a layer's K/V history is under half the prefetched bytes (past that the
+  // attention itself streams from HBM)
+  const double kv_pos_bytes = double(2 * c.num_key_value_heads * D * el);
   for (uint64_t l = 0; l < c.num_hidden_layers; l++) {
     const Layer& w = m->layers[l];
     f.w_in = w.w_in; f.w_qkv = w.w_qkv; f.q_norm = w.q_norm; f.k_norm = w.k_norm; f.w_o = w.w_o;
     f.w_post = w.w_post; f.w_gu = w.w_gu; f.w_down = w.w_down;
     f.k_cache = static_cast<uint8_t*>(kv->k) + l * layer_kv;
     f.v_cache = static_cast<uint8_t*>(kv->v) + l * layer_kv;
-    // attention block: x = res0 + the previous layer's down partials (layer 0: the embedding)
+    // attention block: x = res0 + the previous layer's down partials (layer 0: the embedding);
+    // its extra workgroups load this layer's gate|up rows and down columns of each XCD
     f.res_in = m->res0; f.part_in = m->part_mlp; f.res_out = m->res1; f.part_out = m->part_attn;
+    for (auto& r : f.pf) r = qe::FusedPrefetch{};
+    f.pf_wgs = m->fused_pf_attn;
+    f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
+    f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
+    f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     if (want("attn_block")) HIP_TRY(qe::launch_fused_attn(f, l == 0, s));
-    // MLP block: x = res1 + the o_proj partials
+    // MLP block: x = res1 + the o_proj partials; its extra workgroups load the next layer's q|k|v
+    // rows and o_proj columns of each XCD
     f.res_in = m->res1; f.part_in = m->part_attn; f.res_out = m->res0; f.part_out = m->part_mlp;
+    for (auto& r : f.pf) r = qe::FusedPrefetch{};
+    f.pf_wgs = l + 1 < c.num_hidden_layers ? m->fused_pf_mlp : 0;
+    if (f.pf_wgs) {
+      const Layer& n = m->layers[l + 1];
+      const uint32_t G = QD / KD;
+      f.pf[0] = qe::FusedPrefetch{bytes(n.w_qkv), G * D * H * 2, G * D * H * 2, 0, 1};
+      f.pf[1] = qe::FusedPrefetch{bytes(n.w_qkv) + size_t(QD) * H * 2, D * H * 2, D * H * 2, 0, 1};
+      f.pf[2] = qe::FusedPrefetch{bytes(n.w_qkv) + size_t(QD + KD) * H * 2, D * H * 2, D * H * 2, 0, 1};
+      f.pf[3] = qe::FusedPrefetch{bytes(n.w_o), G * D * 2, G * D * 2, QD * 2, H};
+      f.pf_max_pos = uint32_t(std::min(0.5 * double((QD + 2 * KD + QD) * H * 2) / kv_pos_bytes, double(kv->max_seq)));
+    }
     if (want("mlp_block")) HIP_TRY(qe::launch_fused_mlp(f, s));
   }
   if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, s));
+  MatvecParams p{};
+  p.eps = c.rms_norm_eps;
+  p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = uint32_t(c.hidden_size);
+  p.out = m->logits; p.cand = m->cand;
+  if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  if (want("argmax")) {
+    HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err,
+                              kv->rope, kv->rope_cur, D / 2, s));
+  }
+  return QE_OK;
+}
+
+// The decode step as one persistent launch for all layers (persist.hip), then the lm_head and the
+// argmax. `only` / `launches` as in enqueue_step, with the stages layers, lm_head and argmax.
+int enqueue_step_persist(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches) {
+  const qe_config& c = m->cfg;
+  const uint32_t V = uint32_t(c.vocab_size), D = uint32_t(c.head_dim);
+  hipStream_t s = m->stream;
+  auto want = [&](const char* name) {
+    bool w = !only;
+    const size_t n = strlen(name);
+    for (const char* t = only; t && !w; t = strchr(t, '+') ? strchr(t, '+') + 1 : nullptr)
+      w = strncmp(t, name, n) == 0 && (t[n] == '+' || t[n] == '\0');
+    if (w && launches) ++*launches;
+    return w;
+  };
+  const Layer& w = m->layers[0];
+  qe::PersistParams q{};
+  q.w_in = w.w_in; q.w_qkv = w.w_qkv; q.q_norm = w.q_norm; q.k_norm = w.k_norm; q.w_o = w.w_o;
+  q.w_post = w.w_post; q.w_gu = w.w_gu; q.w_down = w.w_down;
+  q.layer_stride = m->layer_stride; q.n_layers = uint32_t(c.num_hidden_layers);
+  q.embed = m->embed; q.tokens = kv->tokens; q.vocab = V; q.state = kv->state;
+  q.k_cache = kv->k; q.v_cache = kv->v; q.layer_kv = uint64_t(c.num_key_value_heads) * kv->max_seq * D;
+  q.kv_bf16 = kv->dtype == QE_KV_BF16; q.max_seq = uint32_t(kv->max_seq); q.rope_cur = kv->rope_cur;
+  q.splits = kv->step_splits; q.run = kv->step_run;
+  q.eps = c.rms_norm_eps; q.scale = 1.0f / sqrtf(float(D));
+  q.x_out = m->x;
+  q.qkv = m->fqkv; q.attn_part = reinterpret_cast<uint2*>(m->attn_part); q.h = m->fh;
+  q.xa = m->pxa; q.xm = m->pxm; q.part_a = m->ppa; q.part_m = m->ppm; q.gen = m->pgen; q.err = m->err;
+  if (want("layers")) HIP_TRY(qe::launch_decode_persist(q, s));
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = uint32_t(c.hidden_size);
@@ -1173,8 +1278,15 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
                                                 "attn_block+mlp_block+final_reduce",
                                                 "attn_block+mlp_block+final_reduce+lm_head",
                                                 nullptr};
+  // one persistent launch for all layers (persist.hip)
+  static const char* const kPersistStageList[] = {"layers", "lm_head", "argmax", "layers+lm_head", nullptr};
+  // and last the whole step ("step"): the argmax's cost in the step is the step minus the prefix
+  // that ends with the lm_head (it advances the step state, so it cannot end a shorter prefix)
   std::vector<const char*> kStages;
-  for (const char* const* st = model->fused ? kFusedStageList : kStageList; *st; st++) kStages.push_back(*st);
+  for (const char* const* st = model->fused == 2 ? kPersistStageList : model->fused ? kFusedStageList : kStageList; *st;
+       st++)
+    kStages.push_back(*st);
+  kStages.push_back("step");
   constexpr int kReps = 8;
   hipEvent_t e0 = nullptr, e1 = nullptr;
   HIP_TRY(hipEventCreate(&e0));
@@ -1182,13 +1294,21 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   uint32_t n = 0;
   for (const char* stage : kStages) {
     if (he != hipSuccess || rc != QE_OK) break;
-    if (strcmp(stage, "argmax") == 0 && kv->tok_cap < uint32_t(kReps + 3)) continue;
+    const bool full = strcmp(stage, "step") == 0;
+    if ((full || strcmp(stage, "argmax") == 0) && kv->tok_cap < uint32_t(kReps + 3)) continue;
+    if (full) {
+      // its replays run the captured attention shape at positions pos .. pos + kReps
+      uint32_t s0, r0, s1, r1;
+      step_shape(kv, pos, s0, r0);
+      step_shape(kv, std::min<uint64_t>(pos + kReps, kv->max_seq - 1), s1, r1);
+      if (s0 != s1 || r0 != r1 || pos + kReps >= kv->max_seq) continue;
+    }
     if ((rc = set_state(model, kv, token, pos)) != QE_OK) break;
     uint32_t launches = 0;
     hipGraph_t g = nullptr;
     hipGraphExec_t ge = nullptr;
     if ((he = hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal)) != hipSuccess) break;
-    rc = enqueue_step(model, kv, stage, &launches);
+    rc = enqueue_step(model, kv, full ? nullptr : stage, &launches);
     he = hipStreamEndCapture(model->stream, &g);
     if (rc == QE_OK && he == hipSuccess && launches > 0) {
       he = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);

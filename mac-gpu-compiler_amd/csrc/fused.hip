@@ -8,21 +8,22 @@
 // (start + i) % 8 with a start that varies from launch to launch. So a workgroup takes its XCD x
 // from HW_REG_XCC_ID and its slot from i / 8, which gives each XCD the slots 0..31 whatever the
 // start. The model has 8 KV heads, so XCD x serves KV head x and the slices of the other
-// projections that go with it. Inside one launch the stages of an XCD hand their outputs to each other
-// through that XCD's L2 only:
-//   - a producer stores its outputs (the vector L1 writes through to L2), waits for the stores
-//     (s_waitcnt vmcnt(0)), and stores its flag word (one 128-byte line per workgroup);
-//   - a consumer polls the flags of the workgroups it needs with device-scope loads (sc1, which
-//     miss the vector L1 and read the XCD's L2), then reads the outputs with sc1 loads too.
-// A flag holds the launch's generation tag: every launch reads its XCD's generation word at
-// the start and writes tag = generation + 1, and slot 0 stores tag as the new generation once
-// every workgroup of the XCD has arrived at the first wait (so after all of them read it). Flags
-// are compared for equality, so no reset is needed and the count can wrap.
+// projections that go with it.
+//
+// Inside one launch the stages of an XCD hand their outputs to each other through that XCD's L2
+// only, as (value bits, tag) pairs written with one 64-bit store each (the vector L1 writes
+// through to L2). A consumer polls the pairs it needs with device-scope loads (sc1: they miss the
+// vector L1 and read the XCD's L2) until every tag is this launch's; the producer never waits for
+// its stores, so loads it has in flight (weights, K/V) hold nothing up. The tag: every launch
+// reads its XCD's generation word at the start and uses tag = generation + 1; slot 0 stores tag
+// as the new generation at its end, which comes after every workgroup of the XCD has published
+// data with that tag (so after all of them read the word). Tags are compared for equality, so
+// nothing is reset and the count can wrap.
 // Every wait is bounded: past kSpinMax polls it sets kErrSync and goes on, so no wave waits for
 // ever (a host check at model load runs this path only if a launch deals its workgroups
 // round-robin, and the 256 workgroups of a launch, one per CU, are all resident at once). A
-// placement that broke the slot assignment would leave a slot empty, and the waits for it would
-// end in kErrSync, so it cannot pass silently.
+// placement that broke the slot assignment would leave some pairs unwritten, and the waits for
+// them would end in kErrSync, so it cannot pass silently.
 //
 // What crosses XCDs goes through a launch boundary: o_proj and down are split over the XCDs by
 // input columns (XCD x owns attention heads 2x, 2x+1 and h[384x .. 384x+383]), each XCD writes a
@@ -30,21 +31,22 @@
 // fixed order.
 //
 //   attention block (k_fused_attn), workgroup (x, s = slot 0..31):
-//     x = res + sum partials (layer 0: the embedding row) -> RMSNorm -> 16 of XCD x's 512 q|k|v rows
-//     -> [wait: all 32 slots] -> run s of the split attention of KV head x (q/k RMSNorm, RoPE,
-//     K/V append by the run that holds pos) -> [wait: the attention runs] -> merge of the runs
-//     -> 32 rows of o_proj over columns [256x, 256x+256) -> partial x
+//     x = res + sum partials (layer 0: the embedding row) -> RMSNorm -> 16 of XCD x's 512 q|k|v
+//     rows; slots s < splits: run s of the split attention of KV head x (q/k RMSNorm, RoPE, K/V
+//     append by the run that holds pos); o_proj slots (16..31 with up to 16 runs, all 32 with
+//     32): merge of the runs -> 64 (or 32) rows of o_proj over columns [256x, 256x+256) -> partial x
 //   MLP block (k_fused_mlp):
 //     x = res + sum partials -> RMSNorm -> 24 of XCD x's 768 gate|up rows, silu * up -> 12 of
-//     h[384x..] -> [wait: all 32 slots] -> 32 rows of down over columns [384x, 384x+384) -> partial x
-// Every workgroup issues all of its weight loads (and its first K/V tile) at the start, so HBM
-// streams the whole launch's weights while the dependent chain runs.
+//     h[384x..] -> 32 rows of down over columns [384x, 384x+384) -> partial x
+// Weights are loaded at the start of each workgroup (o_proj's once the q|k|v rows are out), and
+// workgroups past the 256 of a launch can load a later launch's weights into the L2 of their XCD.
 #include <cmath>
 
 #include "attn_tile.h"
 #include "device_common.h"
 #include "kernels.h"
 #include "l2_prefetch.h"
+#include "xcd_exchange.h"
 
 namespace qe {
 namespace {
@@ -52,69 +54,13 @@ namespace {
 constexpr uint32_t H = kFusedH, I = kFusedI, D = kHeadDim, NKV = kFusedKv, G = kFusedHeads / kFusedKv;
 constexpr uint32_t QD = kFusedHeads * D, KD = NKV * D;
 constexpr uint32_t NX = kFusedXcds, NS = kFusedSlots;
-constexpr uint32_t kSpinMax = 1u << 16;
-constexpr int kSc1 = 16;  // buffer-load cache policy: device scope (sc1), misses the vector L1
 
 static_assert(NKV == NX, "one KV head per XCD");
 static_assert(G == 2 && H == 1024 && I == 3072, "the launch layouts below are written for these sizes");
 static_assert((G * D + 2 * D) == 16 * NS, "16 q|k|v rows per workgroup");
-static_assert(2 * I / NX == 24 * NS && H == 32 * NS, "24 gate|up rows and 32 o_proj / down rows per workgroup");
+static_assert(2 * I / NX == 24 * NS && H == 32 * NS, "24 gate|up rows and 32 down rows per workgroup");
 
 __device__ __forceinline__ uint32_t* gen_word(uint32_t* sync, uint32_t x) { return sync + x * kFusedLineWords; }
-__device__ __forceinline__ uint32_t* flag_word(uint32_t* sync, uint32_t phase, uint32_t x, uint32_t slot) {
-  return sync + (NX + (phase * NX + x) * NS + slot) * kFusedLineWords;
-}
-
-// This workgroup's stores that other workgroups of the XCD will read are complete in the L2,
-// then its flag says so.
-__device__ __forceinline__ void arrive(uint32_t* flag, uint32_t tag) {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_store(flag, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-
-// Waits until the flags of slots 0..n-1 of XCD x hold tag: lane i of wave 0 polls slot i.
-// Once any wait of the step has run out of spins (kErrSync in the error word, checked every
-// 1024 polls) the others stop waiting too, so a failing step ends within milliseconds.
-__device__ __forceinline__ void wait_flags(uint32_t* sync, uint32_t phase, uint32_t x, uint32_t n, uint32_t tag,
-                                           uint32_t* err) {
-  if (threadIdx.x < 64) {
-    const uint32_t* f = flag_word(sync, phase, x, min(uint32_t(threadIdx.x), n - 1));
-    for (uint32_t spins = 0;; spins++) {
-      const bool ok = __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == tag;
-      if (__all(ok)) break;
-      if ((spins & 1023) == 1023 && (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) & kErrSync))
-        break;
-      if (spins >= kSpinMax) {
-        if (threadIdx.x == 0) atomicOr(err, kErrSync);
-        break;
-      }
-    }
-  }
-  __syncthreads();
-}
-
-// L1-bypassing loads of data another workgroup of this XCD wrote during the launch
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc_of(const void* p, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), short(0), int(bytes), 0x00020000);
-}
-__device__ __forceinline__ float ld_l2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, int(byte_off), 0, kSc1));
-}
-__device__ __forceinline__ float4 ld4_l2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, int(byte_off), 0, kSc1));
-}
-
-// sum over each aligned group of 16 lanes, returned to all 16
-__device__ __forceinline__ float sum16(float v) {
-  v = sum8(v);
-  v += dpp<0x140>(v);  // row mirror
-  return v;
-}
-
-__device__ __forceinline__ float4 add4(float4 a, float4 b) {
-  return make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
-}
 
 // x[4 tid .. 4 tid + 3] = xin + part[0] + ... + part[7] (a fixed order) into xs; workgroup 0
 // also stores it to res_out. Returns the RMSNorm scale 1 / sqrt(mean(x^2) + eps) of all of x.
@@ -135,34 +81,75 @@ __device__ __forceinline__ float residual_and_scale(float4 xin, const float4 (&x
   return 1.0f / sqrtf(tot / float(H) + eps);
 }
 
-// the XCD this workgroup runs on (wave-uniform); an id past the 8 XCDs is an error
-__device__ __forceinline__ uint32_t fused_xcd(uint32_t* err) {
-  const uint32_t x = xcc_id();
-  if (x >= NX) {
-    if (threadIdx.x == 0) atomicOr(err, kErrPlace);
-    return x % NX;
-  }
-  return x;
-}
-
 // first q|k|v row of slot s of KV head x: slots 0-15 take 16 rows each of q heads 2x, 2x+1,
 // slots 16-23 of k head x, slots 24-31 of v head x (a slot's 16 rows are consecutive)
 __device__ __forceinline__ uint32_t qkv_row0(uint32_t x, uint32_t s) {
   return s < 16 ? x * G * D + 16 * s : s < 24 ? QD + x * D + 16 * (s - 16) : QD + KD + x * D + 16 * (s - 24);
 }
 
+// Prefetch workgroup k (of p.pf_wgs on this XCD) loads one word of every 64-byte half line
+// i = k + pf_wgs j of the regions' lines on XCD x, so the lines sit in this XCD's L2 when the
+// later launch's workgroups on XCD x read them; the words only feed a never-taken store.
+__device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32_t x, uint32_t k) {
+  constexpr uint32_t U = 8, SEG = 64;
+  uint32_t per_row[kFusedMaxPrefetch], span[kFusedMaxPrefetch], tot = 0;
+#pragma unroll
+  for (int t = 0; t < kFusedMaxPrefetch; t++) {
+    per_row[t] = p.pf[t].base ? ceil_div(p.pf[t].row_bytes, SEG) : 0;
+    span[t] = per_row[t] * (p.pf[t].base ? p.pf[t].rows : 0);
+    tot += span[t];
+  }
+  if (tot == 0) return;
+  uint32_t hsum = 0;
+  for (uint32_t j0 = 0; (j0 * p.pf_wgs + k) * 256 < tot; j0 += U) {
+    uint32_t v[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      uint32_t i = min(((j0 + u) * p.pf_wgs + k) * 256 + threadIdx.x, tot - 1);
+      uint32_t t = 0;
+#pragma unroll
+      for (int q = 0; q + 1 < kFusedMaxPrefetch; q++) {
+        if (t == uint32_t(q) && i >= span[q]) {
+          i -= span[q];
+          t = q + 1;
+        }
+      }
+      const FusedPrefetch& r = p.pf[t];
+      const uint32_t row = i / per_row[t], seg = i - row * per_row[t];
+      const uint8_t* a = r.base + size_t(x) * r.xcd_bytes + size_t(row) * r.stride + min(seg * SEG, r.row_bytes - 4);
+      v[u] = *reinterpret_cast<const uint32_t*>(a);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) hsum ^= v[u];
+  }
+  if (p.pf_wgs == 0xFFFFFFFFu && hsum == 0x5A5A5A5Au) *p.err = hsum;  // never: keeps the loads
+}
+
 // ---------------------------------------------------------------------------------------------
-// attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type.
+// attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type,
+// MULTI: runs of more than one 64-position tile (only with 32 runs).
 // ---------------------------------------------------------------------------------------------
-template <bool FIRST, bool KV_BF16, int SM>
+template <bool FIRST, bool KV_BF16, int SM, bool MULTI>
 __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
+  static_assert(SM == 32 || !MULTI, "runs of several tiles come with 32 runs");
   constexpr uint32_t T = 64;
+  // o_proj: with up to 16 runs, slots 16..31 take 64 rows each (4 per 16-thread row group), so
+  // the attention runs (slots 0..15) carry no o_proj weights; with 32 runs every slot takes 32
+  constexpr uint32_t ORR = SM <= 16 ? 4 : 2;
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t x = fused_xcd(p.err), s = blockIdx.x / NX;
+  const uint32_t x = fused_xcd(p.err);
+  if (blockIdx.x >= NX * NS) {  // a prefetch workgroup (the whole workgroup)
+    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX);
+    return;
+  }
+  const uint32_t s = blockIdx.x / NX;
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
   const uint32_t splits = max(p.splits, 1u);
   const bool attn = s < splits;  // this workgroup also runs attention run s of KV head x
+  const bool oproj = SM <= 16 ? s >= 16 : true;
+  const uint32_t orow0 = SM <= 16 ? 64 * (s - 16) : 32 * s;
 
   __shared__ __align__(16) float xs[H];
   __shared__ float red4[4];
@@ -173,10 +160,11 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   __shared__ float Ms[G], Ls[G], Cs[G];
   __shared__ __align__(16) float red[8][G][D];
   __shared__ __align__(16) float att[G * D];
+  __shared__ float mw[G][SM], msum[G];  // merge weights of the runs and their sums per head
 
   const uint32_t tag = *gen_word(p.sync, x) + 1;
 
-  // ---- every load that does not depend on another workgroup, issued before any use ----
+  // ---- loads that depend on no other workgroup, issued before any use ----
   // the residual stream (from the previous launch) or the embedding row
   float4 xin;
   float4 xp[NX];
@@ -201,37 +189,24 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   uint4 wq[4][2];
 #pragma unroll
   for (int r = 0; r < 4; r++) {
-    const uint32_t row = qrow0 + r;
 #pragma unroll
-    for (int k = 0; k < 2; k++) wq[r][k] = Wq[size_t(row) * (H / 8) + lane + 64 * k];
+    for (int k = 0; k < 2; k++) wq[r][k] = Wq[size_t(qrow0 + r) * (H / 8) + lane + 64 * k];
   }
   uint4 gin[2];
 #pragma unroll
   for (int k = 0; k < 2; k++) gin[k] = reinterpret_cast<const uint4*>(p.w_in)[lane + 64 * k];
-  // o_proj rows 32 s + 2 rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
+  // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
   const uint32_t rg = tid >> 4, t16 = tid & 15;
   const uint4* Wo = reinterpret_cast<const uint4*>(p.w_o);
-  uint4 wo[2][2];
+  uint4 wo[ORR][2];
+  auto load_wo = [&]() {
 #pragma unroll
-  for (int r = 0; r < 2; r++) {
+    for (uint32_t r = 0; r < ORR; r++) {
 #pragma unroll
-    for (int k = 0; k < 2; k++) wo[r][k] = Wo[size_t(32 * s + 2 * rg + r) * (QD / 8) + 32 * x + t16 + 16 * k];
-  }
-  // attention inputs: the first K/V tile of the run (the row at pos is not read from it: the
-  // run that holds pos substitutes the new row from LDS), the norm gains, this position's RoPE row
-  const size_t head_base = size_t(x) * p.max_seq * D;
-  KVTile<KV_BF16> A, B;
-  float gqa = 0.f, gqb = 0.f, gka = 0.f, gkb = 0.f;
-  float2 cs = make_float2(0.f, 0.f);
-  if (attn) {
-    load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, s * p.run, tid);
-    gqa = bf16f(p.q_norm[lane]);
-    gqb = bf16f(p.q_norm[lane + 64]);
-    gka = bf16f(p.k_norm[lane]);
-    gkb = bf16f(p.k_norm[lane + 64]);
-    cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
-  }
+      for (int k = 0; k < 2; k++) wo[r][k] = Wo[size_t(orow0 + ORR * rg + r) * (QD / 8) + 32 * x + t16 + 16 * k];
+    }
+  };
   __builtin_amdgcn_sched_barrier(0);
 
   // ---- input RMSNorm + this workgroup's 16 q|k|v rows (cpu_inference.rs:129-132) ----
@@ -243,15 +218,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     for (int k = 0; k < 2; k++) {
       const uint32_t c = lane + 64 * k;
       float4 a = xs4[2 * c], b = xs4[2 * c + 1];
-      const uint4 g = gin[k];
-      a.x *= __uint_as_float(g.x << 16);
-      a.y *= __uint_as_float(g.x & 0xFFFF0000u);
-      a.z *= __uint_as_float(g.y << 16);
-      a.w *= __uint_as_float(g.y & 0xFFFF0000u);
-      b.x *= __uint_as_float(g.z << 16);
-      b.y *= __uint_as_float(g.z & 0xFFFF0000u);
-      b.z *= __uint_as_float(g.w << 16);
-      b.w *= __uint_as_float(g.w & 0xFFFF0000u);
+      scale8(a, b, gin[k]);
 #pragma unroll
       for (int r = 0; r < 4; r++) acc[r] = dot8(wq[r][k], a, b, acc[r]);
     }
@@ -259,20 +226,39 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     for (int r = 0; r < 4; r++) acc[r] = wave_sum(acc[r]) * rs;
     if (lane == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) p.qkv[qrow0 + r] = acc[r];
+      for (int r = 0; r < 4; r++) p.qkv[qrow0 + r] = pair(acc[r], tag);
     }
   }
-  arrive(flag_word(p.sync, 0, x, s), tag);
+  // attention inputs, loaded once the q|k|v rows are out (loads complete in issue order, so
+  // loaded earlier they would hold up this workgroup's rows, which every run waits for): the
+  // first K/V tile of the run (the row at pos is not read from it: the run that holds pos
+  // substitutes the new row from LDS), the raw norm gains, this position's RoPE row
+  const size_t head_base = size_t(x) * p.max_seq * D;
+  KVTile<KV_BF16> A;
+  uint16_t gq[2] = {0, 0}, gk[2] = {0, 0};
+  float2 cs = make_float2(0.f, 0.f);
+  if (attn) {
+    load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, s * p.run, tid);
+    gq[0] = p.q_norm[lane];
+    gq[1] = p.q_norm[lane + 64];
+    gk[0] = p.k_norm[lane];
+    gk[1] = p.k_norm[lane + 64];
+    cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+    if (SM > 16) load_wo();
+  }
 
   // ---- attention run s of KV head x (cpu_inference.rs:134-162) ----
-  if (attn) {
-    wait_flags(p.sync, 0, x, NS, tag, p.err);
-    // every workgroup of the XCD has read the generation word before arriving
-    if (s == 0 && tid == 0) __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  auto attention = [&]() __attribute__((always_inline)) {
     // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v]; lane l holds dims l, l + 64
-    const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, (QD + 2 * KD) * 4);
+    const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, uint32_t(kFusedQkvPairs * 8));
     const uint32_t off = wave < G ? (x * G + wave) * D : wave == G ? QD + x * D : QD + KD + x * D;
-    float a = ld_l2(rq, (off + lane) * 4), b = ld_l2(rq, (off + lane + 64) * 4);
+    uint2 qa, qb;
+    for (uint32_t spins = 0;;) {
+      qa = ld_pair(rq, off + lane);
+      qb = ld_pair(rq, off + lane + 64);
+      if (poll_done(qa.y == tag && qb.y == tag, spins, p.err)) break;
+    }
+    float a = __uint_as_float(qa.x), b = __uint_as_float(qb.x);
 
     const uint32_t pos = p.state->pos;
     const bool bad = pos >= p.max_seq;
@@ -290,8 +276,8 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     if (wave <= G) {
       const float ss = wave_sum(a * a + b * b);
       const float scl = 1.0f / sqrtf(ss / float(D) + p.eps);
-      a = a * scl * (wave < G ? gqa : gka);
-      b = b * scl * (wave < G ? gqb : gkb);
+      a = a * scl * bf16f(wave < G ? gq[0] : gk[0]);
+      b = b * scl * bf16f(wave < G ? gq[1] : gk[1]);
       const float ar = a * cs.x - b * cs.y, br = b * cs.x + a * cs.y;
       a = ar;
       b = br;
@@ -391,88 +377,131 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       }
     };
 
-    // runs of several tiles alternate between two register sets, so the next tile's loads are
-    // in flight while one is computed (sc / pes / Cs are rewritten only after the next barrier)
-    for (uint32_t tile = t0;; tile += 2 * T) {
-      const bool more = tile + T < t1;
-      if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
-      __builtin_amdgcn_sched_barrier(0);
-      process(A, tile);
-      if (!more) break;
-      const bool more2 = tile + 2 * T < t1;
-      if (more2) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, tile + 2 * T, tid);
-      __builtin_amdgcn_sched_barrier(0);
-      process(B, tile + T);
-      if (!more2) break;
+    if constexpr (MULTI) {
+      // runs of several tiles alternate between two register sets, so the next tile's loads are
+      // in flight while one is computed (sc / pes / Cs are rewritten only after the next barrier)
+      KVTile<KV_BF16> B;
+      for (uint32_t tile = t0;; tile += 2 * T) {
+        const bool more = tile + T < t1;
+        if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        process(A, tile);
+        if (!more) break;
+        const bool more2 = tile + 2 * T < t1;
+        if (more2) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, tile + 2 * T, tid);
+        __builtin_amdgcn_sched_barrier(0);
+        process(B, tile + T);
+        if (!more2) break;
+      }
+    } else {
+      process(A, t0);
     }
 
-    // the 8 position groups meet; m and l are the softmax state
+    // the 8 position groups meet; m and l are the softmax state; the partial goes out as pairs
 #pragma unroll
     for (uint32_t j = 0; j < G; j++) reinterpret_cast<float4*>(red[pp][j])[dg] = acc[j];
     __syncthreads();
-    float* part = p.attn_part + (size_t(x) * kFusedMaxRuns + s) * G * kPartStride;
-    for (uint32_t o = tid; o < G * D; o += 256) {
-      const uint32_t j = o / D, d = o % D;
+    uint2* part = p.attn_part + (size_t(x) * kFusedMaxRuns + s) * G * kPartStride;
+    {
+      const uint32_t j = tid / D, d = tid % D;  // 256 threads = G x D outputs
       float v = 0.f;
 #pragma unroll
       for (int q = 0; q < 8; q++) v += red[q][j][d];
-      part[j * kPartStride + 4 + d] = v;
+      part[j * kPartStride + 4 + d] = pair(v, tag);
       if (d == 0) {
-        part[j * kPartStride] = Ms[j];
-        part[j * kPartStride + 1] = Ls[j];
+        part[j * kPartStride] = pair(Ms[j], tag);
+        part[j * kPartStride + 1] = pair(Ls[j], tag);
       }
     }
-    arrive(flag_word(p.sync, 1, x, s), tag);
-  }
+  };
 
-  // ---- merge of the runs (thread: head 2x + (tid >> 7), dim tid & 127), then o_proj ----
-  wait_flags(p.sync, 1, x, splits, tag, p.err);
-  {
-    const __amdgpu_buffer_rsrc_t rp =
-        rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride, kFusedMaxRuns * G * kPartStride * 4);
-    const uint32_t j = tid >> 7, d = tid & 127;
-    float mv[SM], lv[SM], av[SM];
+  // ---- merge of the runs, then o_proj ----
+  // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
+  // slots past the last run weigh 0. Wave 0 takes the (m, l) of every run (lane u: head u / SM,
+  // run u % SM) and leaves the weights e_s and the sums in LDS; then thread (head 2x + tid / 128,
+  // dim tid % 128) adds up its acc values.
+  auto merge_oproj = [&]() __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride,
+                                              uint32_t(kFusedMaxRuns * G * kPartStride * 8));
+    if (wave == 0) {
+      const uint32_t jh = min(lane / SM, G - 1), u = lane % SM;
+      const bool live = lane < G * SM && u < splits;
+      const uint32_t base = (min(u, splits - 1) * G + jh) * kPartStride;
+      uint4 ml;  // pairs m, l
+      for (uint32_t spins = 0;;) {
+        ml = ld_pair2(rp, base);
+        if (poll_done(!live || (ml.y == tag && ml.w == tag), spins, p.err)) break;
+      }
+      const float m = live ? __uint_as_float(ml.x) : -INFINITY;
+      float M = m;
 #pragma unroll
-    for (int u = 0; u < SM; u++) {
-      const uint32_t base = (min(uint32_t(u), splits - 1) * G + j) * kPartStride;
-      mv[u] = ld_l2(rp, base * 4);
-      lv[u] = ld_l2(rp, (base + 1) * 4);
-      av[u] = ld_l2(rp, (base + 4 + d) * 4);
+      for (int o = 1; o < SM; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+      const float e = m != -INFINITY ? expf(m - M) : 0.f;
+      float L = e * (live ? __uint_as_float(ml.z) : 0.f);
+#pragma unroll
+      for (int o = 1; o < SM; o <<= 1) L += __shfl_xor(L, o);
+      if (lane < G * SM) {
+        mw[jh][u] = e;
+        if (u == 0) msum[jh] = L;
+      }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
-    // slots past the last run weigh 0
-    float M = -INFINITY;
+    {
+      const uint32_t j = tid >> 7, d = tid & 127;
+      uint2 av[SM];
+      for (uint32_t spins = 0;;) {
+        bool ok = true;
 #pragma unroll
-    for (int u = 0; u < SM; u++) M = uint32_t(u) < splits ? fmaxf(M, mv[u]) : M;
-    float L = 0.f, Av = 0.f;
+        for (int u = 0; u < SM; u++) av[u] = ld_pair(rp, (min(uint32_t(u), splits - 1) * G + j) * kPartStride + 4 + d);
 #pragma unroll
-    for (int u = 0; u < SM; u++) {
-      const float e = (uint32_t(u) < splits && mv[u] != -INFINITY) ? expf(mv[u] - M) : 0.f;
-      L += e * lv[u];
-      Av += e * av[u];
+        for (int u = 0; u < SM; u++) ok = ok && av[u].y == tag;
+        if (poll_done(ok, spins, p.err)) break;
+      }
+      __syncthreads();
+      float Av = 0.f;
+#pragma unroll
+      for (int u = 0; u < SM; u++) Av += uint32_t(u) < splits ? mw[j][u] * __uint_as_float(av[u].x) : 0.f;
+      att[tid] = Av * (1.0f / msum[j]);
     }
-    att[tid] = Av * (1.0f / L);
-  }
-  __syncthreads();
-  {
-    // o_proj over this XCD's 256 columns (cpu_inference.rs:163-164): the partial of rows
-    // 32 s .. 32 s + 31; the next launch adds the 8 partials and the residual
+    __syncthreads();
+    // o_proj over this XCD's 256 columns (cpu_inference.rs:163-164): the partial of rows orow0..;
+    // the next launch adds the 8 partials and the residual
     const float4* at4 = reinterpret_cast<const float4*>(att);
-    float oa[2] = {0.f, 0.f};
+    float oa[ORR];
+#pragma unroll
+    for (uint32_t r = 0; r < ORR; r++) oa[r] = 0.f;
 #pragma unroll
     for (int k = 0; k < 2; k++) {
       const uint32_t c = t16 + 16 * k;
       const float4 a = at4[2 * c], b = at4[2 * c + 1];
 #pragma unroll
-      for (int r = 0; r < 2; r++) oa[r] = dot8(wo[r][k], a, b, oa[r]);
+      for (uint32_t r = 0; r < ORR; r++) oa[r] = dot8(wo[r][k], a, b, oa[r]);
     }
 #pragma unroll
-    for (int r = 0; r < 2; r++) oa[r] = sum16(oa[r]);
+    for (uint32_t r = 0; r < ORR; r++) oa[r] = sum16(oa[r]);
     if (t16 == 0) {
 #pragma unroll
-      for (int r = 0; r < 2; r++) p.part_out[x * H + 32 * s + 2 * rg + r] = oa[r];
+      for (uint32_t r = 0; r < ORR; r++) p.part_out[x * H + orow0 + ORR * rg + r] = oa[r];
     }
+  };
+
+  // Slot 0 stores the new generation when its part of the launch is done: every workgroup of
+  // the XCD has published its q|k|v rows with this tag by then (the attention reads all of them),
+  // so all of them have read the word.
+  if constexpr (SM <= 16) {
+    if (attn) {  // slots 0..15: the attention runs, no o_proj rows
+      attention();
+      if (s == 0 && tid == 0)
+        __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      return;
+    }
+    if (!oproj) return;
+    load_wo();
+    merge_oproj();
+  } else {
+    attention();
+    merge_oproj();
+    if (s == 0 && tid == 0)
+      __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
@@ -482,7 +511,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
 __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const uint32_t x = fused_xcd(p.err), s = blockIdx.x / NX;
+  const uint32_t x = fused_xcd(p.err);
+  if (blockIdx.x >= NX * NS) {  // a prefetch workgroup (the whole workgroup)
+    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX);
+    return;
+  }
+  const uint32_t s = blockIdx.x / NX;
   __shared__ __align__(16) float xs[H];
   __shared__ float red4[4];
 
@@ -495,7 +529,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   // gate|up: rows 768 x + 24 s + 6 wave + r (pairs (gate_i, up_i) interleaved), lane l holds
   // chunks l and l + 64
   const uint4* Wg = reinterpret_cast<const uint4*>(p.w_gu);
-  const uint32_t row0 = (2 * I / NX) * x + 24 * s + 6 * wave;
+  const uint32_t row0 = __builtin_amdgcn_readfirstlane((2 * I / NX) * x + 24 * s + 6 * wave);
   uint4 wg[6][2];
 #pragma unroll
   for (int r = 0; r < 6; r++) {
@@ -526,15 +560,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
     for (int k = 0; k < 2; k++) {
       const uint32_t c = lane + 64 * k;
       float4 a = xs4[2 * c], b = xs4[2 * c + 1];
-      const uint4 g = gp[k];
-      a.x *= __uint_as_float(g.x << 16);
-      a.y *= __uint_as_float(g.x & 0xFFFF0000u);
-      a.z *= __uint_as_float(g.y << 16);
-      a.w *= __uint_as_float(g.y & 0xFFFF0000u);
-      b.x *= __uint_as_float(g.z << 16);
-      b.y *= __uint_as_float(g.z & 0xFFFF0000u);
-      b.z *= __uint_as_float(g.w << 16);
-      b.w *= __uint_as_float(g.w & 0xFFFF0000u);
+      scale8(a, b, gp[k]);
 #pragma unroll
       for (int r = 0; r < 6; r++) acc[r] = dot8(wg[r][k], a, b, acc[r]);
     }
@@ -544,28 +570,37 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
 #pragma unroll
       for (int i = 0; i < 3; i++) {
         const float gt = acc[2 * i];
-        p.h[(row0 >> 1) + i] = gt / (1.0f + expf(-gt)) * acc[2 * i + 1];
+        p.h[(row0 >> 1) + i] = pair(gt / (1.0f + expf(-gt)) * acc[2 * i + 1], tag);
       }
     }
   }
-  arrive(flag_word(p.sync, 2, x, s), tag);
-  wait_flags(p.sync, 2, x, NS, tag, p.err);
-  if (s == 0 && tid == 0) __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 
   // down over this XCD's 384 columns (cpu_inference.rs:171-172): the partial of rows 32 s ..
-  const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, (I / NX) * 4);
-  float4 ha[3], hb[3];
+  const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, (I / NX) * 8);
+  uint4 hv[3][4];  // chunk t16 + 16 k: h pairs 8 c .. 8 c + 7, two per load
+  for (uint32_t spins = 0;;) {
+    bool ok = true;
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
-    const uint32_t c = t16 + 16 * k;
-    ha[k] = ld4_l2(rh, c * 32);
-    hb[k] = ld4_l2(rh, c * 32 + 16);
+    for (int k = 0; k < 3; k++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) hv[k][q] = ld_pair2(rh, 8 * (t16 + 16 * k) + 2 * q);
+    }
+#pragma unroll
+    for (int k = 0; k < 3; k++) {
+#pragma unroll
+      for (int q = 0; q < 4; q++) ok = ok && hv[k][q].y == tag && hv[k][q].w == tag;
+    }
+    if (poll_done(ok, spins, p.err)) break;
   }
   float da[2] = {0.f, 0.f};
 #pragma unroll
   for (int k = 0; k < 3; k++) {
+    const float4 ha = make_float4(__uint_as_float(hv[k][0].x), __uint_as_float(hv[k][0].z),
+                                  __uint_as_float(hv[k][1].x), __uint_as_float(hv[k][1].z));
+    const float4 hb = make_float4(__uint_as_float(hv[k][2].x), __uint_as_float(hv[k][2].z),
+                                  __uint_as_float(hv[k][3].x), __uint_as_float(hv[k][3].z));
 #pragma unroll
-    for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha[k], hb[k], da[r]);
+    for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha, hb, da[r]);
   }
 #pragma unroll
   for (int r = 0; r < 2; r++) da[r] = sum16(da[r]);
@@ -573,6 +608,10 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
 #pragma unroll
     for (int r = 0; r < 2; r++) p.part_out[x * H + 32 * s + 2 * rg + r] = da[r];
   }
+  // every workgroup of the XCD has published its h values with this tag (the down rows need all
+  // of them), so all of them have read the generation word
+  if (s == 0 && tid == 0)
+    __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // x = res + part[0] + ... + part[7]
@@ -595,22 +634,28 @@ __global__ __launch_bounds__(256) void k_place_check(uint32_t* ids) {
 
 template <bool FIRST, bool KV_BF16>
 hipError_t launch_attn_sm(const FusedLayerParams& p, hipStream_t s) {
-  const dim3 grid(NX * NS), block(256);
-  if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4>), grid, block, 0, s, p);
-  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8>), grid, block, 0, s, p);
-  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32>), grid, block, 0, s, p);
+  const dim3 grid(NX * (NS + p.pf_wgs)), block(256);
+  if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false>), grid, block, 0, s, p);
+  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false>), grid, block, 0, s, p);
+  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false>), grid, block, 0, s, p);
+  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 
-bool common_ok(const FusedLayerParams& p) { return p.res_out && p.part_out && p.sync && p.err; }
+bool common_ok(const FusedLayerParams& p) {
+  if (!p.res_out || !p.part_out || !p.sync || !p.err || !p.state || p.pf_wgs > 64) return false;
+  for (const FusedPrefetch& r : p.pf)
+    if (r.base && (r.row_bytes < 4 || r.rows == 0)) return false;
+  return true;
+}
 
 }  // namespace
 
 hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s) {
   if (!common_ok(p) || !p.w_in || !p.w_qkv || !p.q_norm || !p.k_norm || !p.w_o || !p.qkv || !p.attn_part ||
-      !p.state || !p.k_cache || !p.v_cache || !p.rope_cur || p.max_seq == 0 || p.splits == 0 ||
-      p.splits > kFusedMaxRuns || p.run == 0 || p.run % 64)
+      !p.k_cache || !p.v_cache || !p.rope_cur || p.max_seq == 0 || p.splits == 0 || p.splits > kFusedMaxRuns ||
+      (p.splits > 16 && p.splits != kFusedMaxRuns) || (p.splits <= 16 && p.run != 64) || p.run == 0 || p.run % 64)
     return hipErrorInvalidValue;
   if (first_layer ? (!p.embed || !p.tokens || p.vocab == 0) : (!p.res_in || !p.part_in)) return hipErrorInvalidValue;
   if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true>(p, s) : launch_attn_sm<true, false>(p, s);
@@ -619,7 +664,7 @@ hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStr
 
 hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s) {
   if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * NS), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p);
   return hipGetLastError();
 }
 

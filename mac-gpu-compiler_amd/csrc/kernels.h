@@ -147,19 +147,29 @@ hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_
 // ---- fused decode layer (fused.hip): two launches per layer for the Qwen3-0.6B shape ----
 // One KV head per XCD: the 256 workgroups of a launch are 8 XCDs x 32 slots (workgroup i runs
 // on XCD (start + i) % 8, the start varying from launch to launch; a workgroup reads its XCD from
-// HW_REG_XCC_ID and takes slot i / 8). The stages of a launch hand data to each other only inside one XCD, through its
-// L2 (plain stores, a flag per workgroup, L1-bypassing loads); what crosses XCDs (the o_proj and
-// down outputs, split over the XCDs' column slices) goes to the next launch as 8 partial vectors
-// that it adds to the residual stream.
+// HW_REG_XCC_ID and takes slot i / 8). The stages of a launch hand data to each other only inside
+// one XCD, through its L2, as (value, tag) pairs; what crosses XCDs (the o_proj and down outputs,
+// split over the XCDs' column slices) goes to the next launch as 8 partial vectors that it adds
+// to the residual stream.
 constexpr uint32_t kFusedXcds = 8;
 constexpr uint32_t kFusedSlots = 32;     // workgroups per XCD
 constexpr uint32_t kFusedMaxRuns = 32;   // attention runs per KV head (one per slot)
 constexpr uint32_t kFusedH = 1024, kFusedI = 3072, kFusedHeads = 16, kFusedKv = 8;
-// sync words: one generation word per XCD, then 3 flag arrays [phase][xcd][slot], each word on
-// its own 128-byte line
+// generation words: one per XCD, each on its own 128-byte line
 constexpr uint32_t kFusedLineWords = 32;
-constexpr uint32_t kFusedPhases = 3;
-constexpr size_t kFusedSyncWords = size_t(kFusedXcds) * kFusedLineWords * (1 + kFusedPhases * kFusedSlots);
+constexpr size_t kFusedSyncWords = size_t(kFusedXcds) * kFusedLineWords;
+// exchange buffers, in (value, tag) pairs
+constexpr size_t kFusedQkvPairs = size_t(kFusedHeads + 2 * kFusedKv) * kHeadDim;
+constexpr size_t kFusedPartPairs = size_t(kFusedKv) * kFusedMaxRuns * (kFusedHeads / kFusedKv) * kPartStride;
+constexpr size_t kFusedHPairs = kFusedI;
+
+// A region of weights that extra workgroups of a launch load into the L2 of each XCD for a later
+// launch: on XCD x the rows [0, rows) of row_bytes bytes at base + x * xcd_bytes + r * stride.
+struct FusedPrefetch {
+  const uint8_t* base;
+  uint32_t xcd_bytes, row_bytes, stride, rows;
+};
+constexpr int kFusedMaxPrefetch = 4;
 
 struct FusedLayerParams {
   // attention block
@@ -172,16 +182,16 @@ struct FusedLayerParams {
   const uint16_t* w_post;   // post_attention_layernorm gain [H]
   const uint16_t* w_gu;     // gate/up rows interleaved [2I][H]
   const uint16_t* w_down;   // [H][I]
-  // residual stream: x = res_in + sum_x part_in[x] (part_in null: x = res_in; layer 0 of the
-  // attention block: x = the embedding row of the step's token)
+  // residual stream: x = res_in + sum_x part_in[x] (layer 0 of the attention block: x = the
+  // embedding row of the step's token)
   const float* res_in;
   const float* part_in;     // [8][H]
   float* res_out;           // x, written by workgroup 0 for the next launch
   float* part_out;          // [8][H]: this launch's o_proj (or down) output, one slice per XCD
-  // exchanged inside one XCD during a launch
-  float* qkv;               // [QD + 2 KD] raw projections
-  float* attn_part;         // [8][kFusedMaxRuns][G][kPartStride]
-  float* h;                 // [I] silu(gate) * up
+  // exchanged inside one XCD during a launch, as (value bits, tag) pairs
+  uint2* qkv;               // [kFusedQkvPairs] raw projections
+  uint2* attn_part;         // [kFusedPartPairs]: [8][kFusedMaxRuns][G][kPartStride]
+  uint2* h;                 // [kFusedHPairs] silu(gate) * up
   const uint16_t* embed;
   const uint32_t* tokens;
   uint32_t vocab;
@@ -193,8 +203,12 @@ struct FusedLayerParams {
   const float* rope_cur;    // [D/2][2]
   uint32_t splits, run;     // attention runs per KV head (<= 32) and positions per run
   float eps, scale;
-  uint32_t* sync;           // kFusedSyncWords words, zeroed once
+  uint32_t* sync;           // kFusedSyncWords generation words, zeroed once
   uint32_t* err;
+  // pf_wgs extra workgroups per XCD load the pf regions into its L2 (at positions below
+  // pf_max_pos; pf_wgs = 0: none)
+  FusedPrefetch pf[kFusedMaxPrefetch];
+  uint32_t pf_wgs, pf_max_pos;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
@@ -204,6 +218,39 @@ hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStr
 hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
 // x = res + sum of the 8 partials (the last layer's output, before the final norm)
 hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s);
+// ---- the decode step's layers in one persistent launch (persist.hip), same shape ----
+struct PersistParams {
+  // layer 0's tensors; layer l's are layer_stride bytes further on
+  const uint16_t *w_in, *w_qkv, *q_norm, *k_norm, *w_o, *w_post, *w_gu, *w_down;
+  uint64_t layer_stride;
+  uint32_t n_layers;       // at most 32
+  const uint16_t* embed;
+  const uint32_t* tokens;
+  uint32_t vocab;
+  const StepState* state;
+  void* k_cache;           // layer 0's [8][max_seq][D], f32 or bf16; layer l at + l * layer_kv elements
+  void* v_cache;
+  uint64_t layer_kv;
+  int kv_bf16;
+  uint32_t max_seq;
+  const float* rope_cur;   // [D/2][2]
+  uint32_t splits, run;    // attention runs per KV head (4, 8, 16 of 64 positions, or 32) and their length
+  float eps, scale;
+  float* x_out;            // [H] the last layer's output (the residual stream before the final norm)
+  // (value, tag) pairs: inside an XCD
+  uint2* qkv;              // [kFusedQkvPairs]
+  uint2* attn_part;        // [kFusedPartPairs]
+  uint2* h;                // [kFusedHPairs]
+  uint2* xa;               // [8][H] each XCD's gathered residual stream after the attention
+  uint2* xm;               // [8][H] ... after the MLP
+  // across XCDs
+  uint2* part_a;           // [8][H] o_proj partials
+  uint2* part_m;           // [8][H] down partials
+  uint32_t* gen;           // one word, zeroed once
+  uint32_t* err;
+};
+hipError_t launch_decode_persist(const PersistParams& p, hipStream_t s);
+
 // Runs a 256-workgroup kernel whose workgroup i writes the XCD it runs on to dev_ids[i] (256
 // words), copies them to host_ids (pinned, 256 words); *ok = the workgroups were dealt to the 8
 // XCDs round-robin (workgroup i on XCD (start + i) % 8 for some start).

@@ -134,7 +134,7 @@ def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> dict:
     pulls into L2 (prefetch_bytes) are counted with the gate_up and down stages, which read them."""
     H, I, V = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size
     QD, KD = cfg.num_attention_heads * cfg.head_dim, cfg.num_key_value_heads * cfg.head_dim
-    return {
+    st = {
         "embed": H * 2 + H * 4,
         "qkv": (QD + 2 * KD) * H * 2 + H * 2 + H * 4 + (QD + 2 * KD) * 4,
         "attention": 2 * KD * (mean_pos + 1) * kv_el + (QD + 2 * KD) * 4 + QD * 4,
@@ -144,6 +144,15 @@ def stage_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> dict:
         "lm_head": V * H * 2 + H * 2 + H * 4 + V * 4,
         "argmax": 8 * ((V + 15) // 16),
     }
+    # the fused decode layers (QE_FUSED=1: attention block and MLP block per layer; 2: one launch
+    # for all layers), counted as the stages they contain; the residual stream's partials travel
+    # between launches (8 partial vectors of H floats, read with the residual)
+    parts = 8 * H * 4 + H * 4
+    st["attn_block"] = st["qkv"] + st["attention"] + st["o_proj"] + parts
+    st["mlp_block"] = st["gate_up"] + st["down"] + parts
+    st["final_reduce"] = parts + H * 4
+    st["layers"] = cfg.num_hidden_layers * (st["qkv"] + st["attention"] + st["o_proj"] + st["gate_up"] + st["down"])
+    return st
 
 
 def prefetch_bytes(cfg: Config, mean_pos: float, kv_el: int = 4) -> int:
@@ -242,10 +251,11 @@ class Model:
     def weight_bytes_per_token(self) -> int:
         return int(lib().qe_weight_bytes_per_token(self._h))
 
-    def fused_layers(self) -> bool:
-        """True if the decode step runs two launches per layer (an attention block and an MLP
-        block, one KV head per XCD), False if one launch per stage."""
-        return bool(lib().qe_model_fused_layers(self._h))
+    def fused_layers(self) -> int:
+        """How the decode step runs its layers: 2 = one persistent launch for all of them, 1 = two
+        launches per layer (attention block, MLP block; one KV head per XCD), 0 = one launch per
+        stage."""
+        return int(lib().qe_model_fused_layers(self._h))
 
     def stream_handle(self) -> int:
         """The hipStream_t all of this model's work runs on (for external timing events)."""

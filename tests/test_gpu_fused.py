@@ -1,10 +1,11 @@
-"""The two-launch decode layer (attention block + MLP block per layer, one KV head per XCD)
-against the one-launch-per-stage step on the same checkpoint, and against the oracle.
+"""The decode step with fused layers against the one-launch-per-stage step on the same checkpoint,
+and against the oracle. Two forms (QE_FUSED at model load): 1 = two launches per layer (attention
+block, MLP block), 2 = one persistent launch for all layers; both serve one KV head per XCD.
 
-The fused layer splits o_proj and down over the 8 XCDs by input columns and adds the 8 partial
-vectors to the residual stream in the next launch, so its sums are ordered differently from the
-per-stage step's: logits agree to float rounding (bound 1e-3 here, measured ~1e-5), greedy tokens
-exactly. QE_FUSED=0 at model load selects the per-stage step.
+The fused layers split o_proj and down over the 8 XCDs by input columns and add the 8 partial
+vectors to the residual stream, so their sums are ordered differently from the per-stage step's:
+logits agree to float rounding (bound 1e-3 here, measured ~1e-5), greedy tokens exactly.
+QE_FUSED=0 selects the per-stage step.
 """
 import os
 
@@ -21,6 +22,7 @@ pytestmark = pytest.mark.gpu
 # and a 4096-token vocabulary, so that the oracle runs it in seconds
 NARROW = qe.Config(1024, 3072, 2, 16, 8, 128, 4096, 1e-6, 1e6, 4095)
 NARROW_SEED = 4321
+MODES = [1, 2]
 
 
 @pytest.fixture(scope="module")
@@ -28,9 +30,9 @@ def narrow_ckpt(workdir):
     return qe.write_random_checkpoint(os.path.join(workdir, "narrow"), NARROW_SEED, NARROW)
 
 
-def load(path, fused: bool):
+def load(path, mode: int):
     old = os.environ.get("QE_FUSED")
-    os.environ["QE_FUSED"] = "1" if fused else "0"
+    os.environ["QE_FUSED"] = str(mode)
     try:
         return qe.Model.load_model(path)
     finally:
@@ -41,15 +43,16 @@ def load(path, fused: bool):
 
 
 def test_fused_path_selected_for_the_qwen3_shape(gpu, narrow_ckpt, tiny_ckpt):
-    assert load(narrow_ckpt, True).fused_layers()
-    assert not load(narrow_ckpt, False).fused_layers()
-    assert not load(tiny_ckpt, True).fused_layers()  # other shapes keep the per-stage step
+    for mode in (0, 1, 2):
+        assert load(narrow_ckpt, mode).fused_layers() == mode
+    assert load(tiny_ckpt, 2).fused_layers() == 0  # other shapes keep the per-stage step
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize("kv", [qe.QE_KV_F32, qe.QE_KV_BF16])
-def test_fused_decode_matches_oracle_lockstep(gpu, narrow_ckpt, kv):
-    m = load(narrow_ckpt, True)
-    assert m.fused_layers()
+def test_fused_decode_matches_oracle_lockstep(gpu, narrow_ckpt, kv, mode):
+    m = load(narrow_ckpt, mode)
+    assert m.fused_layers() == mode
     om = oracle.Model(narrow_ckpt)
     V = NARROW.vocab_size
     prompt = qe.random_prompt(5, 40, V)
@@ -71,13 +74,14 @@ def test_fused_decode_matches_oracle_lockstep(gpu, narrow_ckpt, kv):
         assert toks[i] == oracle.argmax(a), f"decode step {i}"
         tok = toks[i]
     assert worst < 1e-3, worst
-    print(f"fused lockstep kv={kv}: worst max-abs {worst:.2e}")
+    print(f"fused mode {mode} lockstep kv={kv}: worst max-abs {worst:.2e}")
 
 
-def test_fused_matches_per_stage_step_long(gpu, narrow_ckpt):
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_matches_per_stage_step_long(gpu, narrow_ckpt, mode):
     """2600 positions: runs of 64 in 4..32 runs, then 32 runs of 128 (past 2048 positions)."""
-    mf, ms = load(narrow_ckpt, True), load(narrow_ckpt, False)
-    assert mf.fused_layers() and not ms.fused_layers()
+    mf, ms = load(narrow_ckpt, mode), load(narrow_ckpt, 0)
+    assert mf.fused_layers() == mode and ms.fused_layers() == 0
     V = NARROW.vocab_size
     prompt = qe.random_prompt(9, 24, V)
     out = []
@@ -92,13 +96,14 @@ def test_fused_matches_per_stage_step_long(gpu, narrow_ckpt):
     assert float(np.max(np.abs(out[0][1] - out[1][1]))) < 1e-3
 
 
-def test_fused_real_model_matches_fixture_tokens(gpu, real_ckpt):
-    """The bench workload on the fused path: 130-token prompt + 128 greedy steps against the
-    oracle's committed run (the per-stage step's own test is test_gpu_parity_real)."""
+@pytest.mark.parametrize("mode", MODES)
+def test_fused_real_model_matches_fixture_tokens(gpu, real_ckpt, mode):
+    """The bench workload: 130-token prompt + 128 greedy steps against the oracle's committed run
+    (the per-stage step's own test is test_gpu_parity_real)."""
     g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "qwen3_0_6b_decode.npz"),
                 allow_pickle=False)
-    m = load(real_ckpt, True)
-    assert m.fused_layers()
+    m = load(real_ckpt, mode)
+    assert m.fused_layers() == mode
     prompt = qe.random_prompt(PROMPT_SEED, PROMPT_LEN, m.config().vocab_size)
     cache = qe.KVCache(m, PROMPT_LEN + 129)
     logits = m.prefill(prompt, 0, cache)
