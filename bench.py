@@ -219,14 +219,15 @@ def sweep_matvec(torch, qe, ceiling: float, repeats: int):
 
 def sweep_attention(torch, qe, ceiling: float, repeats: int):
     """The isolated decode attention (16 q heads, 8 KV heads, head_dim 128) over L cached
-    positions, f32 q/K/V ~ N(0, 1); buffers rotate past the MALL for L <= 8192. Split into runs
+    positions, f32 q/K/V ~ N(0, 1); launches rotate over at least two K/V copies worth at least
+    twice the 256 MB MALL, so every figure is an HBM one (tests/read_bandwidth.rs:139-140). Split into runs
     of 64 positions (the default) and single-pass (one workgroup per KV head).
     Bytes = 8192 L (K and V) + 2 * 16 * 128 * 4 (q in, out)."""
     rows = []
     n_heads, n_kv, D = 16, 8, 128
     for L in (128, 512, 2048, 8192, 32768):
         kvbytes = 2 * n_kv * L * D * 4
-        copies = max(1, -(-2 * MALL_BYTES // kvbytes)) if L <= 8192 else 1
+        copies = max(2, -(-2 * MALL_BYTES // kvbytes))
         K = torch.randn(copies, n_kv, L, D, device="cuda")
         V = torch.randn(copies, n_kv, L, D, device="cuda")
         q = torch.randn(n_heads * D, device="cuda")

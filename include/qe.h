@@ -157,7 +157,10 @@ int qe_decode_lookup(qe_model* model, const uint32_t* context, uint64_t n_contex
                      uint64_t steps, qe_kv* kv, uint32_t k_max, uint32_t ngram, qe_on_token on_token, void* user,
                      qe_lookup_stats* stats);
 /* A draft source: writes up to k_max tokens that are to follow history[0..n) (context, first and
- * the tokens emitted so far) to draft_out and returns their count (0: no draft). */
+ * the tokens emitted so far) to draft_out and returns their count (0: no draft), or
+ * QE_DRAFT_ERROR when it fails: the decode then stops before another pass and returns QE_ERR_ARG,
+ * with the tokens emitted so far delivered and the cache valid up to the next position. */
+#define QE_DRAFT_ERROR 0xFFFFFFFFu
 typedef uint32_t (*qe_draft_fn)(void* user, const uint32_t* history, uint64_t n, uint32_t k_max, uint32_t* draft_out);
 /* qe_decode_lookup with the drafts of `draft` (a draft model, another lookup rule, ...) instead
  * of prompt lookup, and the adaptive rule on when adaptive != 0. No reference counterpart. */
@@ -224,7 +227,9 @@ int qe_op_attention(const float* q, const float* k, const float* v, float* out, 
  * HIP graph capture, serving loops that forbid hipMalloc). Same arguments and results as
  * qe_op_attention; calls with n_heads x runs above 2048 (runs = n_splits, or n_pos / 64 rounded
  * up, at most 128) are refused with QE_ERR_ARG. Every call on one GPU shares that GPU's array, so
- * calls that overlap on one GPU (two streams or two threads) race. */
+ * calls that overlap on one GPU (two streams or two threads) race. The first call on each device
+ * looks up the array's device address (hipGetSymbolAddress, which may load the library's device
+ * code): make it outside stream capture; later calls may be captured into a graph. */
 int qe_op_attention_static(const float* q, const float* k, const float* v, float* out, uint64_t n_pos,
                            uint64_t kv_stride, uint64_t n_heads, uint64_t n_kv_heads, uint32_t n_splits,
                            void* stream);

@@ -1586,7 +1586,12 @@ int decode_drafted(qe_model* model, const uint32_t* context, uint64_t n_context,
     }
     // a pass emits accepted drafts + 1 token, so it never runs past `steps`
     const uint32_t kk = uint32_t(std::min<uint64_t>(k_max, steps - emitted - 1));
-    const uint32_t nd = kk ? std::min(draft(h, kk, d.data()), kk) : 0u;
+    const uint32_t nr = kk ? draft(h, kk, d.data()) : 0u;
+    if (nr == QE_DRAFT_ERROR) {
+      kv->len = pos;  // positions before pos hold the emitted sequence; the next one is cur's
+      return fail(QE_ERR_ARG, "the draft function reported an error after %llu tokens", (unsigned long long)emitted);
+    }
+    const uint32_t nd = std::min(nr, kk);
     if (nd == 0) {  // nothing to verify: one decode step
       uint32_t tok = 0;
       auto keep = [](void* u, uint32_t t) { *static_cast<uint32_t*>(u) = t; };

@@ -24,7 +24,8 @@ constexpr uint32_t kStaticAttnRows = 2048;
 static __device__ __align__(256) float scratch[size_t(kStaticAttnRows) * qe::kPartStride];
 
 // `scratch` names the array in host code but is not its device address: kernels get the address
-// hipGetSymbolAddress returns on each device, looked up once per device with it current.
+// hipGetSymbolAddress returns on each device, looked up once per device with it current, on the
+// first call there (which therefore must not be under stream capture; later calls launch only).
 constexpr int kMaxDevices = 64;
 std::mutex g_mu;
 float* g_ptr[kMaxDevices] = {};

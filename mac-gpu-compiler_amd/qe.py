@@ -33,6 +33,7 @@ QE_ERR_UNSUPPORTED = 6
 QE_ERR_HIP = 7
 QE_ERR_NO_DEVICE = 8
 QE_ERR_KERNEL = 9
+QE_DRAFT_ERROR = 0xFFFFFFFF  # a draft callback's failure return (qe_draft_fn)
 
 QE_KV_F32 = 0
 QE_KV_BF16 = 1
@@ -351,9 +352,9 @@ class Model:
         def dcb(_user, hist, n, k, out):
             try:
                 d = [int(t) for t in draft(np.ctypeslib.as_array(hist, shape=(n,)).tolist(), int(k))][:int(k)]
-            except Exception as e:  # an exception cannot cross the C frames: report it afterwards
+            except Exception as e:  # an exception cannot cross the C frames: stop the decode, raise it after
                 err.append(e)
-                return 0
+                return QE_DRAFT_ERROR
             for i, t in enumerate(d):
                 out[i] = t
             return len(d)
@@ -361,11 +362,12 @@ class Model:
         ccb, cdraft = ON_TOKEN(cb), DRAFT_FN(dcb)
         ctx = np.ascontiguousarray(context, dtype=np.uint32)
         st = _LookupStats()
-        _check(lib().qe_decode_drafted(self._h, ctx.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ctx),
-                                       int(first), int(start_pos), int(steps), cache._h, int(k_max), cdraft, None,
-                                       int(bool(adaptive)), ccb, None, ctypes.byref(st)))
+        rc = lib().qe_decode_drafted(self._h, ctx.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)), len(ctx),
+                                     int(first), int(start_pos), int(steps), cache._h, int(k_max), cdraft, None,
+                                     int(bool(adaptive)), ccb, None, ctypes.byref(st))
         if err:
             raise err[0]
+        _check(rc)
         return toks, {f: int(getattr(st, f)) for f, _ in _LookupStats._fields_}
 
     def decode(self, first: int, start_pos: int, steps: int, cache: "KVCache",

@@ -146,6 +146,29 @@ def test_tiny_prefill_batch_continues_a_cache(gpu, tiny_ckpt):
     assert len(cache) == 150
 
 
+@pytest.mark.parametrize("chunk", [64, 128])
+def test_tiny_prefill_streams_change_no_result(gpu, tiny_ckpt, monkeypatch, chunk):
+    """chunks of more than 32 tokens go round-robin over QE_PREFILL_STREAMS streams, each chunk's
+    attention ordered after the earlier chunks' K/V rows of the same layer: with 2, 3 and 4
+    streams over ten or five GEMM-path chunks (and a short tail) the last token's logits equal one
+    stream's bit for bit, and decoding from the filled cache gives the same tokens"""
+    prompt = qe.random_prompt(71, 600, TINY.vocab_size)
+
+    def run(streams):
+        monkeypatch.setenv("QE_PREFILL_STREAMS", streams)
+        m = qe.Model.load_model(tiny_ckpt)  # QE_PREFILL_STREAMS is read here
+        c = qe.KVCache(m, len(prompt) + 8)
+        lg = m.prefill_batch(prompt, 0, c, chunk=chunk)
+        toks, _ = m.decode(oracle.argmax(lg), len(prompt), 6, c)
+        return lg, toks
+
+    lg1, t1 = run("1")
+    for streams in ("2", "3", "4"):
+        lgn, tn = run(streams)
+        np.testing.assert_array_equal(lgn, lg1, err_msg=f"{streams} streams")
+        assert tn == t1, f"{streams} streams"
+
+
 def test_batch_argument_errors(gpu, tiny_ckpt):
     m = qe.Model.load_model(tiny_ckpt)
     cache = qe.KVCache(m, 8)

@@ -82,7 +82,7 @@ def run_attention(q, k_pm, v_pm, n_heads, n_kv, n_splits, stride_pad=3):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("n_pos", [1, 2, 5, 16, 17, 64, 129, 258, 500, 2048, 8192, 32768])
+@pytest.mark.parametrize("n_pos", [1, 2, 5, 16, 17, 64, 128, 129, 258, 500, 512, 2048, 8192, 32768])
 @pytest.mark.parametrize("n_splits", [0, 1, 7, 128])
 def test_attention_matches_oracle(gpu, n_pos, n_splits):
     # runs of 1..n_pos positions: one 64-position tile or many per workgroup, runs past the last

@@ -100,11 +100,21 @@ def test_drafted_decode_reports_a_draft_source_error(gpu, tiny_ckpt):
     c = qe.KVCache(m, 40)
     first = oracle.argmax(m.prefill(prompt, 0, c))
 
-    def bad(hist, k):
-        raise ValueError("draft source failed")
+    P = len(prompt)
+    calls, emitted = [0], []
+
+    def bad(hist, k):  # drafts nothing twice (two single steps), then fails
+        calls[0] += 1
+        if calls[0] == 3:
+            raise ValueError("draft source failed")
+        return []
 
     with pytest.raises(ValueError, match="draft source failed"):
-        m.decode_drafted(first, len(prompt), 5, c, bad, context=prompt, k_max=2)
+        m.decode_drafted(first, P, 20, c, bad, context=prompt, k_max=2, adaptive=False, on_token=emitted.append)
+    # the decode stopped at the failing call: two tokens out, the cache valid up to the next position
+    assert calls[0] == 3 and len(emitted) == 2 and len(c) == P + 2
+    want, _ = m.decode(first, P, 2, c)
+    assert want == emitted
     with pytest.raises(qe.QeError):  # a draft token outside the vocabulary
         m.decode_drafted(first, len(prompt), 5, c, lambda h, k: [TINY.vocab_size] * k, context=prompt, k_max=2)
 

@@ -47,6 +47,42 @@ def test_static_attention_matches_work_buffer_variant(gpu):
         np.testing.assert_array_equal(got, ref)
 
 
+def test_static_attention_under_graph_capture(gpu):
+    """after one eager call on the device (it looks up the array's address), the op is captured in a
+    graph; each replay, with new q values written eagerly in between, equals qe_op_attention's
+    output on the same inputs bit for bit"""
+    import torch
+    n_pos, stride, nh, nkv = 700, 704, 16, 8
+    rng = np.random.default_rng(11)
+    qs = torch.from_numpy(rng.standard_normal((4, nh * 128)).astype(np.float32)).cuda()
+    k = torch.from_numpy(rng.standard_normal((nkv, stride, 128)).astype(np.float32)).cuda()
+    v = torch.from_numpy(rng.standard_normal((nkv, stride, 128)).astype(np.float32)).cuda()
+    q = qs[0].clone()
+    got = torch.full((nh * 128,), float("nan"), device="cuda")
+    ref = torch.empty_like(got)
+    work = torch.empty(qe.op_attention_work_bytes(nh, nkv, n_pos) // 4 + 64, device="cuda")
+    f = static_fn()
+
+    def call():
+        rc = f(q.data_ptr(), k.data_ptr(), v.data_ptr(), got.data_ptr(), n_pos, stride, nh, nkv, 0,
+               ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert rc == qe.QE_OK, qe.lib().qe_last_error()
+
+    call()  # the eager first call on this device
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        call()
+    for i in range(4):
+        q.copy_(qs[i])
+        got.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        qe.op_attention(q, k, v, ref, n_pos, nh, nkv, work)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(got.cpu().numpy(), ref.cpu().numpy(), err_msg=f"replay {i}")
+
+
 def test_static_attention_refuses_oversized_calls(gpu):
     import torch
     q = torch.zeros(32 * 128, device="cuda")
