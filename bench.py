@@ -103,8 +103,16 @@ def pmc_traffic(stage: str):
     (FETCH_SIZE and WRITE_SIZE per dispatch, each scaled by the same counter's reading for the
     1 GiB copy), or None when the summary does not cover that stage. The attention's figure is
     from the counter runs without the L2 prefetch, so that it covers the same bytes as the
-    attention's algorithmic bytes (its own K/V, q/k/v and output)."""
-    name = "decode_step_qwen3_0_6b_pmc_no_prefetch.json" if stage == "attention" else "decode_step_qwen3_0_6b_pmc.json"
+    attention's algorithmic bytes (its own K/V, q/k/v and output); the two-launch layer's stages
+    (attn_block, mlp_block, final_reduce) are from the counter runs of those launches. On gfx950
+    FETCH_SIZE counts L2 read requests to the memory fabric: these are L2-miss bytes, an upper
+    bound on HBM bytes."""
+    if stage in ("attn_block", "mlp_block", "final_reduce"):
+        name = "decode_step_fused_qwen3_0_6b_pmc.json"
+    elif stage == "attention":
+        name = "decode_step_qwen3_0_6b_pmc_no_prefetch.json"
+    else:
+        name = "decode_step_qwen3_0_6b_pmc.json"
     path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:

@@ -109,7 +109,7 @@ def build_cli(verbose: bool = False) -> str:
 
 
 
-PMC_SRCS = ["qe_stage_pmc.hip", "kernels.hip", "attention.hip", "batch.hip"]
+PMC_SRCS = ["qe_stage_pmc.hip", "kernels.hip", "attention.hip", "batch.hip", "fused.hip"]
 PMC = os.path.join(PKG, "qe_stage_pmc")
 
 

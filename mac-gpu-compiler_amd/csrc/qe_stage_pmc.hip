@@ -6,6 +6,16 @@
 // the attention launch's L2 prefetch of the layer's gate/up and down weights.
 //
 //   qe_stage_pmc [--pos P] [--no-prefetch]   (attention attends positions 0..P, default 193)
+//   qe_stage_pmc --fused [--pos P]   the two-launch layer instead: 8 x (attention block, MLP
+//                         block) in step order with the engine's attention shape for P + 1
+//                         positions (runs of 64 positions, 4 / 8 / 16 / 32 of them), then
+//                         2 x (final reduce, lm_head, argmax); exits with status 2 if this
+//                         device does not deal a launch's workgroups to its XCDs round-robin
+//   qe_stage_pmc --l2-persist   no counters: times, as graphs of 64 launches, a launch whose
+//                         workgroup (XCD x, slot s) reads 64 KiB of XCD x's 2 MiB share of a
+//                         16 MiB chunk, for the same chunk every launch, 8 rotating chunks
+//                         (128 MiB, within the MALL) and 48 (768 MiB): whether L2 keeps lines
+//                         from one launch to the next
 //   qe_stage_pmc --gemm   the chunked prefill's GEMM instead (launch_gemm, no norm, plain store),
 //                         3 launches at each of M x N x K = 2048 x 4096 x 1024 (q|k|v of a
 //                         2048-token chunk: k_gemm_tile), 512 x 6144 x 1024 and 512 x 4096 x 1024
@@ -22,6 +32,7 @@
 
 #include "batch.h"
 #include "kernels.h"
+#include "l2_prefetch.h"
 
 namespace {
 
@@ -36,6 +47,17 @@ namespace {
 
 __global__ void k_copy(const float4* __restrict__ s, float4* __restrict__ d, size_t n) {
   for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < n; i += size_t(gridDim.x) * 256) d[i] = s[i];
+}
+
+// every workgroup reads all of p[0..n): each XCD's L2 misses on the buffer once per launch, unless
+// the lines are still in it from an earlier launch (the sum only feeds a never-taken store)
+__global__ void k_reread(const float4* __restrict__ p, size_t n, float* sink) {
+  float a = 0.f;
+  for (size_t i = threadIdx.x; i < n; i += 256) {
+    const float4 v = p[i];
+    a += v.x + v.y + v.z + v.w;
+  }
+  if (a == -1.25f) sink[threadIdx.x] = a;
 }
 
 // bf16 ~ small values, so sums stay finite
@@ -68,6 +90,19 @@ __global__ void k_fill_hash_bf16(uint16_t* p, size_t n, float scale) {
     p[i] = uint16_t(__float_as_uint(scale * hash_unit(uint32_t(i) ^ 0x9E3779B9u)) >> 16);
 }
 
+// workgroup (XCD x, slot blockIdx / 8) reads 64 KiB of XCD x's 2 MiB share of 16 MiB chunk `chunk`
+__global__ __launch_bounds__(256) void k_read_xcd_share(const float4* __restrict__ base, uint32_t chunk, float* sink) {
+  const uint32_t x = qe::xcc_id() & 7, slot = blockIdx.x >> 3;
+  const float4* p = base + (size_t(chunk) * (16u << 20) + size_t(x) * (2u << 20) + size_t(slot) * (64u << 10)) / 16;
+  float a = 0.f;
+#pragma unroll 4
+  for (uint32_t i = threadIdx.x; i < (64u << 10) / 16; i += 256) {
+    const float4 v = p[i];
+    a += v.x + v.y + v.z + v.w;
+  }
+  if (a == -1.25f) sink[threadIdx.x] = a;
+}
+
 template <typename T>
 T* dalloc(size_t n) {
   T* p = nullptr;
@@ -79,14 +114,55 @@ T* dalloc(size_t n) {
 
 int main(int argc, char** argv) {
   uint32_t pos = 193;
-  bool prefetch = true, gemm = false, random = false;
+  bool prefetch = true, gemm = false, random = false, fused = false, persist = false;
   int reps = 3;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
     else if (!strcmp(argv[i], "--no-prefetch")) prefetch = false;
     else if (!strcmp(argv[i], "--gemm")) gemm = true;
+    else if (!strcmp(argv[i], "--fused")) fused = true;
+    else if (!strcmp(argv[i], "--l2-persist")) persist = true;
     else if (!strcmp(argv[i], "--random")) random = true;
     else if (!strcmp(argv[i], "--reps") && i + 1 < argc) reps = std::max(1, atoi(argv[++i]));
+  }
+  if (persist) {
+    CK(hipSetDevice(0));
+    hipStream_t ps;
+    CK(hipStreamCreate(&ps));
+    const uint32_t NCH = 48;  // 16 MiB chunks
+    float4* buf = dalloc<float4>(size_t(NCH) * (16u << 20) / 16);
+    float* sink = dalloc<float>(256);
+    k_fill_f32<<<8192, 256, 0, ps>>>(reinterpret_cast<float*>(buf), size_t(NCH) * (16u << 20) / 4, 1.f);
+    hipEvent_t e0, e1;
+    CK(hipEventCreate(&e0));
+    CK(hipEventCreate(&e1));
+    const uint32_t rot[3] = {1, 8, NCH};
+    const char* what[3] = {"the same 16 MiB chunk every launch", "8 chunks in turn (128 MiB)", "48 chunks in turn (768 MiB)"};
+    for (int v = 0; v < 3; v++) {
+      hipGraph_t g;
+      hipGraphExec_t ge;
+      CK(hipStreamBeginCapture(ps, hipStreamCaptureModeGlobal));
+      for (uint32_t i = 0; i < 64; i++) hipLaunchKernelGGL(k_read_xcd_share, dim3(256), dim3(256), 0, ps, buf, i % rot[v], sink);
+      CK(hipStreamEndCapture(ps, &g));
+      CK(hipGraphInstantiate(&ge, g, nullptr, nullptr, 0));
+      CK(hipGraphLaunch(ge, ps));
+      CK(hipStreamSynchronize(ps));
+      float best = 1e30f;
+      for (int t = 0; t < 5; t++) {
+        CK(hipEventRecord(e0, ps));
+        CK(hipGraphLaunch(ge, ps));
+        CK(hipEventRecord(e1, ps));
+        CK(hipEventSynchronize(e1));
+        float ms = 0.f;
+        CK(hipEventElapsedTime(&ms, e0, e1));
+        best = std::min(best, ms);
+      }
+      const double us = best * 1e3 / 64;
+      std::printf("l2-persist: %-36s %.3f us per launch, %.0f GB/s\n", what[v], us, 16.0 * 1048576 / (us * 1e-6) / 1e9);
+      CK(hipGraphExecDestroy(ge));
+      CK(hipGraphDestroy(g));
+    }
+    return 0;
   }
   if (gemm) {
     CK(hipSetDevice(0));
@@ -131,6 +207,11 @@ int main(int argc, char** argv) {
     k_fill_f32<<<4096, 256, 0, s>>>(reinterpret_cast<float*>(a), n4 * 4, 1.f);
     hipLaunchKernelGGL(k_copy, dim3(8192), dim3(256), 0, s, a, b, n4);
     CK(hipStreamSynchronize(s));
+    // L2 persistence between dispatches: two launches that each read a 2 MiB buffer (under one
+    // XCD's 4 MB L2) from all 256 workgroups; the second fetches ~nothing if L2 keeps the lines
+    const size_t r4 = (size_t(2) << 20) / 16;
+    for (int r = 0; r < 2; r++) hipLaunchKernelGGL(k_reread, dim3(256), dim3(256), 0, s, a, r4, reinterpret_cast<float*>(b));
+    CK(hipStreamSynchronize(s));
     CK(hipFree(a));
     CK(hipFree(b));
   }
@@ -172,6 +253,67 @@ int main(int argc, char** argv) {
   CK(hipMemsetAsync(tokens, 0, (max_seq + 2) * 4, s));
   CK(hipMemsetAsync(err, 0, 4, s));
   CK(hipStreamSynchronize(s));
+
+  if (fused) {
+    // the launches need the round-robin workgroup -> XCD placement the engine checks at load
+    uint32_t* place = dalloc<uint32_t>(qe::kFusedXcds * qe::kFusedSlots);
+    uint32_t* host_ids = nullptr;
+    CK(hipHostMalloc(&host_ids, qe::kFusedXcds * qe::kFusedSlots * 4, hipHostMallocDefault));
+    bool ok = false;
+    CK(qe::fused_placement_check(place, host_ids, &ok, s));
+    CK(hipHostFree(host_ids));
+    if (!ok) {
+      std::fprintf(stderr, "qe_stage_pmc: workgroups are not dealt to the XCDs round-robin; no fused launches\n");
+      return 2;
+    }
+    const uint32_t NX = qe::kFusedXcds, n = pos + 1, R = qe::kFusedMaxRuns;
+    const uint32_t run = 64 * ((n + 64 * R - 1) / (64 * R)), active = (n + run - 1) / run;
+    const uint32_t fsplits = run > 64 ? R : active <= 4 ? 4 : active <= 8 ? 8 : active <= 16 ? 16 : R;
+    float* res0 = dalloc<float>(H);
+    float* res1 = dalloc<float>(H);
+    float* part_attn = dalloc<float>(size_t(NX) * H);
+    float* part_mlp = dalloc<float>(size_t(NX) * H);
+    uint2* fqkv = dalloc<uint2>(qe::kFusedQkvPairs);
+    uint2* fpart = dalloc<uint2>(qe::kFusedPartPairs);
+    uint2* fh = dalloc<uint2>(qe::kFusedHPairs);
+    uint32_t* fsync = dalloc<uint32_t>(qe::kFusedSyncWords);
+    k_fill_f32<<<4, 256, 0, s>>>(res0, H, 0.5f);
+    CK(hipMemsetAsync(part_mlp, 0, size_t(NX) * H * 4, s));
+    CK(hipMemsetAsync(fqkv, 0, qe::kFusedQkvPairs * 8, s));
+    CK(hipMemsetAsync(fpart, 0, qe::kFusedPartPairs * 8, s));
+    CK(hipMemsetAsync(fh, 0, qe::kFusedHPairs * 8, s));
+    CK(hipMemsetAsync(fsync, 0, qe::kFusedSyncWords * 4, s));
+    CK(hipStreamSynchronize(s));
+    qe::FusedLayerParams f{};
+    f.w_in = gains; f.q_norm = gains; f.k_norm = gains; f.w_post = gains;
+    f.qkv = fqkv; f.attn_part = fpart; f.h = fh;
+    f.tokens = tokens; f.vocab = V; f.state = st;
+    f.k_cache = kc; f.v_cache = vc; f.kv_bf16 = 0; f.max_seq = max_seq; f.rope_cur = rope_cur;
+    f.splits = fsplits; f.run = run; f.eps = 1e-6f; f.scale = 0.08838834764f;
+    f.sync = fsync; f.err = err;
+    for (int it = 0; it < 8; it++) {
+      const uint16_t* Wc = W + per_copy * (it % 4);
+      f.w_qkv = Wc; f.w_o = Wc + n_qkv; f.w_gu = Wc + n_qkv + n_o; f.w_down = Wc + n_qkv + n_o + n_gu;
+      f.res_in = res0; f.part_in = part_mlp; f.res_out = res1; f.part_out = part_attn;
+      CK(qe::launch_fused_attn(f, false, s));
+      f.res_in = res1; f.part_in = part_attn; f.res_out = res0; f.part_out = part_mlp;
+      CK(qe::launch_fused_mlp(f, s));
+      CK(hipStreamSynchronize(s));
+    }
+    for (int it = 0; it < 2; it++) {
+      CK(qe::launch_fused_reduce(res0, part_mlp, x, s));
+      qe::MatvecParams p{};
+      p.eps = 1e-6f; p.w = LM; p.x = x; p.nw = gains; p.rows = V; p.cols = H; p.out = logits; p.cand = cand;
+      CK(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+      CK(qe::launch_argmax(cand, n_cand, logits, st, tokens, nullptr, err, nullptr, nullptr, 0, s));
+      CK(hipStreamSynchronize(s));
+    }
+    uint32_t e = 0;
+    CK(hipMemcpy(&e, err, 4, hipMemcpyDeviceToHost));
+    std::printf("qe_stage_pmc: 8 x (attention block at pos %u in %u runs of %u, MLP block), 2 x (final reduce, "
+                "lm_head, argmax); error bits 0x%x\n", pos, fsplits, run, e);
+    return e ? 1 : 0;
+  }
 
   for (int it = 0; it < 8; it++) {
     const uint16_t* Wc = W + per_copy * (it % 4);
