@@ -138,6 +138,8 @@ struct qe_model {
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
   // and o_proj weights (QE_FUSED_PF_MLP)
   uint32_t fused_pf_attn = 0, fused_pf_mlp = 0;
+  // the attention block's idle slots load the layer's MLP weights into L2 (QE_FUSED_PF_IDLE)
+  bool fused_pf_idle = false;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -458,6 +460,7 @@ int qe_model_load(const char* path, qe_model** out) {
   m->pgen = reinterpret_cast<uint32_t*>(m->scratch + s_pgen);
   if (const char* v = getenv("QE_FUSED_PF_ATTN")) m->fused_pf_attn = uint32_t(std::min(std::max(atoi(v), 0), 64));
   if (const char* v = getenv("QE_FUSED_PF_MLP")) m->fused_pf_mlp = uint32_t(std::min(std::max(atoi(v), 0), 64));
+  if (const char* v = getenv("QE_FUSED_PF_IDLE")) m->fused_pf_idle = strcmp(v, "0") != 0;
   // the layers' tensors sit at one stride in the arena (the persistent launch finds layer l's from
   // layer 0's)
   m->layer_stride = L > 1 ? lo[1].in - lo[0].in : 0;
@@ -662,6 +665,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     f.res_in = m->res0; f.part_in = m->part_mlp; f.res_out = m->res1; f.part_out = m->part_attn;
     for (auto& r : f.pf) r = qe::FusedPrefetch{};
     f.pf_wgs = m->fused_pf_attn;
+    f.pf_idle = m->fused_pf_idle;
     f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
     f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
@@ -670,6 +674,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     // rows and o_proj columns of each XCD
     f.res_in = m->res1; f.part_in = m->part_attn; f.res_out = m->res0; f.part_out = m->part_mlp;
     for (auto& r : f.pf) r = qe::FusedPrefetch{};
+    f.pf_idle = 0;
     f.pf_wgs = l + 1 < c.num_hidden_layers ? m->fused_pf_mlp : 0;
     if (f.pf_wgs) {
       const Layer& n = m->layers[l + 1];

@@ -87,10 +87,10 @@ __device__ __forceinline__ uint32_t qkv_row0(uint32_t x, uint32_t s) {
   return s < 16 ? x * G * D + 16 * s : s < 24 ? QD + x * D + 16 * (s - 16) : QD + KD + x * D + 16 * (s - 24);
 }
 
-// Prefetch workgroup k (of p.pf_wgs on this XCD) loads one word of every 64-byte half line
-// i = k + pf_wgs j of the regions' lines on XCD x, so the lines sit in this XCD's L2 when the
-// later launch's workgroups on XCD x read them; the words only feed a never-taken store.
-__device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32_t x, uint32_t k) {
+// Prefetcher k of n on this XCD loads one word of every 64-byte half line i = k + n j of the
+// regions' lines on XCD x, so the lines sit in this XCD's L2 when the later launch's workgroups
+// on XCD x read them; the words only feed a never-taken store.
+__device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32_t x, uint32_t k, uint32_t n) {
   constexpr uint32_t U = 8, SEG = 64;
   uint32_t per_row[kFusedMaxPrefetch], span[kFusedMaxPrefetch], tot = 0;
 #pragma unroll
@@ -101,11 +101,11 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
   }
   if (tot == 0) return;
   uint32_t hsum = 0;
-  for (uint32_t j0 = 0; (j0 * p.pf_wgs + k) * 256 < tot; j0 += U) {
+  for (uint32_t j0 = 0; (j0 * n + k) * 256 < tot; j0 += U) {
     uint32_t v[U];
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) {
-      uint32_t i = min(((j0 + u) * p.pf_wgs + k) * 256 + threadIdx.x, tot - 1);
+      uint32_t i = min(((j0 + u) * n + k) * 256 + threadIdx.x, tot - 1);
       uint32_t t = 0;
 #pragma unroll
       for (int q = 0; q + 1 < kFusedMaxPrefetch; q++) {
@@ -123,7 +123,7 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) hsum ^= v[u];
   }
-  if (p.pf_wgs == 0xFFFFFFFFu && hsum == 0x5A5A5A5Au) *p.err = hsum;  // never: keeps the loads
+  if (n == 0xFFFFFFFFu && hsum == 0x5A5A5A5Au) *p.err = hsum;  // never: keeps the loads
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t x = fused_xcd(p.err);
   if (blockIdx.x >= NX * NS) {  // a prefetch workgroup (the whole workgroup)
-    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX);
+    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
   const uint32_t s = blockIdx.x / NX;
@@ -195,6 +195,30 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   uint4 gin[2];
 #pragma unroll
   for (int k = 0; k < 2; k++) gin[k] = reinterpret_cast<const uint4*>(p.w_in)[lane + 64 * k];
+  // Attention inputs, issued behind the residual and q|k|v weight loads: loads complete in issue
+  // order, so they do not hold up this workgroup's q|k|v rows (which every run waits for), and
+  // they arrive while the rows are computed instead of after them. The raw norm gains, this
+  // position's RoPE row, and the first K/V tile of the run (the row at pos is not read from it:
+  // the run that holds pos substitutes the new row from LDS). Every workgroup issues all of
+  // them, the tile through descriptors over the run's first rows (none for a workgroup without
+  // a run: its loads read 0 without touching memory): behind a branch, the wait counts of the
+  // two paths would merge and every workgroup's q|k|v rows would wait for the tile.
+  const size_t head_base = size_t(x) * p.max_seq * D;
+  KVTile<KV_BF16> A;
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
+  const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
+  const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  {
+    constexpr uint32_t EL = KV_BF16 ? 2 : 4;
+    const uint32_t r0 = s * p.run;
+    const uint32_t rows = attn && r0 < p.max_seq ? min(p.max_seq - r0, T) : 0u;
+    auto run_rsrc = [&](const void* cache) __attribute__((always_inline)) {
+      const uint8_t* b = static_cast<const uint8_t*>(cache) + (head_base + size_t(r0) * D) * EL;
+      return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(b), short(0), int(rows * D * EL), 0x00020000);
+    };
+    load_tile_buf<KV_BF16>(A, run_rsrc(p.k_cache), run_rsrc(p.v_cache), 0, tid);
+  }
   // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
   const uint32_t rg = tid >> 4, t16 = tid & 15;
@@ -229,23 +253,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       for (int r = 0; r < 4; r++) p.qkv[qrow0 + r] = pair(acc[r], tag);
     }
   }
-  // attention inputs, loaded once the q|k|v rows are out (loads complete in issue order, so
-  // loaded earlier they would hold up this workgroup's rows, which every run waits for): the
-  // first K/V tile of the run (the row at pos is not read from it: the run that holds pos
-  // substitutes the new row from LDS), the raw norm gains, this position's RoPE row
-  const size_t head_base = size_t(x) * p.max_seq * D;
-  KVTile<KV_BF16> A;
-  uint16_t gq[2] = {0, 0}, gk[2] = {0, 0};
-  float2 cs = make_float2(0.f, 0.f);
-  if (attn) {
-    load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, s * p.run, tid);
-    gq[0] = p.q_norm[lane];
-    gq[1] = p.q_norm[lane + 64];
-    gk[0] = p.k_norm[lane];
-    gk[1] = p.k_norm[lane + 64];
-    cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
-    if (SM > 16) load_wo();
-  }
+  if (SM > 16 && attn) load_wo();
 
   // ---- attention run s of KV head x (cpu_inference.rs:134-162) ----
   auto attention = [&]() __attribute__((always_inline)) {
@@ -494,7 +502,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
         __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       return;
     }
-    if (!oproj) return;
+    if (!oproj) {
+      // slots splits..15 are done once their q|k|v rows are out: they load the pf regions (this
+      // layer's gate|up rows and down columns of XCD x) into the XCD's L2 for the MLP launch
+      if (p.pf_idle && splits < 16 && p.state->pos < p.pf_max_pos) fused_prefetch(p, x, s - splits, 16 - splits);
+      return;
+    }
     load_wo();
     merge_oproj();
   } else {
@@ -513,12 +526,13 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t x = fused_xcd(p.err);
   if (blockIdx.x >= NX * NS) {  // a prefetch workgroup (the whole workgroup)
-    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX);
+    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
   const uint32_t s = blockIdx.x / NX;
   __shared__ __align__(16) float xs[H];
   __shared__ float red4[4];
+  __shared__ __align__(16) float hs[I / NX];  // this XCD's h values
 
   const uint32_t tag = *gen_word(p.sync, x) + 1;
 
@@ -576,29 +590,32 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   }
 
   // down over this XCD's 384 columns (cpu_inference.rs:171-172): the partial of rows 32 s ..
+  // Wave 0 alone polls the XCD's 384 h pairs (lane l: pairs 6 l .. 6 l + 5) and leaves the values
+  // in LDS: a poll round is 3 KB of L2 reads per workgroup instead of every thread's 24 pairs.
   const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, (I / NX) * 8);
-  uint4 hv[3][4];  // chunk t16 + 16 k: h pairs 8 c .. 8 c + 7, two per load
-  for (uint32_t spins = 0;;) {
-    bool ok = true;
+  if (wave == 0) {
+    uint4 hv[3];
+    for (uint32_t spins = 0;;) {
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
+      for (int k = 0; k < 3; k++) hv[k] = ld_pair2(rh, 6 * lane + 2 * k);
+      bool ok = true;
 #pragma unroll
-      for (int q = 0; q < 4; q++) hv[k][q] = ld_pair2(rh, 8 * (t16 + 16 * k) + 2 * q);
+      for (int k = 0; k < 3; k++) ok = ok && hv[k].y == tag && hv[k].w == tag;
+      if (poll_done(ok, spins, p.err)) break;
     }
 #pragma unroll
     for (int k = 0; k < 3; k++) {
-#pragma unroll
-      for (int q = 0; q < 4; q++) ok = ok && hv[k][q].y == tag && hv[k][q].w == tag;
+      hs[6 * lane + 2 * k] = __uint_as_float(hv[k].x);
+      hs[6 * lane + 2 * k + 1] = __uint_as_float(hv[k].z);
     }
-    if (poll_done(ok, spins, p.err)) break;
   }
+  __syncthreads();
+  const float4* hs4 = reinterpret_cast<const float4*>(hs);
   float da[2] = {0.f, 0.f};
 #pragma unroll
-  for (int k = 0; k < 3; k++) {
-    const float4 ha = make_float4(__uint_as_float(hv[k][0].x), __uint_as_float(hv[k][0].z),
-                                  __uint_as_float(hv[k][1].x), __uint_as_float(hv[k][1].z));
-    const float4 hb = make_float4(__uint_as_float(hv[k][2].x), __uint_as_float(hv[k][2].z),
-                                  __uint_as_float(hv[k][3].x), __uint_as_float(hv[k][3].z));
+  for (int k = 0; k < 3; k++) {  // chunk c = t16 + 16 k: h values 8 c .. 8 c + 7
+    const uint32_t c = t16 + 16 * k;
+    const float4 ha = hs4[2 * c], hb = hs4[2 * c + 1];
 #pragma unroll
     for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha, hb, da[r]);
   }

@@ -209,6 +209,9 @@ struct FusedLayerParams {
   // pf_max_pos; pf_wgs = 0: none)
   FusedPrefetch pf[kFusedMaxPrefetch];
   uint32_t pf_wgs, pf_max_pos;
+  // the attention block's slots without a run or o_proj rows load the pf regions once their
+  // q|k|v rows are out
+  int pf_idle;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
