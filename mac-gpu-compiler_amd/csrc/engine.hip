@@ -138,8 +138,9 @@ struct qe_model {
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
   // and o_proj weights (QE_FUSED_PF_MLP)
   uint32_t fused_pf_attn = 0, fused_pf_mlp = 0;
-  // the attention block's idle slots load the layer's MLP weights into L2 (QE_FUSED_PF_IDLE)
-  bool fused_pf_idle = false;
+  // the attention block's slots without a run or o_proj rows load part of the layer's gate|up
+  // rows into L2 for the MLP block (QE_FUSED_PF_IDLE=0: off)
+  bool fused_pf_idle = true;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -665,9 +666,19 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     f.res_in = m->res0; f.part_in = m->part_mlp; f.res_out = m->res1; f.part_out = m->part_attn;
     for (auto& r : f.pf) r = qe::FusedPrefetch{};
     f.pf_wgs = m->fused_pf_attn;
-    f.pf_idle = m->fused_pf_idle;
-    f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
-    f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
+    f.pf_idle = 0;
+    if (f.pf_wgs) {
+      f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
+      f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
+    } else if (m->fused_pf_idle && f.splits < 16) {
+      // the 16 - splits slots without a run each pull ~128 KB into L2 while the runs and o_proj
+      // are latency-bound (a CU takes in ~30 GB/s; more would hold up the launch's end): the
+      // first 2 (16 - splits) of each MLP slot's 24 gate|up rows, all 24 with 4 runs, 16 with 8
+      // (measured at 130..257 positions: 1948 -> 2101 tok/s; all 24 rows with 8 runs: 1935 -> 1852)
+      const uint32_t rows = std::min(2 * (16 - f.splits), 24u);
+      f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, rows * H * 2, 24 * H * 2, qe::kFusedSlots};
+      f.pf_idle = 1;
+    }
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     if (want("attn_block")) HIP_TRY(qe::launch_fused_attn(f, l == 0, s));
     // MLP block: x = res1 + the o_proj partials; its extra workgroups load the next layer's q|k|v

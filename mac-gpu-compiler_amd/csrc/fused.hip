@@ -89,7 +89,7 @@ __device__ __forceinline__ uint32_t qkv_row0(uint32_t x, uint32_t s) {
 
 // Prefetcher k of n on this XCD loads one word of every 64-byte half line i = k + n j of the
 // regions' lines on XCD x, so the lines sit in this XCD's L2 when the later launch's workgroups
-// on XCD x read them; the words only feed a never-taken store.
+// on XCD x read them; the words only feed an empty asm statement, which keeps the loads.
 __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32_t x, uint32_t k, uint32_t n) {
   constexpr uint32_t U = 8, SEG = 64;
   uint32_t per_row[kFusedMaxPrefetch], span[kFusedMaxPrefetch], tot = 0;
@@ -123,7 +123,7 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
 #pragma unroll
     for (uint32_t u = 0; u < U; u++) hsum ^= v[u];
   }
-  if (n == 0xFFFFFFFFu && hsum == 0x5A5A5A5Au) *p.err = hsum;  // never: keeps the loads
+  asm volatile("" ::"v"(hsum));
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -504,8 +504,9 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     }
     if (!oproj) {
       // slots splits..15 are done once their q|k|v rows are out: they load the pf regions (this
-      // layer's gate|up rows and down columns of XCD x) into the XCD's L2 for the MLP launch
-      if (p.pf_idle && splits < 16 && p.state->pos < p.pf_max_pos) fused_prefetch(p, x, s - splits, 16 - splits);
+      // layer's gate|up rows of XCD x) into the XCD's L2 for the MLP launch (fewer than 16 runs
+      // are fewer than 1024 positions, where prefetching pays at any cache element type)
+      if (p.pf_idle && splits < 16) fused_prefetch(p, x, s - splits, 16 - splits);
       return;
     }
     load_wo();

@@ -114,7 +114,7 @@ T* dalloc(size_t n) {
 
 int main(int argc, char** argv) {
   uint32_t pos = 193;
-  bool prefetch = true, gemm = false, random = false, fused = false, persist = false;
+  bool prefetch = true, gemm = false, random = false, fused = false, persist = false, pf_idle = false;
   int reps = 3;
   for (int i = 1; i < argc; i++) {
     if (!strcmp(argv[i], "--pos") && i + 1 < argc) pos = uint32_t(strtoul(argv[++i], nullptr, 10));
@@ -122,6 +122,7 @@ int main(int argc, char** argv) {
     else if (!strcmp(argv[i], "--gemm")) gemm = true;
     else if (!strcmp(argv[i], "--fused")) fused = true;
     else if (!strcmp(argv[i], "--l2-persist")) persist = true;
+    else if (!strcmp(argv[i], "--pf-idle")) pf_idle = true;
     else if (!strcmp(argv[i], "--random")) random = true;
     else if (!strcmp(argv[i], "--reps") && i + 1 < argc) reps = std::max(1, atoi(argv[++i]));
   }
@@ -295,7 +296,17 @@ int main(int argc, char** argv) {
       const uint16_t* Wc = W + per_copy * (it % 4);
       f.w_qkv = Wc; f.w_o = Wc + n_qkv; f.w_gu = Wc + n_qkv + n_o; f.w_down = Wc + n_qkv + n_o + n_gu;
       f.res_in = res0; f.part_in = part_mlp; f.res_out = res1; f.part_out = part_attn;
+      if (pf_idle) {  // the attention block's idle slots load the MLP block's weights of each XCD
+        const uint8_t* gu = reinterpret_cast<const uint8_t*>(f.w_gu);
+        const uint8_t* dn = reinterpret_cast<const uint8_t*>(f.w_down);
+        f.pf[0] = qe::FusedPrefetch{gu, 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
+        f.pf[1] = qe::FusedPrefetch{dn, I / NX * 2, I / NX * 2, I * 2, H};
+        f.pf_idle = 1;
+        f.pf_max_pos = max_seq;
+      }
       CK(qe::launch_fused_attn(f, false, s));
+      f.pf_idle = 0;
+      for (auto& r : f.pf) r = qe::FusedPrefetch{};
       f.res_in = res1; f.part_in = part_attn; f.res_out = res0; f.part_out = part_mlp;
       CK(qe::launch_fused_mlp(f, s));
       CK(hipStreamSynchronize(s));
