@@ -431,15 +431,23 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   auto merge_oproj = [&]() __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride,
                                               uint32_t(kFusedMaxRuns * G * kPartStride * 8));
+    // one poll round trip for both: wave 0's (m, l) pairs and every thread's acc values
+    const uint32_t j = tid >> 7, d = tid & 127;
+    const uint32_t jh = min(lane / SM, G - 1), u = lane % SM;
+    const bool live = wave == 0 && lane < G * SM && u < splits;
+    const uint32_t base = (min(u, splits - 1) * G + jh) * kPartStride;
+    uint4 ml = make_uint4(0u, 0u, 0u, 0u);  // pairs m, l (wave 0)
+    uint2 av[SM];
+    for (uint32_t spins = 0;;) {
+      if (wave == 0) ml = ld_pair2(rp, base);
+#pragma unroll
+      for (int q = 0; q < SM; q++) av[q] = ld_pair(rp, (min(uint32_t(q), splits - 1) * G + j) * kPartStride + 4 + d);
+      bool ok = !live || (ml.y == tag && ml.w == tag);
+#pragma unroll
+      for (int q = 0; q < SM; q++) ok = ok && av[q].y == tag;
+      if (poll_done(ok, spins, p.err)) break;
+    }
     if (wave == 0) {
-      const uint32_t jh = min(lane / SM, G - 1), u = lane % SM;
-      const bool live = lane < G * SM && u < splits;
-      const uint32_t base = (min(u, splits - 1) * G + jh) * kPartStride;
-      uint4 ml;  // pairs m, l
-      for (uint32_t spins = 0;;) {
-        ml = ld_pair2(rp, base);
-        if (poll_done(!live || (ml.y == tag && ml.w == tag), spins, p.err)) break;
-      }
       const float m = live ? __uint_as_float(ml.x) : -INFINITY;
       float M = m;
 #pragma unroll
@@ -453,21 +461,11 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
         if (u == 0) msum[jh] = L;
       }
     }
+    __syncthreads();
     {
-      const uint32_t j = tid >> 7, d = tid & 127;
-      uint2 av[SM];
-      for (uint32_t spins = 0;;) {
-        bool ok = true;
-#pragma unroll
-        for (int u = 0; u < SM; u++) av[u] = ld_pair(rp, (min(uint32_t(u), splits - 1) * G + j) * kPartStride + 4 + d);
-#pragma unroll
-        for (int u = 0; u < SM; u++) ok = ok && av[u].y == tag;
-        if (poll_done(ok, spins, p.err)) break;
-      }
-      __syncthreads();
       float Av = 0.f;
 #pragma unroll
-      for (int u = 0; u < SM; u++) Av += uint32_t(u) < splits ? mw[j][u] * __uint_as_float(av[u].x) : 0.f;
+      for (int q = 0; q < SM; q++) Av += uint32_t(q) < splits ? mw[j][q] * __uint_as_float(av[q].x) : 0.f;
       att[tid] = Av * (1.0f / msum[j]);
     }
     __syncthreads();
