@@ -123,6 +123,19 @@ def pmc_traffic(stage: str):
     return int(row["traffic_bytes"]) if row and "traffic_bytes" in row else None
 
 
+def pmc_prefetch(stage: str):
+    """bytes of a later launch's weights that one launch of `stage` loads into L2, as counted in the
+    same counter summary (0 when it loads none), or None when the summary does not cover `stage`"""
+    if stage not in ("attn_block", "mlp_block", "final_reduce"):
+        return None
+    try:
+        with open(os.path.join(ROOT, "profiles", "decode_step_fused_qwen3_0_6b_pmc.json")) as f:
+            row = json.load(f).get("stages", {}).get(stage)
+    except (OSError, ValueError):
+        return None
+    return int(row.get("prefetch_bytes", 0)) if row else None
+
+
 def cpu_baseline(ckpt: str, prompt, target_s: float = 15.0, min_steps: int = 16):
     """The oracle (C restatement of cpu_inference.rs) on this host at the benchmark's own
     positions: an untimed prefill of the whole prompt, then greedy decode steps from the prompt's
@@ -646,6 +659,7 @@ def main():
             "unit": "GB/s",
             "frac": round(dom["achieved_gbs"] / SPEC_HBM_GBS, 4) if dom["achieved_gbs"] else None,
             "traffic": pmc_traffic(dom_name),
+            "traffic_prefetch_bytes": pmc_prefetch(dom_name),
             "kernel": dom_name,
             "bytes_per_launch": dom["bytes_per_launch"],
             "mean_position": mean_pos,

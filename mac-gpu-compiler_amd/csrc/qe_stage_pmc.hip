@@ -296,13 +296,12 @@ int main(int argc, char** argv) {
       const uint16_t* Wc = W + per_copy * (it % 4);
       f.w_qkv = Wc; f.w_o = Wc + n_qkv; f.w_gu = Wc + n_qkv + n_o; f.w_down = Wc + n_qkv + n_o + n_gu;
       f.res_in = res0; f.part_in = part_mlp; f.res_out = res1; f.part_out = part_attn;
-      if (pf_idle) {  // the attention block's idle slots load the MLP block's weights of each XCD
+      if (pf_idle && fsplits < 16) {  // the engine's rule: the attention block's idle slots load the
+        // first 2 (16 - runs) of each MLP workgroup's 24 gate|up rows of their XCD
         const uint8_t* gu = reinterpret_cast<const uint8_t*>(f.w_gu);
-        const uint8_t* dn = reinterpret_cast<const uint8_t*>(f.w_down);
-        f.pf[0] = qe::FusedPrefetch{gu, 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
-        f.pf[1] = qe::FusedPrefetch{dn, I / NX * 2, I / NX * 2, I * 2, H};
+        const uint32_t rows = std::min(2 * (16 - fsplits), 24u);
+        f.pf[0] = qe::FusedPrefetch{gu, 2 * I / NX * H * 2, rows * H * 2, 24 * H * 2, qe::kFusedSlots};
         f.pf_idle = 1;
-        f.pf_max_pos = max_seq;
       }
       CK(qe::launch_fused_attn(f, false, s));
       f.pf_idle = 0;

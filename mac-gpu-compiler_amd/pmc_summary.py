@@ -69,6 +69,8 @@ def main():
     ap.add_argument("--no-prefetch", action="store_true",
                     help="the counter runs used qe_stage_pmc --no-prefetch (attention without the L2 prefetch)")
     ap.add_argument("--fused", action="store_true", help="the counter runs used qe_stage_pmc --fused")
+    ap.add_argument("--pf-idle", action="store_true",
+                    help="... --fused --pf-idle: the attention block's idle workgroups load the MLP block's gate|up rows")
     ap.add_argument("--l2", default=None, help="counter CSV of TCC_HIT_sum, TCC_MISS_sum, TCC_EA0_RDREQ_sum")
     ap.add_argument("--persist-log", default=None, help="output of qe_stage_pmc --l2-persist (timings, no counters)")
     a = ap.parse_args()
@@ -110,6 +112,10 @@ def main():
         wk = sum(d["write_kib"]) / len(d["write_kib"])
         traffic = (fk * ff + wk * fw) * 1024.0
         extra = pf if st == "attention" else 0
+        if a.pf_idle and st == "attn_block":
+            # with 4 runs (up to 256 positions) all 24 gate|up rows of each MLP workgroup
+            cfg = qe.QWEN3_0_6B
+            extra = 2 * cfg.intermediate_size * cfg.hidden_size * 2 if a.attn_pos < 256 else 0
         out["stages"][st] = {
             "kernel": d["kernel"],
             "dispatches": len(d["fetch_kib"]),
@@ -158,6 +164,8 @@ def main():
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
         "for attention (the figures `bench.py` divides by the launch time)." +
+        (" The attention block's idle workgroups also load the MLP block's gate|up rows into L2 (prefetch bytes;"
+         " its ratio is traffic over own + prefetch bytes)." if a.pf_idle else "") +
         ("" if a.no_prefetch else " The attention launch also streams the layer's gate/up and down weights into"
          " L2 (prefetch bytes, counted with those stages); its ratio is traffic over own + prefetch bytes."),
         "",
