@@ -115,3 +115,25 @@ def test_fused_real_model_matches_fixture_tokens(gpu, real_ckpt, mode):
     idx = g["sample_idx"]
     worst = max(float(np.max(np.abs(l[idx] - g["sample_val"][i + 1]))) for i, l in enumerate(lg))
     assert worst < 1e-2, worst
+
+
+@pytest.mark.parametrize("env", ["QE_FUSED_PF_IDLE", "QE_FUSED_PF_ATTN", "QE_FUSED_PF_MLP"])
+def test_fused_prefetch_switches_change_no_result(gpu, narrow_ckpt, monkeypatch, env):
+    """the two-launch layer's L2 prefetches only load: turning the idle-slot prefetch off, or
+    adding prefetch workgroups, gives the same tokens and bit-identical logits, at 4, 8 and 16
+    attention runs per KV head (positions 40..339)"""
+    prompt = qe.random_prompt(9, 40, NARROW.vocab_size)
+
+    def run():
+        m = load(narrow_ckpt, 1)
+        assert m.fused_layers() == 1
+        c = qe.KVCache(m, 400)
+        lg0 = m.prefill(prompt, 0, c)
+        toks, lg = m.decode(oracle.argmax(lg0), len(prompt), 300, c, want_logits=True)
+        return toks, lg
+
+    want_toks, want_lg = run()
+    monkeypatch.setenv(env, "0" if env == "QE_FUSED_PF_IDLE" else "8")
+    toks, lg = run()
+    assert toks == want_toks
+    np.testing.assert_array_equal(lg, want_lg)
