@@ -1,5 +1,6 @@
-// K/V tile loads of the decode attention kernels (attention.hip, fused.hip): one 64-position tile
-// of one KV head in the two per-thread layouts the score and P.V phases use.
+// K/V tile loads of the decode attention kernels (attention.hip, fused.hip, persist.hip): one tile
+// of NT = 64 (or 32) positions of one KV head in the two per-thread layouts the score and P.V
+// phases use.
 #pragma once
 
 #include "device_common.h"
@@ -8,17 +9,17 @@
 namespace qe {
 namespace {
 
-template <bool KV_BF16>
+template <bool KV_BF16, int NT = 64>
 struct KVTile;
-template <>
-struct KVTile<false> {
-  float4 k[2][4];  // scores layout: 2 positions x 16 dims
-  float4 v[8];     // PV layout: 8 positions x 4 dims
+template <int NT>
+struct KVTile<false, NT> {
+  float4 k[NT / 32][4];  // scores layout: NT / 32 positions x 16 dims
+  float4 v[NT / 8];      // PV layout: NT / 8 positions x 4 dims
 };
-template <>
-struct KVTile<true> {
-  uint4 k[2][2];
-  uint2 v[8];
+template <int NT>
+struct KVTile<true, NT> {
+  uint4 k[NT / 32][2];
+  uint2 v[NT / 8];
 };
 
 // component-wise select (a ternary on float4 objects selects between their addresses, which
@@ -68,15 +69,16 @@ __device__ __forceinline__ void load_tile(KVTile<KV_BF16>& X, const void* k_cach
 
 // load_tile through buffer descriptors over one head's K and V regions ([max_seq][D] each, so
 // rows past the cache end read as 0 instead of being clamped): two lane offsets, and the rows'
-// distances as scalar or immediate offsets
-template <bool KV_BF16>
-__device__ __forceinline__ void load_tile_buf(KVTile<KV_BF16>& X, __amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
-                                              uint32_t tile, int tid) {
-  constexpr uint32_t D = kHeadDim, EL = KV_BF16 ? 2 : 4;
+// distances as scalar or immediate offsets. A tile of NT = 32 positions: thread (pg, dc) holds
+// position tile + pg of K, thread (dg, pp) positions tile + 4 pp .. + 3 of V.
+template <bool KV_BF16, int NT = 64>
+__device__ __forceinline__ void load_tile_buf(KVTile<KV_BF16, NT>& X, __amdgpu_buffer_rsrc_t rk,
+                                              __amdgpu_buffer_rsrc_t rv, uint32_t tile, int tid) {
+  constexpr uint32_t D = kHeadDim, EL = KV_BF16 ? 2 : 4, VP = NT / 8;
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
-  const uint32_t koff = ((tile + pg) * D + 16 * dc) * EL, voff = ((tile + 8 * pp) * D + 4 * dg) * EL;
+  const uint32_t koff = ((tile + pg) * D + 16 * dc) * EL, voff = ((tile + VP * pp) * D + 4 * dg) * EL;
 #pragma unroll
-  for (int u = 0; u < 2; u++) {
+  for (int u = 0; u < NT / 32; u++) {
     if constexpr (KV_BF16) {
 #pragma unroll
       for (int i = 0; i < 2; i++)
@@ -88,7 +90,7 @@ __device__ __forceinline__ void load_tile_buf(KVTile<KV_BF16>& X, __amdgpu_buffe
     }
   }
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
+  for (int i = 0; i < int(VP); i++) {
     if constexpr (KV_BF16) {
       X.v[i] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(rv, int(voff), int(i * D * EL), 0));
     } else {
@@ -97,8 +99,8 @@ __device__ __forceinline__ void load_tile_buf(KVTile<KV_BF16>& X, __amdgpu_buffe
   }
 }
 
-template <bool KV_BF16>
-__device__ __forceinline__ void tile_k(const KVTile<KV_BF16>& X, int u, float4 (&k4)[4]) {
+template <bool KV_BF16, int NT>
+__device__ __forceinline__ void tile_k(const KVTile<KV_BF16, NT>& X, int u, float4 (&k4)[4]) {
   if constexpr (KV_BF16) {
     k4[0] = bf16x4(X.k[u][0].x, X.k[u][0].y);
     k4[1] = bf16x4(X.k[u][0].z, X.k[u][0].w);
@@ -110,8 +112,8 @@ __device__ __forceinline__ void tile_k(const KVTile<KV_BF16>& X, int u, float4 (
   }
 }
 
-template <bool KV_BF16>
-__device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16>& X, int i) {
+template <bool KV_BF16, int NT>
+__device__ __forceinline__ float4 tile_v(const KVTile<KV_BF16, NT>& X, int i) {
   if constexpr (KV_BF16) {
     return bf16x4(X.v[i].x, X.v[i].y);
   } else {

@@ -141,6 +141,11 @@ struct qe_model {
   // the attention block's slots without a run or o_proj rows load part of the layer's gate|up
   // rows into L2 for the MLP block (QE_FUSED_PF_IDLE=0: off)
   bool fused_pf_idle = true;
+  // ... and the run workgroups the rest of them once their partials are out (QE_FUSED_PF_RUN=0: off)
+  bool fused_pf_run = true;
+  // attention runs of 32 positions up to this many cached positions (QE_FUSED_RUN32; a multiple
+  // of 64, at most 512: 16 runs)
+  uint64_t fused_run32 = 256;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -462,6 +467,8 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* v = getenv("QE_FUSED_PF_ATTN")) m->fused_pf_attn = uint32_t(std::min(std::max(atoi(v), 0), 64));
   if (const char* v = getenv("QE_FUSED_PF_MLP")) m->fused_pf_mlp = uint32_t(std::min(std::max(atoi(v), 0), 64));
   if (const char* v = getenv("QE_FUSED_PF_IDLE")) m->fused_pf_idle = strcmp(v, "0") != 0;
+  if (const char* v = getenv("QE_FUSED_PF_RUN")) m->fused_pf_run = strcmp(v, "0") != 0;
+  if (const char* v = getenv("QE_FUSED_RUN32")) m->fused_run32 = uint64_t(std::min(std::max(atoi(v), 0), 512)) / 64 * 64;
   // the layers' tensors sit at one stride in the arena (the persistent launch finds layer l's from
   // layer 0's)
   m->layer_stride = L > 1 ? lo[1].in - lo[0].in : 0;
@@ -667,6 +674,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     for (auto& r : f.pf) r = qe::FusedPrefetch{};
     f.pf_wgs = m->fused_pf_attn;
     f.pf_idle = 0;
+    f.pf_run = 0;
     if (f.pf_wgs) {
       f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
       f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
@@ -678,6 +686,13 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       const uint32_t rows = std::min(2 * (16 - f.splits), 24u);
       f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, rows * H * 2, 24 * H * 2, qe::kFusedSlots};
       f.pf_idle = 1;
+      if (rows < 24 && m->fused_pf_run) {
+        // the run workgroups finish ~2 us before the launch does (the merge and o_proj follow
+        // them): they load the rest of each MLP slot's rows, 8 of 24 with 8 runs
+        f.pf[1] = qe::FusedPrefetch{bytes(w.w_gu) + size_t(rows) * H * 2, 2 * I / NX * H * 2, (24 - rows) * H * 2,
+                                    24 * H * 2, qe::kFusedSlots};
+        f.pf_run = 1;
+      }
     }
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     if (want("attn_block")) HIP_TRY(qe::launch_fused_attn(f, l == 0, s));
@@ -686,6 +701,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     f.res_in = m->res1; f.part_in = m->part_attn; f.res_out = m->res0; f.part_out = m->part_mlp;
     for (auto& r : f.pf) r = qe::FusedPrefetch{};
     f.pf_idle = 0;
+    f.pf_run = 0;
     f.pf_wgs = l + 1 < c.num_hidden_layers ? m->fused_pf_mlp : 0;
     if (f.pf_wgs) {
       const Layer& n = m->layers[l + 1];
@@ -1052,8 +1068,15 @@ int set_state(qe_model* m, qe_kv* kv, uint32_t token, uint64_t pos) {
 void step_shape(const qe_kv* kv, uint64_t pos, uint32_t& splits, uint32_t& run) {
   const uint64_t n = pos + 1, S = kv->attn_splits;
   if (kv->model->fused) {
-    // one run per slot of an XCD: runs of 64 in 4, 8, 16 or 32 up to 64 x 32 positions, then 32
-    // runs of a whole number of tiles
+    // one run per slot of an XCD: up to fused_run32 positions runs of 32 in 4, 8 or 16 (half the
+    // K/V and the work per run of a 64-position tile); then runs of 64 in 4, 8, 16 or 32 up to
+    // 64 x 32 positions, then 32 runs of a whole number of tiles
+    if (kv->model->fused == 1 && n <= kv->model->fused_run32) {  // (the persistent launch takes runs of 64)
+      run = 32;
+      const uint64_t active = (n + 31) / 32;
+      splits = uint32_t(active <= 4 ? 4 : active <= 8 ? 8 : 16);
+      return;
+    }
     const uint64_t R = qe::kFusedMaxRuns;
     run = uint32_t(64 * ((n + 64 * R - 1) / (64 * R)));
     const uint64_t active = (n + run - 1) / run;

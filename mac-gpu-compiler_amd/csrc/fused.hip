@@ -88,15 +88,17 @@ __device__ __forceinline__ uint32_t qkv_row0(uint32_t x, uint32_t s) {
 }
 
 // Prefetcher k of n on this XCD loads one word of every 64-byte half line i = k + n j of the
-// regions' lines on XCD x, so the lines sit in this XCD's L2 when the later launch's workgroups
-// on XCD x read them; the words only feed an empty asm statement, which keeps the loads.
+// lines of regions T0..T1-1 on XCD x, so the lines sit in this XCD's L2 when the later launch's
+// workgroups on XCD x read them; the words only feed an empty asm statement, which keeps the loads.
+template <int T0 = 0, int T1 = kFusedMaxPrefetch>
 __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32_t x, uint32_t k, uint32_t n) {
   constexpr uint32_t U = 8, SEG = 64;
   uint32_t per_row[kFusedMaxPrefetch], span[kFusedMaxPrefetch], tot = 0;
 #pragma unroll
   for (int t = 0; t < kFusedMaxPrefetch; t++) {
-    per_row[t] = p.pf[t].base ? ceil_div(p.pf[t].row_bytes, SEG) : 0;
-    span[t] = per_row[t] * (p.pf[t].base ? p.pf[t].rows : 0);
+    const bool on = t >= T0 && t < T1 && p.pf[t].base;
+    per_row[t] = on ? ceil_div(p.pf[t].row_bytes, SEG) : 0;
+    span[t] = per_row[t] * (on ? p.pf[t].rows : 0);
     tot += span[t];
   }
   if (tot == 0) return;
@@ -128,12 +130,14 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
 
 // ---------------------------------------------------------------------------------------------
 // attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type,
-// MULTI: runs of more than one 64-position tile (only with 32 runs).
+// MULTI: runs of more than one 64-position tile (only with 32 runs), NT: positions per tile and
+// per single-tile run (64, or 32 for short contexts: half the K/V each run's CU takes in).
 // ---------------------------------------------------------------------------------------------
-template <bool FIRST, bool KV_BF16, int SM, bool MULTI>
+template <bool FIRST, bool KV_BF16, int SM, bool MULTI, int NT>
 __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   static_assert(SM == 32 || !MULTI, "runs of several tiles come with 32 runs");
-  constexpr uint32_t T = 64;
+  static_assert(NT == 64 || (NT == 32 && !MULTI), "runs of several tiles use 64-position tiles");
+  constexpr uint32_t T = NT, VP = NT / 8;  // positions per tile, per thread in the P.V layout
   // o_proj: with up to 16 runs, slots 16..31 take 64 rows each (4 per 16-thread row group), so
   // the attention runs (slots 0..15) carry no o_proj weights; with 32 runs every slot takes 32
   constexpr uint32_t ORR = SM <= 16 ? 4 : 2;
@@ -204,7 +208,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   // a run: its loads read 0 without touching memory): behind a branch, the wait counts of the
   // two paths would merge and every workgroup's q|k|v rows would wait for the tile.
   const size_t head_base = size_t(x) * p.max_seq * D;
-  KVTile<KV_BF16> A;
+  KVTile<KV_BF16, NT> A;
   __builtin_amdgcn_sched_barrier(0);
   const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
   const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
@@ -217,7 +221,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       const uint8_t* b = static_cast<const uint8_t*>(cache) + (head_base + size_t(r0) * D) * EL;
       return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(b), short(0), int(rows * D * EL), 0x00020000);
     };
-    load_tile_buf<KV_BF16>(A, run_rsrc(p.k_cache), run_rsrc(p.v_cache), 0, tid);
+    load_tile_buf<KV_BF16, NT>(A, run_rsrc(p.k_cache), run_rsrc(p.v_cache), 0, tid);
   }
   // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
@@ -314,10 +318,10 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
 #pragma unroll
     for (uint32_t j = 0; j < G; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    auto process = [&](const KVTile<KV_BF16>& X, uint32_t tile) __attribute__((always_inline)) {
+    auto process = [&](const KVTile<KV_BF16, NT>& X, uint32_t tile) __attribute__((always_inline)) {
       // scores s_t = (q . k_t) * scale (cpu_inference.rs:144-152); the new position's k is knew
 #pragma unroll
-      for (int u = 0; u < 2; u++) {
+      for (int u = 0; u < int(NT / 32); u++) {
         const uint32_t t = tile + uint32_t(pg + 32 * u);
         float4 k4[4];
         tile_k<KV_BF16>(X, u, k4);
@@ -346,13 +350,13 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       // softmax (cpu_inference.rs:217-223) as an online update: running max, rescaled sum
       if (wave < G) {
         const uint32_t j = wave;
-        const float xv = sc[j][lane];
+        const float xv = lane < T ? sc[j][lane] : -INFINITY;
         const float m_old = Ms[j];
         const float m_new = fmaxf(m_old, wave_max(xv));
         const float pe = xv == -INFINITY ? 0.f : expf(xv - m_new);
         const float c = m_old == -INFINITY ? 0.f : expf(m_old - m_new);
         const float tsum = wave_sum(pe);
-        pes[j][lane] = pe;
+        if (lane < T) pes[j][lane] = pe;
         if (lane == 0) {
           Ls[j] = Ls[j] * c + tsum;
           Ms[j] = m_new;
@@ -361,11 +365,11 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       }
       __syncthreads();
       // out += p_t * v_t (cpu_inference.rs:153-160); positions past the run add 0
-      float4 v4[8];
+      float4 v4[VP];
       const float4 vn = reinterpret_cast<const float4*>(vnew)[dg];
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const uint32_t t = tile + uint32_t(8 * pp + i);
+      for (int i = 0; i < int(VP); i++) {
+        const uint32_t t = tile + uint32_t(VP * pp + i);
         v4[i] = sel4(owns_new && t == pos, vn, tile_v<KV_BF16>(X, i));
         v4[i] = sel4(t < t1, v4[i], make_float4(0.f, 0.f, 0.f, 0.f));
       }
@@ -374,8 +378,8 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
         const float c = Cs[j];
         float4 o = make_float4(acc[j].x * c, acc[j].y * c, acc[j].z * c, acc[j].w * c);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-          const float pe = pes[j][8 * pp + i];
+        for (int i = 0; i < int(VP); i++) {
+          const float pe = pes[j][VP * pp + i];
           o.x += pe * v4[i].x;
           o.y += pe * v4[i].y;
           o.z += pe * v4[i].z;
@@ -388,7 +392,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     if constexpr (MULTI) {
       // runs of several tiles alternate between two register sets, so the next tile's loads are
       // in flight while one is computed (sc / pes / Cs are rewritten only after the next barrier)
-      KVTile<KV_BF16> B;
+      KVTile<KV_BF16, NT> B;
       for (uint32_t tile = t0;; tile += 2 * T) {
         const bool more = tile + T < t1;
         if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
@@ -498,13 +502,16 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       attention();
       if (s == 0 && tid == 0)
         __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      // done before the merge and o_proj: the run workgroups load pf region 1 (the rest of the
+      // MLP block's gate|up rows) while those finish
+      if (p.pf_run) fused_prefetch<1, 2>(p, x, s, splits);
       return;
     }
     if (!oproj) {
       // slots splits..15 are done once their q|k|v rows are out: they load the pf regions (this
       // layer's gate|up rows of XCD x) into the XCD's L2 for the MLP launch (fewer than 16 runs
       // are fewer than 1024 positions, where prefetching pays at any cache element type)
-      if (p.pf_idle && splits < 16) fused_prefetch(p, x, s - splits, 16 - splits);
+      if (p.pf_idle && splits < 16) fused_prefetch<0, 1>(p, x, s - splits, 16 - splits);
       return;
     }
     load_wo();
@@ -651,11 +658,15 @@ __global__ __launch_bounds__(256) void k_place_check(uint32_t* ids) {
 template <bool FIRST, bool KV_BF16>
 hipError_t launch_attn_sm(const FusedLayerParams& p, hipStream_t s) {
   const dim3 grid(NX * (NS + p.pf_wgs)), block(256);
-  if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false>), grid, block, 0, s, p);
-  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false>), grid, block, 0, s, p);
-  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false>), grid, block, 0, s, p);
-  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true>), grid, block, 0, s, p);
+  if (p.run == 32) {  // runs of one 32-position tile
+    if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 32>), grid, block, 0, s, p);
+    else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 32>), grid, block, 0, s, p);
+    else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 32>), grid, block, 0, s, p);
+  } else if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 64>), grid, block, 0, s, p);
+  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 64>), grid, block, 0, s, p);
+  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 64>), grid, block, 0, s, p);
+  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false, 64>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true, 64>), grid, block, 0, s, p);
   return hipGetLastError();
 }
 
@@ -671,7 +682,8 @@ bool common_ok(const FusedLayerParams& p) {
 hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s) {
   if (!common_ok(p) || !p.w_in || !p.w_qkv || !p.q_norm || !p.k_norm || !p.w_o || !p.qkv || !p.attn_part ||
       !p.k_cache || !p.v_cache || !p.rope_cur || p.max_seq == 0 || p.splits == 0 || p.splits > kFusedMaxRuns ||
-      (p.splits > 16 && p.splits != kFusedMaxRuns) || (p.splits <= 16 && p.run != 64) || p.run == 0 || p.run % 64)
+      (p.splits > 16 && p.splits != kFusedMaxRuns) || (p.splits <= 16 && p.run != 64 && p.run != 32) ||
+      (p.splits > 16 && (p.run == 0 || p.run % 64)))
     return hipErrorInvalidValue;
   if (first_layer ? (!p.embed || !p.tokens || p.vocab == 0) : (!p.res_in || !p.part_in)) return hipErrorInvalidValue;
   if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true>(p, s) : launch_attn_sm<true, false>(p, s);

@@ -212,6 +212,8 @@ struct FusedLayerParams {
   // the attention block's slots without a run or o_proj rows load the pf regions once their
   // q|k|v rows are out
   int pf_idle;
+  // the workgroups of the runs load pf region 1 once their partials are out
+  int pf_run;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->

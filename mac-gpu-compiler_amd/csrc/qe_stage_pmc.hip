@@ -305,6 +305,7 @@ int main(int argc, char** argv) {
       }
       CK(qe::launch_fused_attn(f, false, s));
       f.pf_idle = 0;
+      f.pf_run = 0;
       for (auto& r : f.pf) r = qe::FusedPrefetch{};
       f.res_in = res1; f.part_in = part_attn; f.res_out = res0; f.part_out = part_mlp;
       CK(qe::launch_fused_mlp(f, s));
