@@ -146,6 +146,9 @@ struct qe_model {
   // attention runs of 32 positions up to this many cached positions (QE_FUSED_RUN32; a multiple
   // of 64, at most 512: 16 runs)
   uint64_t fused_run32 = 256;
+  // each MLP block's workgroups load the next layer's q|k|v rows that their slot of the next
+  // attention block reads into their XCD's L2 (QE_FUSED_PF_QKV=0: off)
+  bool fused_pf_qkv = true;
   uint8_t* scratch = nullptr;
   // pinned host staging
   float* h_logits = nullptr;
@@ -468,6 +471,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* v = getenv("QE_FUSED_PF_MLP")) m->fused_pf_mlp = uint32_t(std::min(std::max(atoi(v), 0), 64));
   if (const char* v = getenv("QE_FUSED_PF_IDLE")) m->fused_pf_idle = strcmp(v, "0") != 0;
   if (const char* v = getenv("QE_FUSED_PF_RUN")) m->fused_pf_run = strcmp(v, "0") != 0;
+  if (const char* v = getenv("QE_FUSED_PF_QKV")) m->fused_pf_qkv = strcmp(v, "0") != 0;
   if (const char* v = getenv("QE_FUSED_RUN32")) m->fused_run32 = uint64_t(std::min(std::max(atoi(v), 0), 512)) / 64 * 64;
   // the layers' tensors sit at one stride in the arena (the persistent launch finds layer l's from
   // layer 0's)
@@ -675,6 +679,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     f.pf_wgs = m->fused_pf_attn;
     f.pf_idle = 0;
     f.pf_run = 0;
+    f.qkv_next = nullptr;
     if (f.pf_wgs) {
       f.pf[0] = qe::FusedPrefetch{bytes(w.w_gu), 2 * I / NX * H * 2, 2 * I / NX * H * 2, 0, 1};
       f.pf[1] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
@@ -703,6 +708,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     f.pf_idle = 0;
     f.pf_run = 0;
     f.pf_wgs = l + 1 < c.num_hidden_layers ? m->fused_pf_mlp : 0;
+    f.qkv_next = l + 1 < c.num_hidden_layers && m->fused_pf_qkv ? m->layers[l + 1].w_qkv : nullptr;
     if (f.pf_wgs) {
       const Layer& n = m->layers[l + 1];
       const uint32_t G = QD / KD;

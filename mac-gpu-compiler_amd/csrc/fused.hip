@@ -167,6 +167,14 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   __shared__ float mw[G][SM], msum[G];  // merge weights of the runs and their sums per head
 
   const uint32_t tag = *gen_word(p.sync, x) + 1;
+  // this step's position (set before the step's first launch), read now so that no load of it
+  // waits behind the attention's polls. It is read as a per-lane value (the offset comes from an
+  // asm statement, which the compiler takes as varying across lanes): a uniform value would be
+  // moved to a scalar register right after the load, and the wave would wait for it there
+  // instead of issuing its weight loads.
+  uint32_t lane_zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(lane_zero));
+  const uint32_t pos_step = (&p.state->pos)[lane_zero];
 
   // ---- loads that depend on no other workgroup, issued before any use ----
   // the residual stream (from the previous launch) or the embedding row
@@ -272,7 +280,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     }
     float a = __uint_as_float(qa.x), b = __uint_as_float(qb.x);
 
-    const uint32_t pos = p.state->pos;
+    const uint32_t pos = pos_step;
     const bool bad = pos >= p.max_seq;
     if (bad && x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
     uint32_t n = bad ? 0u : pos + 1;
@@ -309,7 +317,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     if (owns_new) {  // append the new K/V row (cpu_inference.rs:140-141)
       const size_t slot = head_base + size_t(pos) * D + (tid & (D - 1));
       const float val = tid < D ? knew[tid] : vnew[tid - D];
-      void* cache = tid < D ? p.k_cache : p.v_cache;
+      void* cache = wave < 2 ? p.k_cache : p.v_cache;  // (threads tid < D: waves 0 and 1)
       if (KV_BF16) static_cast<uint16_t*>(cache)[slot] = f32_to_bf16(val);
       else static_cast<float*>(cache)[slot] = val;
     }
@@ -546,6 +554,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   float4 xp[NX];
 #pragma unroll
   for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(p.part_in + g * H)[tid];
+  __builtin_amdgcn_sched_barrier(0);  // the residual's loads first: loads complete in issue order
   // gate|up: rows 768 x + 24 s + 6 wave + r (pairs (gate_i, up_i) interleaved), lane l holds
   // chunks l and l + 64
   const uint4* Wg = reinterpret_cast<const uint4*>(p.w_gu);
@@ -569,6 +578,15 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
 #pragma unroll
     for (int k = 0; k < 3; k++) wd[r][k] = Wd[size_t(32 * s + 2 * rg + r) * (I / 8) + 48 * x + t16 + 16 * k];
   }
+  // the next layer's q|k|v rows that slot s of its attention block reads (16 rows of 2 KB: 512
+  // 64-byte half lines) into XCD x's L2, one word of half lines tid and tid + 256, through a
+  // descriptor that holds no bytes for the last layer (its loads then read 0 without touching
+  // memory; a branch here would make the waits after it wait for every load)
+  const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv_next ? p.qkv_next + size_t(qkv_row0(x, s)) * H : p.w_gu,
+                                            p.qkv_next ? 16 * H * 2 : 0);
+  uint32_t pfw[2];
+#pragma unroll
+  for (int k = 0; k < 2; k++) pfw[k] = __builtin_amdgcn_raw_buffer_load_b32(rq, int((tid + 256 * k) * 64), 0, 0);
   __builtin_amdgcn_sched_barrier(0);
 
   // post_attention_layernorm + gate|up + silu * up (cpu_inference.rs:167-170)
@@ -625,6 +643,9 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
 #pragma unroll
     for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha, hb, da[r]);
   }
+  // keeps the prefetch loads: they were issued after down's weights, which are in by now (a wait
+  // for them after this wave's next store would also wait for that store)
+  asm volatile("" ::"v"(pfw[0] ^ pfw[1]));
 #pragma unroll
   for (int r = 0; r < 2; r++) da[r] = sum16(da[r]);
   if (t16 == 0) {

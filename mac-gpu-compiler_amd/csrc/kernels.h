@@ -214,6 +214,9 @@ struct FusedLayerParams {
   int pf_idle;
   // the workgroups of the runs load pf region 1 once their partials are out
   int pf_run;
+  // MLP block: the next layer's q|k|v rows [QD + 2 KD][H] (null: none); workgroup (x, s) loads
+  // the rows that slot s of the next attention block reads into XCD x's L2
+  const uint16_t* qkv_next;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
