@@ -439,7 +439,7 @@ int qe_model_load(const char* path, qe_model** out) {
                s_err = stake(4), s_res0 = stake(H * 4), s_res1 = stake(H * 4),
                s_pa = stake(qe::kFusedXcds * H * 4), s_pm = stake(qe::kFusedXcds * H * 4),
                s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4),
-               s_fqkv = stake(qe::kFusedQkvPairs * 8), s_fh = stake(qe::kFusedHPairs * 8),
+               s_fqkv = stake((qe::kFusedQkvPairs + qe::kFusedAttPairs) * 8), s_fh = stake(qe::kFusedHPairs * 8),
                s_pxa = stake(qe::kFusedXcds * H * 8), s_pxm = stake(qe::kFusedXcds * H * 8),
                s_ppa = stake(qe::kFusedXcds * H * 8), s_ppm = stake(qe::kFusedXcds * H * 8), s_pgen = stake(256);
   static_assert(qe::kFusedPartPairs * 8 <= size_t(qe::kFusedKv) * qe::kAttnMaxWideSplits * 2 * qe::kPartStride * 4,

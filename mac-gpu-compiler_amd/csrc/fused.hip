@@ -437,13 +437,64 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
 
   // ---- merge of the runs, then o_proj ----
   // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
-  // slots past the last run weigh 0. Wave 0 takes the (m, l) of every run (lane u: head u / SM,
-  // run u % SM) and leaves the weights e_s and the sums in LDS; then thread (head 2x + tid / 128,
-  // dim tid % 128) adds up its acc values.
+  // slots past the last run weigh 0.
   auto merge_oproj = [&]() __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride,
                                               uint32_t(kFusedMaxRuns * G * kPartStride * 8));
-    // one poll round trip for both: wave 0's (m, l) pairs and every thread's acc values
+    if constexpr (SM == 32) {
+      // 32 runs, all 32 slots with o_proj rows: in two rounds. Slot s merges the 8 values
+      // [8 s, 8 s + 8) of the XCD's 256 (head j1 = s / 16): thread t takes run t / 8, value t % 8,
+      // wave 0 lanes 0..31 the (m, l) of the 32 runs; the 8 merged values go out as pairs after the
+      // q|k|v pairs, and every slot then gathers the 256 (one per thread), instead of each slot
+      // polling 32 pairs per thread of every run.
+      const uint32_t j1 = s >> 4, q = tid >> 3, e = tid & 7;
+      const uint32_t d1 = 8 * (s & 15) + e;
+      const bool live = wave == 0 && lane < 32 && lane < splits;
+      uint4 ml = make_uint4(0u, 0u, 0u, 0u);
+      uint2 a1;
+      for (uint32_t spins = 0;;) {
+        if (wave == 0) ml = ld_pair2(rp, (min(lane & 31u, splits - 1) * G + j1) * kPartStride);
+        a1 = ld_pair(rp, (min(q, splits - 1) * G + j1) * kPartStride + 4 + d1);
+        const bool ok = (!live || (ml.y == tag && ml.w == tag)) && a1.y == tag;
+        if (poll_done(ok, spins, p.err)) break;
+      }
+      if (wave == 0) {
+        const float m = live ? __uint_as_float(ml.x) : -INFINITY;
+        float M = m;
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
+        const float w = m != -INFINITY ? expf(m - M) : 0.f;
+        float L = w * (live ? __uint_as_float(ml.z) : 0.f);
+#pragma unroll
+        for (int o = 1; o < 32; o <<= 1) L += __shfl_xor(L, o);
+        if (lane < 32) mw[0][lane] = w;
+        if (lane == 0) msum[0] = L;
+      }
+      __syncthreads();
+      // sum over the runs: lanes 8 r + e of a wave (its 8 runs), then the 4 waves in LDS
+      float c = q < splits ? mw[0][q] * __uint_as_float(a1.x) : 0.f;
+      c += __shfl_xor(c, 8);
+      c += __shfl_xor(c, 16);
+      c += __shfl_xor(c, 32);
+      if (lane < 8) red[wave][0][lane] = c;
+      __syncthreads();
+      uint2* ax = p.qkv + kFusedQkvPairs + size_t(x) * (G * D);
+      if (tid < 8) {
+        const float v = ((red[0][0][tid] + red[1][0][tid]) + (red[2][0][tid] + red[3][0][tid])) * (1.0f / msum[0]);
+        ax[8 * s + tid] = pair(v, tag);
+      }
+      const __amdgpu_buffer_rsrc_t ra = rsrc_of(ax, G * D * 8);
+      uint2 av1;
+      for (uint32_t spins = 0;;) {
+        av1 = ld_pair(ra, tid);
+        if (poll_done(av1.y == tag, spins, p.err)) break;
+      }
+      att[tid] = __uint_as_float(av1.x);
+      __syncthreads();
+    } else {
+    // Wave 0 takes the (m, l) of every run (lane u: head u / SM, run u % SM) and leaves the
+    // weights e_s and the sums in LDS; then thread (head 2x + tid / 128, dim tid % 128) adds up its
+    // acc values. One poll round trip for both: wave 0's (m, l) pairs and every thread's acc values.
     const uint32_t j = tid >> 7, d = tid & 127;
     const uint32_t jh = min(lane / SM, G - 1), u = lane % SM;
     const bool live = wave == 0 && lane < G * SM && u < splits;
@@ -481,6 +532,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
       att[tid] = Av * (1.0f / msum[j]);
     }
     __syncthreads();
+    }
     // o_proj over this XCD's 256 columns (cpu_inference.rs:163-164): the partial of rows orow0..;
     // the next launch adds the 8 partials and the residual
     const float4* at4 = reinterpret_cast<const float4*>(att);

@@ -160,6 +160,8 @@ constexpr uint32_t kFusedLineWords = 32;
 constexpr size_t kFusedSyncWords = size_t(kFusedXcds) * kFusedLineWords;
 // exchange buffers, in (value, tag) pairs
 constexpr size_t kFusedQkvPairs = size_t(kFusedHeads + 2 * kFusedKv) * kHeadDim;
+// ... followed by the merged attention output of each XCD ([8][G * 128] pairs) of a 32-run step
+constexpr size_t kFusedAttPairs = size_t(kFusedHeads) * kHeadDim;
 constexpr size_t kFusedPartPairs = size_t(kFusedKv) * kFusedMaxRuns * (kFusedHeads / kFusedKv) * kPartStride;
 constexpr size_t kFusedHPairs = kFusedI;
 
@@ -189,7 +191,7 @@ struct FusedLayerParams {
   float* res_out;           // x, written by workgroup 0 for the next launch
   float* part_out;          // [8][H]: this launch's o_proj (or down) output, one slice per XCD
   // exchanged inside one XCD during a launch, as (value bits, tag) pairs
-  uint2* qkv;               // [kFusedQkvPairs] raw projections
+  uint2* qkv;               // [kFusedQkvPairs] raw projections, then [kFusedAttPairs] merged heads
   uint2* attn_part;         // [kFusedPartPairs]: [8][kFusedMaxRuns][G][kPartStride]
   uint2* h;                 // [kFusedHPairs] silu(gate) * up
   const uint16_t* embed;

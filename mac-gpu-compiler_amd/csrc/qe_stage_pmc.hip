@@ -274,13 +274,13 @@ int main(int argc, char** argv) {
     float* res1 = dalloc<float>(H);
     float* part_attn = dalloc<float>(size_t(NX) * H);
     float* part_mlp = dalloc<float>(size_t(NX) * H);
-    uint2* fqkv = dalloc<uint2>(qe::kFusedQkvPairs);
+    uint2* fqkv = dalloc<uint2>(qe::kFusedQkvPairs + qe::kFusedAttPairs);
     uint2* fpart = dalloc<uint2>(qe::kFusedPartPairs);
     uint2* fh = dalloc<uint2>(qe::kFusedHPairs);
     uint32_t* fsync = dalloc<uint32_t>(qe::kFusedSyncWords);
     k_fill_f32<<<4, 256, 0, s>>>(res0, H, 0.5f);
     CK(hipMemsetAsync(part_mlp, 0, size_t(NX) * H * 4, s));
-    CK(hipMemsetAsync(fqkv, 0, qe::kFusedQkvPairs * 8, s));
+    CK(hipMemsetAsync(fqkv, 0, (qe::kFusedQkvPairs + qe::kFusedAttPairs) * 8, s));
     CK(hipMemsetAsync(fpart, 0, qe::kFusedPartPairs * 8, s));
     CK(hipMemsetAsync(fh, 0, qe::kFusedHPairs * 8, s));
     CK(hipMemsetAsync(fsync, 0, qe::kFusedSyncWords * 4, s));
