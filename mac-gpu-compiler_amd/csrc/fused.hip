@@ -48,6 +48,11 @@
 #include "l2_prefetch.h"
 #include "xcd_exchange.h"
 
+// attention blocks with at least this many runs merge them in two rounds (below)
+#ifndef QE_MERGE2_MIN_SM
+#define QE_MERGE2_MIN_SM 8
+#endif
+
 namespace qe {
 namespace {
 
@@ -441,47 +446,49 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   auto merge_oproj = [&]() __attribute__((always_inline)) {
     const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride,
                                               uint32_t(kFusedMaxRuns * G * kPartStride * 8));
-    if constexpr (SM == 32) {
-      // 32 runs, all 32 slots with o_proj rows: in two rounds. Slot s merges the 8 values
-      // [8 s, 8 s + 8) of the XCD's 256 (head j1 = s / 16): thread t takes run t / 8, value t % 8,
-      // wave 0 lanes 0..31 the (m, l) of the 32 runs; the 8 merged values go out as pairs after the
-      // q|k|v pairs, and every slot then gathers the 256 (one per thread), instead of each slot
-      // polling 32 pairs per thread of every run.
-      const uint32_t j1 = s >> 4, q = tid >> 3, e = tid & 7;
-      const uint32_t d1 = 8 * (s & 15) + e;
-      const bool live = wave == 0 && lane < 32 && lane < splits;
+    if constexpr (SM >= QE_MERGE2_MIN_SM) {
+      // In two rounds. The OW slots with o_proj rows (all 32 with 32 runs, else slots 16..31)
+      // each merge VW = 256 / OW of the XCD's 256 values (head j1) over the runs: thread t takes
+      // run t / VW, value t % VW, wave 0 lanes 0..SM-1 the (m, l) of the runs; the merged values go
+      // out as pairs after the q|k|v pairs, and every o_proj slot then gathers the 256 (one per
+      // thread), instead of each polling SM pairs per thread of every run.
+      constexpr uint32_t OW = SM <= 16 ? 16 : 32, VW = G * D / OW;
+      const uint32_t o = SM <= 16 ? s - 16 : s;
+      const uint32_t q = tid / VW, e = tid % VW, j1 = (VW * o) / D;
+      const uint32_t d1 = (VW * o) % D + e;
+      const bool live = wave == 0 && lane < SM && lane < splits;
+      const bool mine = q < SM && q < splits;
       uint4 ml = make_uint4(0u, 0u, 0u, 0u);
-      uint2 a1;
+      uint2 a1 = make_uint2(0u, 0u);
       for (uint32_t spins = 0;;) {
-        if (wave == 0) ml = ld_pair2(rp, (min(lane & 31u, splits - 1) * G + j1) * kPartStride);
+        if (wave == 0) ml = ld_pair2(rp, (min(lane, splits - 1) * G + j1) * kPartStride);
         a1 = ld_pair(rp, (min(q, splits - 1) * G + j1) * kPartStride + 4 + d1);
-        const bool ok = (!live || (ml.y == tag && ml.w == tag)) && a1.y == tag;
+        const bool ok = (!live || (ml.y == tag && ml.w == tag)) && (!mine || a1.y == tag);
         if (poll_done(ok, spins, p.err)) break;
       }
       if (wave == 0) {
         const float m = live ? __uint_as_float(ml.x) : -INFINITY;
         float M = m;
 #pragma unroll
-        for (int o = 1; o < 32; o <<= 1) M = fmaxf(M, __shfl_xor(M, o));
-        const float w = m != -INFINITY ? expf(m - M) : 0.f;
-        float L = w * (live ? __uint_as_float(ml.z) : 0.f);
+        for (int w = 1; w < int(SM); w <<= 1) M = fmaxf(M, __shfl_xor(M, w));
+        const float wt = m != -INFINITY ? expf(m - M) : 0.f;
+        float L = wt * (live ? __uint_as_float(ml.z) : 0.f);
 #pragma unroll
-        for (int o = 1; o < 32; o <<= 1) L += __shfl_xor(L, o);
-        if (lane < 32) mw[0][lane] = w;
+        for (int w = 1; w < int(SM); w <<= 1) L += __shfl_xor(L, w);
+        if (lane < SM) mw[0][lane] = wt;
         if (lane == 0) msum[0] = L;
       }
       __syncthreads();
-      // sum over the runs: lanes 8 r + e of a wave (its 8 runs), then the 4 waves in LDS
-      float c = q < splits ? mw[0][q] * __uint_as_float(a1.x) : 0.f;
-      c += __shfl_xor(c, 8);
-      c += __shfl_xor(c, 16);
-      c += __shfl_xor(c, 32);
-      if (lane < 8) red[wave][0][lane] = c;
+      // sum over the runs: the lanes of a wave with the same value index, then the 4 waves in LDS
+      float c = mine ? mw[0][q] * __uint_as_float(a1.x) : 0.f;
+#pragma unroll
+      for (uint32_t w = VW; w < 64; w <<= 1) c += __shfl_xor(c, w);
+      if (lane < VW) red[wave][0][lane] = c;
       __syncthreads();
       uint2* ax = p.qkv + kFusedQkvPairs + size_t(x) * (G * D);
-      if (tid < 8) {
+      if (tid < VW) {
         const float v = ((red[0][0][tid] + red[1][0][tid]) + (red[2][0][tid] + red[3][0][tid])) * (1.0f / msum[0]);
-        ax[8 * s + tid] = pair(v, tag);
+        ax[VW * o + tid] = pair(v, tag);
       }
       const __amdgpu_buffer_rsrc_t ra = rsrc_of(ax, G * D * 8);
       uint2 av1;
