@@ -48,6 +48,9 @@
 #include "l2_prefetch.h"
 #include "xcd_exchange.h"
 
+#ifndef QE_PF32
+#define QE_PF32 1
+#endif
 // attention blocks with at least this many runs merge them in two rounds (below)
 #ifndef QE_MERGE2_MIN_SM
 #define QE_MERGE2_MIN_SM 8
@@ -440,6 +443,9 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     }
   };
 
+  // words of the MLP block's gate|up rows that 32-run slots load while the runs finish (below)
+  uint32_t gpf[3] = {0u, 0u, 0u};
+
   // ---- merge of the runs, then o_proj ----
   // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
   // slots past the last run weigh 0.
@@ -497,6 +503,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
         if (poll_done(av1.y == tag, spins, p.err)) break;
       }
       att[tid] = __uint_as_float(av1.x);
+      asm volatile("" ::"v"(gpf[0] ^ gpf[1] ^ gpf[2]));  // (in: the polls waited for every load)
       __syncthreads();
     } else {
     // Wave 0 takes the (m, l) of every run (lane u: head u / SM, run u % SM) and leaves the
@@ -585,6 +592,15 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     merge_oproj();
   } else {
     attention();
+#if QE_PF32
+    // slot s's partial is out and the merge waits for the slowest run: load the 24 gate|up rows
+    // of MLP slot s on this XCD (48 KB, one word of each 64-byte half line) into its L2
+    {
+      const uint8_t* gb = reinterpret_cast<const uint8_t*>(p.w_gu + size_t((2 * I / NX) * x + 24 * s) * H);
+#pragma unroll
+      for (int k = 0; k < 3; k++) gpf[k] = *reinterpret_cast<const uint32_t*>(gb + (tid + 256 * k) * 64);
+    }
+#endif
     merge_oproj();
     if (s == 0 && tid == 0)
       __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
