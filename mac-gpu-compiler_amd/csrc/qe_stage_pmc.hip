@@ -267,9 +267,19 @@ int main(int argc, char** argv) {
       std::fprintf(stderr, "qe_stage_pmc: workgroups are not dealt to the XCDs round-robin; no fused launches\n");
       return 2;
     }
+    // the engine's step shape (step_shape): runs of 32 positions up to 256 cached positions, then
+    // runs of 64 (4, 8, 16 or 32 per KV head), then 32 runs of a whole number of 64-position tiles
     const uint32_t NX = qe::kFusedXcds, n = pos + 1, R = qe::kFusedMaxRuns;
-    const uint32_t run = 64 * ((n + 64 * R - 1) / (64 * R)), active = (n + run - 1) / run;
-    const uint32_t fsplits = run > 64 ? R : active <= 4 ? 4 : active <= 8 ? 8 : active <= 16 ? 16 : R;
+    uint32_t run, fsplits;
+    if (n <= 256) {
+      run = 32;
+      const uint32_t active = (n + 31) / 32;
+      fsplits = active <= 4 ? 4 : active <= 8 ? 8 : 16;
+    } else {
+      run = 64 * ((n + 64 * R - 1) / (64 * R));
+      const uint32_t active = (n + run - 1) / run;
+      fsplits = run > 64 ? R : active <= 4 ? 4 : active <= 8 ? 8 : active <= 16 ? 16 : R;
+    }
     float* res0 = dalloc<float>(H);
     float* res1 = dalloc<float>(H);
     float* part_attn = dalloc<float>(size_t(NX) * H);
@@ -296,17 +306,26 @@ int main(int argc, char** argv) {
       const uint16_t* Wc = W + per_copy * (it % 4);
       f.w_qkv = Wc; f.w_o = Wc + n_qkv; f.w_gu = Wc + n_qkv + n_o; f.w_down = Wc + n_qkv + n_o + n_gu;
       f.res_in = res0; f.part_in = part_mlp; f.res_out = res1; f.part_out = part_attn;
+      f.qkv_next = nullptr;
       if (pf_idle && fsplits < 16) {  // the engine's rule: the attention block's idle slots load the
-        // first 2 (16 - runs) of each MLP workgroup's 24 gate|up rows of their XCD
+        // first 2 (16 - runs) of each MLP workgroup's 24 gate|up rows of their XCD, the run slots
+        // the rest once their partials are out
         const uint8_t* gu = reinterpret_cast<const uint8_t*>(f.w_gu);
         const uint32_t rows = std::min(2 * (16 - fsplits), 24u);
         f.pf[0] = qe::FusedPrefetch{gu, 2 * I / NX * H * 2, rows * H * 2, 24 * H * 2, qe::kFusedSlots};
         f.pf_idle = 1;
+        if (rows < 24) {
+          f.pf[1] = qe::FusedPrefetch{gu + size_t(rows) * H * 2, 2 * I / NX * H * 2, (24 - rows) * H * 2, 24 * H * 2,
+                                      qe::kFusedSlots};
+          f.pf_run = 1;
+        }
       }
       CK(qe::launch_fused_attn(f, false, s));
       f.pf_idle = 0;
       f.pf_run = 0;
       for (auto& r : f.pf) r = qe::FusedPrefetch{};
+      // ... and the MLP block loads the next layer's q|k|v rows (the next weight copy's)
+      if (pf_idle) f.qkv_next = W + per_copy * ((it + 1) % 4);
       f.res_in = res1; f.part_in = part_attn; f.res_out = res0; f.part_out = part_mlp;
       CK(qe::launch_fused_mlp(f, s));
       CK(hipStreamSynchronize(s));

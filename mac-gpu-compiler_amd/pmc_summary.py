@@ -70,7 +70,8 @@ def main():
                     help="the counter runs used qe_stage_pmc --no-prefetch (attention without the L2 prefetch)")
     ap.add_argument("--fused", action="store_true", help="the counter runs used qe_stage_pmc --fused")
     ap.add_argument("--pf-idle", action="store_true",
-                    help="... --fused --pf-idle: the attention block's idle workgroups load the MLP block's gate|up rows")
+                    help="... --fused --pf-idle: the attention block's idle and run workgroups load the MLP block's gate|up"
+                         " rows, the MLP block the next layer's q|k|v rows")
     ap.add_argument("--l2", default=None, help="counter CSV of TCC_HIT_sum, TCC_MISS_sum, TCC_EA0_RDREQ_sum")
     ap.add_argument("--persist-log", default=None, help="output of qe_stage_pmc --l2-persist (timings, no counters)")
     a = ap.parse_args()
@@ -112,10 +113,16 @@ def main():
         wk = sum(d["write_kib"]) / len(d["write_kib"])
         traffic = (fk * ff + wk * fw) * 1024.0
         extra = pf if st == "attention" else 0
+        cfg = qe.QWEN3_0_6B
         if a.pf_idle and st == "attn_block":
-            # with 4 runs (up to 256 positions) all 24 gate|up rows of each MLP workgroup
-            cfg = qe.QWEN3_0_6B
-            extra = 2 * cfg.intermediate_size * cfg.hidden_size * 2 if a.attn_pos < 256 else 0
+            # with fewer than 16 runs (up to 1024 positions) the idle and run slots load all 24
+            # gate|up rows of each MLP workgroup
+            extra = 2 * cfg.intermediate_size * cfg.hidden_size * 2 if a.attn_pos < 1024 else 0
+        if a.pf_idle and st == "mlp_block":
+            # the MLP block loads the next layer's q|k|v rows
+            qd = cfg.num_attention_heads * cfg.head_dim
+            kd = cfg.num_key_value_heads * cfg.head_dim
+            extra = (qd + 2 * kd) * cfg.hidden_size * 2
         out["stages"][st] = {
             "kernel": d["kernel"],
             "dispatches": len(d["fetch_kib"]),
@@ -164,8 +171,9 @@ def main():
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
         "for attention (the figures `bench.py` divides by the launch time)." +
-        (" The attention block's idle workgroups also load the MLP block's gate|up rows into L2 (prefetch bytes;"
-         " its ratio is traffic over own + prefetch bytes)." if a.pf_idle else "") +
+        (" The attention block's idle and run workgroups also load the MLP block's gate|up rows into L2, and the"
+         " MLP block the next layer's q|k|v rows (prefetch bytes; the ratio is traffic over own + prefetch bytes)."
+         if a.pf_idle else "") +
         ("" if a.no_prefetch else " The attention launch also streams the layer's gate/up and down weights into"
          " L2 (prefetch bytes, counted with those stages); its ratio is traffic over own + prefetch bytes."),
         "",
