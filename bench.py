@@ -432,6 +432,60 @@ def lookup_bench(qe, model, cfg, args):
     return res
 
 
+def other_configs(torch, qe, model, cfg, ceiling: float, args) -> dict:
+    """Short runs of the other workloads, so that one default `bench.py` run also measures them
+    (outside the timed decode): the isolated matvec and attention sweeps (100 launches per shape
+    instead of 1000), the 4096-step decode with an f32 cache (one untimed decode that captures its
+    step graphs, then one timed), its tokens against the oracle's committed run, and the
+    2048-token chunked prefill with the k = 4 verify."""
+    import numpy as np
+    out = {}
+    t0 = time.time()
+    # config 5 first: the two-stream chunked prefill runs slower once this process has run the
+    # sweeps' launches on torch's streams (13.3 vs 11.0 ms for 2048 tokens in chunks of 512; the
+    # streams then share hardware queues)
+    pf = prefill_bench(torch, qe, model, cfg, args)
+    out["prefill"] = {k: pf[k] for k in ("ms", "value", "chunk", "achieved_tflops_algorithmic", "mfma_tflops_issued",
+                                         "one_chunk_ms", "verify_k4_ms", "verify_greedy_k4_ms", "forward_1_ms")
+                      if k in pf}
+    mv = sweep_matvec(torch, qe, ceiling, 100)
+    out["matvec_sweep"] = {f"{r['in']}->{r['out']}" + (" (tp8 shard)" if r["tp8_shard"] else ""):
+                           {"us": r["us"], "gb_s": r["gb_s"], "frac_of_measured": r["frac_of_measured"]} for r in mv}
+    at = sweep_attention(torch, qe, ceiling, 100)
+    out["attention_sweep"] = {str(r["positions"]): {k: r[k] for k in ("split", "single_pass")} for r in at}
+    # config 4: 4096 greedy steps after the 130-token prompt, f32 cache
+    P, DS = PROMPT_LEN, 4096
+    prompt = qe.random_prompt(PROMPT_SEED, P, cfg.vocab_size)
+    cache = qe.KVCache(model, P + DS + 1, qe.QE_KV_F32)
+    first = int(np.argmax(model.prefill(prompt, 0, cache)))
+    model.decode(first, P, DS, cache)
+    torch.cuda.synchronize()
+    gaps, last = [], [time.perf_counter()]
+
+    def on_token(_t):
+        now = time.perf_counter()
+        gaps.append(now - last[0])
+        last[0] = now
+
+    t1 = time.perf_counter()
+    last[0] = t1
+    toks, _ = model.decode(first, P, DS, cache, on_token=on_token)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t1
+    got = [first] + toks
+    fx = os.path.join(ROOT, "tests", "golden", "qwen3_0_6b_long_f32.npz")
+    ref = [int(t) for t in np.load(fx, allow_pickle=False)["tokens"]] if os.path.exists(fx) else []
+    n = min(len(ref), len(got))
+    out["long_decode_f32"] = {
+        "tok_s": round(DS / wall, 1),
+        "by_position": [by_position(gaps, P, 512)[i] for i in (0, -1)],
+        "parity_vs_oracle_fixture": {"compared": n, "first_divergence": next((i for i in range(n) if got[i] != ref[i]), None)}
+        if ref else None}
+    del cache
+    out["seconds"] = round(time.time() - t0, 1)
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -458,6 +512,9 @@ def main():
                          "history_<chip>_<prompt>.jsonl here, in the reference harness's format")
     ap.add_argument("--label", default="", help="label stored in the --results record")
     ap.add_argument("--prompt-name", default="random130", help="prompt name in the --results file names")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="decode mode: skip the short runs of the other workloads (sweeps, 4096-step decode, "
+                         "prefill) that the default run adds as other_configs")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -693,6 +750,8 @@ def main():
         "weight_bytes_per_token": weight_bytes,
         "parity_vs_oracle_fixture": parity,
     }
+    if not args.no_other_configs and DS == 128 and P == PROMPT_LEN and args.kv == "f32":
+        result["other_configs"] = other_configs(torch, qe, model, cfg, ceiling, args)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(ckpt, prompt)
     if args.results:
