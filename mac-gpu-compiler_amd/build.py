@@ -44,7 +44,11 @@ def hipcc() -> str:
 # Per-source additions. batch.hip: matrix-core results go to ordinary VGPRs, where the MFMAs
 # accumulate in place; with the default accumulation registers the compiler moves the GEMM
 # accumulators between register files on every k stage.
-SOURCE_FLAGS = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+SOURCE_FLAGS = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+                # fused.hip: the leading pointer arguments of the two-launch layer's kernels go
+                # into scalar registers at wave launch (up to 14 dwords), so their first loads do
+                # not wait for a load of the argument block
+                "fused.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
 
 OBJ_DIR = os.path.join(PKG, "_build")
 # the host pass warns that it does not know the packed-fp32 feature; that is expected

@@ -141,8 +141,12 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
 // MULTI: runs of more than one 64-position tile (only with 32 runs), NT: positions per tile and
 // per single-tile run (64, or 32 for short contexts: half the K/V each run's CU takes in).
 // ---------------------------------------------------------------------------------------------
+// The arguments the first loads need come first, as plain pointers (preloaded into scalar
+// registers at wave launch, as in k_fused_mlp).
 template <bool FIRST, bool KV_BF16, int SM, bool MULTI, int NT>
-__global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
+__global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepState* state, const float* res_in,
+                                                    const float* part_in, const uint16_t* w_qkv, const uint16_t* w_in,
+                                                    uint32_t n_runs, uint32_t run_len, FusedLayerParams p) {
   static_assert(SM == 32 || !MULTI, "runs of several tiles come with 32 runs");
   static_assert(NT == 64 || (NT == 32 && !MULTI), "runs of several tiles use 64-position tiles");
   constexpr uint32_t T = NT, VP = NT / 8;  // positions per tile, per thread in the P.V layout
@@ -153,12 +157,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t x = fused_xcd(p.err);
   if (blockIdx.x >= NX * NS) {  // a prefetch workgroup (the whole workgroup)
-    if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
+    if (state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
   const uint32_t s = blockIdx.x / NX;
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
-  const uint32_t splits = max(p.splits, 1u);
+  const uint32_t splits = max(n_runs, 1u);
   const bool attn = s < splits;  // this workgroup also runs attention run s of KV head x
   const bool oproj = SM <= 16 ? s >= 16 : true;
   const uint32_t orow0 = SM <= 16 ? 64 * (s - 16) : 32 * s;
@@ -174,7 +178,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   __shared__ __align__(16) float att[G * D];
   __shared__ float mw[G][SM], msum[G];  // merge weights of the runs and their sums per head
 
-  const uint32_t tag = *gen_word(p.sync, x) + 1;
+  const uint32_t tag = *gen_word(sync, x) + 1;
   // this step's position (set before the step's first launch), read now so that no load of it
   // waits behind the attention's polls. It is read as a per-lane value (the offset comes from an
   // asm statement, which the compiler takes as varying across lanes): a uniform value would be
@@ -182,14 +186,14 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   // instead of issuing its weight loads.
   uint32_t lane_zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(lane_zero));
-  const uint32_t pos_step = (&p.state->pos)[lane_zero];
+  const uint32_t pos_step = (&state->pos)[lane_zero];
 
   // ---- loads that depend on no other workgroup, issued before any use ----
   // the residual stream (from the previous launch) or the embedding row
   float4 xin;
   float4 xp[NX];
   if constexpr (FIRST) {
-    uint32_t tok = p.tokens[p.state->tok_idx];
+    uint32_t tok = p.tokens[state->tok_idx];
     if (tok >= p.vocab) {
       if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
       tok = 0;
@@ -199,12 +203,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
 #pragma unroll
     for (uint32_t g = 0; g < NX; g++) xp[g] = make_float4(0.f, 0.f, 0.f, 0.f);
   } else {
-    xin = reinterpret_cast<const float4*>(p.res_in)[tid];
+    xin = reinterpret_cast<const float4*>(res_in)[tid];
 #pragma unroll
-    for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(p.part_in + g * H)[tid];
+    for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
   }
   // q|k|v: row group = wave, 4 rows of 1024 columns, lane l holds chunks l and l + 64
-  const uint4* Wq = reinterpret_cast<const uint4*>(p.w_qkv);
+  const uint4* Wq = reinterpret_cast<const uint4*>(w_qkv);
   const uint32_t qrow0 = __builtin_amdgcn_readfirstlane(qkv_row0(x, s) + 4 * wave);
   uint4 wq[4][2];
 #pragma unroll
@@ -214,7 +218,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   }
   uint4 gin[2];
 #pragma unroll
-  for (int k = 0; k < 2; k++) gin[k] = reinterpret_cast<const uint4*>(p.w_in)[lane + 64 * k];
+  for (int k = 0; k < 2; k++) gin[k] = reinterpret_cast<const uint4*>(w_in)[lane + 64 * k];
   // Attention inputs, issued behind the residual and q|k|v weight loads: loads complete in issue
   // order, so they do not hold up this workgroup's q|k|v rows (which every run waits for), and
   // they arrive while the rows are computed instead of after them. The raw norm gains, this
@@ -231,7 +235,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
   const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
   {
     constexpr uint32_t EL = KV_BF16 ? 2 : 4;
-    const uint32_t r0 = s * p.run;
+    const uint32_t r0 = s * run_len;
     const uint32_t rows = attn && r0 < p.max_seq ? min(p.max_seq - r0, T) : 0u;
     auto run_rsrc = [&](const void* cache) __attribute__((always_inline)) {
       const uint8_t* b = static_cast<const uint8_t*>(cache) + (head_base + size_t(r0) * D) * EL;
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     const bool bad = pos >= p.max_seq;
     if (bad && x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
     uint32_t n = bad ? 0u : pos + 1;
-    const uint32_t run = p.run;
+    const uint32_t run = run_len;
     if (n > splits * run) {  // the host's runs would skip positions
       if (x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrShape);
       n = 0;
@@ -575,7 +579,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
     if (attn) {  // slots 0..15: the attention runs, no o_proj rows
       attention();
       if (s == 0 && tid == 0)
-        __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       // done before the merge and o_proj: the run workgroups load pf region 1 (the rest of the
       // MLP block's gate|up rows) while those finish
       if (p.pf_run) fused_prefetch<1, 2>(p, x, s, splits);
@@ -603,14 +607,19 @@ __global__ __launch_bounds__(256) void k_fused_attn(FusedLayerParams p) {
 #endif
     merge_oproj();
     if (s == 0 && tid == 0)
-      __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // MLP block of one layer (cpu_inference.rs:166-172)
 // ---------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
+// The arguments the first loads need come first, as plain pointers: those are preloaded into
+// scalar registers at wave launch (the build's -amdgpu-kernarg-preload-count), so the loads do not
+// wait for a scalar load of the argument block.
+__global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* res_in, const float* part_in,
+                                                   const uint16_t* w_gu, const uint16_t* w_post, const uint16_t* w_down,
+                                                   FusedLayerParams p) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t x = fused_xcd(p.err);
@@ -623,16 +632,16 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   __shared__ float red4[4];
   __shared__ __align__(16) float hs[I / NX];  // this XCD's h values
 
-  const uint32_t tag = *gen_word(p.sync, x) + 1;
+  const uint32_t tag = *gen_word(sync, x) + 1;
 
-  const float4 xin = reinterpret_cast<const float4*>(p.res_in)[tid];
+  const float4 xin = reinterpret_cast<const float4*>(res_in)[tid];
   float4 xp[NX];
 #pragma unroll
-  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(p.part_in + g * H)[tid];
+  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
   __builtin_amdgcn_sched_barrier(0);  // the residual's loads first: loads complete in issue order
   // gate|up: rows 768 x + 24 s + 6 wave + r (pairs (gate_i, up_i) interleaved), lane l holds
   // chunks l and l + 64
-  const uint4* Wg = reinterpret_cast<const uint4*>(p.w_gu);
+  const uint4* Wg = reinterpret_cast<const uint4*>(w_gu);
   const uint32_t row0 = __builtin_amdgcn_readfirstlane((2 * I / NX) * x + 24 * s + 6 * wave);
   uint4 wg[6][2];
 #pragma unroll
@@ -642,11 +651,11 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   }
   uint4 gp[2];
 #pragma unroll
-  for (int k = 0; k < 2; k++) gp[k] = reinterpret_cast<const uint4*>(p.w_post)[lane + 64 * k];
+  for (int k = 0; k < 2; k++) gp[k] = reinterpret_cast<const uint4*>(w_post)[lane + 64 * k];
   // down rows 32 s + 2 rg + r over columns [384 x, 384 x + 384): 16 threads per row, chunks
   // t16, t16 + 16, t16 + 32 of the slice
   const uint32_t rg = tid >> 4, t16 = tid & 15;
-  const uint4* Wd = reinterpret_cast<const uint4*>(p.w_down);
+  const uint4* Wd = reinterpret_cast<const uint4*>(w_down);
   uint4 wd[2][3];
 #pragma unroll
   for (int r = 0; r < 2; r++) {
@@ -657,7 +666,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   // 64-byte half lines) into XCD x's L2, one word of half lines tid and tid + 256, through a
   // descriptor that holds no bytes for the last layer (its loads then read 0 without touching
   // memory; a branch here would make the waits after it wait for every load)
-  const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv_next ? p.qkv_next + size_t(qkv_row0(x, s)) * H : p.w_gu,
+  const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv_next ? p.qkv_next + size_t(qkv_row0(x, s)) * H : w_gu,
                                             p.qkv_next ? 16 * H * 2 : 0);
   uint32_t pfw[2];
 #pragma unroll
@@ -730,7 +739,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(FusedLayerParams p) {
   // every workgroup of the XCD has published its h values with this tag (the down rows need all
   // of them), so all of them have read the generation word
   if (s == 0 && tid == 0)
-    __hip_atomic_store(gen_word(p.sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 // x = res + part[0] + ... + part[7]
@@ -755,14 +764,22 @@ template <bool FIRST, bool KV_BF16>
 hipError_t launch_attn_sm(const FusedLayerParams& p, hipStream_t s) {
   const dim3 grid(NX * (NS + p.pf_wgs)), block(256);
   if (p.run == 32) {  // runs of one 32-position tile
-    if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 32>), grid, block, 0, s, p);
-    else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 32>), grid, block, 0, s, p);
-    else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 32>), grid, block, 0, s, p);
-  } else if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 64>), grid, block, 0, s, p);
-  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 64>), grid, block, 0, s, p);
-  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 64>), grid, block, 0, s, p);
-  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false, 64>), grid, block, 0, s, p);
-  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true, 64>), grid, block, 0, s, p);
+    if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+    else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+    else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+  } else if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
+  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
+                                     p.splits, p.run, p);
   return hipGetLastError();
 }
 
@@ -788,7 +805,8 @@ hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStr
 
 hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s) {
   if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p);
+  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
+                     p.w_post, p.w_down, p);
   return hipGetLastError();
 }
 
