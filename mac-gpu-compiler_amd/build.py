@@ -48,7 +48,9 @@ SOURCE_FLAGS = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                 # fused.hip: the leading pointer arguments of the two-launch layer's kernels go
                 # into scalar registers at wave launch (up to 14 dwords), so their first loads do
                 # not wait for a load of the argument block
-                "fused.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
+                "fused.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"],
+                # kernels.hip: the same for k_matvec (the lm_head) and k_argmax
+                "kernels.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
 
 OBJ_DIR = os.path.join(PKG, "_build")
 # the host pass warns that it does not know the packed-fp32 feature; that is expected

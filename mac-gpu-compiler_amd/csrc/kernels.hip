@@ -27,31 +27,34 @@ namespace {
 // All weight loads are issued before the x prologue so they are in flight during it.
 // Prologue kNorm: xin = (x * s) * gain with s = 1/sqrt(mean(x^2) + eps)  (cpu_inference.rs:189-194)
 // ---------------------------------------------------------------------------------------------
+// w and x are also leading arguments, preloaded into scalar registers at wave launch (the build's
+// -amdgpu-kernarg-preload-count), so the weight loads do not wait for a load of the argument block.
 template <int R, int CPL, int PRO, int EPI>
-__global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
+__global__ __launch_bounds__(256) void k_matvec(const uint16_t* w, const float* xv, uint32_t rows, uint32_t cols,
+                                                MatvecParams p) {
   extern __shared__ __align__(16) float xs[];
   __shared__ float red[4];
   __shared__ ArgCand cbest[4];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const uint32_t nch = p.cols >> 3;
+  const uint32_t nch = cols >> 3;
   const uint32_t row0 = (blockIdx.x * 4u + uint32_t(wave)) * R;
-  const uint4* W = reinterpret_cast<const uint4*>(p.w);
+  const uint4* W = reinterpret_cast<const uint4*>(w);
 
   // unconditional loads (a load behind a divergent branch is waited for on the spot): chunk
   // indexes past the row end re-read the last chunk and are skipped in the dot product
   uint4 wv[R][CPL];
 #pragma unroll
   for (int r = 0; r < R; r++) {
-    const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);  // past the end: re-read the last row
+    const uint32_t row = min(row0 + uint32_t(r), rows - 1);  // past the end: re-read the last row
     const uint4* wr = W + size_t(row) * nch;
 #pragma unroll
     for (int k = 0; k < CPL; k++) wv[r][k] = wr[min(uint32_t(lane) + 64u * k, nch - 1)];
   }
 
-  const float4* x4 = reinterpret_cast<const float4*>(p.x);
+  const float4* x4 = reinterpret_cast<const float4*>(xv);
   float4* xs4 = reinterpret_cast<float4*>(xs);
   float ss = 0.f;
-  for (uint32_t i = tid; i < p.cols / 4; i += 256) {
+  for (uint32_t i = tid; i < cols / 4; i += 256) {
     float4 v = x4[i];
     xs4[i] = v;
     if (PRO == kNorm) ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
@@ -61,8 +64,8 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
     if (lane == 0) red[wave] = ss;
     __syncthreads();
     const float tot = (red[0] + red[1]) + (red[2] + red[3]);
-    const float s = 1.0f / sqrtf(tot / float(p.cols) + p.eps);
-    for (uint32_t i = tid; i < p.cols; i += 256) xs[i] = xs[i] * s * bf16f(p.nw[i]);
+    const float s = 1.0f / sqrtf(tot / float(cols) + p.eps);
+    for (uint32_t i = tid; i < cols; i += 256) xs[i] = xs[i] * s * bf16f(p.nw[i]);
   }
   __syncthreads();
 
@@ -86,7 +89,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
 #pragma unroll
       for (int r = 0; r < R; r++) {
         const uint32_t row = row0 + r;
-        if (row < p.rows) {
+        if (row < rows) {
           if (EPI == kStore) p.out[row] = acc[r];
           else p.out[row] += acc[r];
         }
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
 #pragma unroll
       for (int r = 0; r + 1 < R; r += 2) {
         const uint32_t row = row0 + r;
-        if (row + 1 < p.rows) {
+        if (row + 1 < rows) {
           const float g = acc[r];
           p.out[row >> 1] = g / (1.0f + expf(-g)) * acc[r + 1];
         }
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(256) void k_matvec(MatvecParams p) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
       const uint32_t row = row0 + r;
-      if (row < p.rows) {
+      if (row < rows) {
         if (lane == 0) p.out[row] = acc[r];
         const float v = acc[r];
         if (!isnan(v) && cand_better(v, row, bv, bi)) { bv = v; bi = row; }
@@ -453,7 +456,8 @@ template <int CPL, int PRO, int EPI>
 hipError_t launch_mv(const MatvecParams& p, hipStream_t s) {
   constexpr int R = rows_per_wave(CPL, EPI);
   const uint32_t blocks = ceil_div(p.rows, 4u * R);
-  hipLaunchKernelGGL((k_matvec<R, CPL, PRO, EPI>), dim3(blocks), dim3(256), size_t(p.cols) * 4, s, p);
+  hipLaunchKernelGGL((k_matvec<R, CPL, PRO, EPI>), dim3(blocks), dim3(256), size_t(p.cols) * 4, s, p.w, p.x, p.rows,
+                     p.cols, p);
   return hipGetLastError();
 }
 
