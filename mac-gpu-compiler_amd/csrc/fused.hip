@@ -70,6 +70,27 @@ static_assert(2 * I / NX == 24 * NS && H == 32 * NS, "24 gate|up rows and 32 dow
 
 __device__ __forceinline__ uint32_t* gen_word(uint32_t* sync, uint32_t x) { return sync + x * kFusedLineWords; }
 
+// One scalar load per 64-byte line of the argument block at the kernel's start, so that the
+// compiler's later loads of the arguments find them in the scalar cache instead of missing there
+// on the critical path. The loaded words are never read: their registers stay reserved to the end
+// of the kernel (kcache_release), where every scalar load has long completed.
+struct KcacheWarm {
+  uint32_t d[6];
+};
+__device__ __forceinline__ KcacheWarm kcache_warm() {
+  KcacheWarm w;
+  const auto ka = __builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile(
+      "s_load_dword %0, %6, 0x40\n\ts_load_dword %1, %6, 0x80\n\ts_load_dword %2, %6, 0xc0\n\t"
+      "s_load_dword %3, %6, 0x100\n\ts_load_dword %4, %6, 0x140\n\ts_load_dword %5, %6, 0x180"
+      : "=s"(w.d[0]), "=s"(w.d[1]), "=s"(w.d[2]), "=s"(w.d[3]), "=s"(w.d[4]), "=s"(w.d[5])
+      : "s"(ka));
+  return w;
+}
+__device__ __forceinline__ void kcache_release(const KcacheWarm& w) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(w.d[0]), "s"(w.d[1]), "s"(w.d[2]), "s"(w.d[3]), "s"(w.d[4]), "s"(w.d[5]));
+}
+
 // x[4 tid .. 4 tid + 3] = xin + part[0] + ... + part[7] (a fixed order) into xs; workgroup 0
 // also stores it to res_out. Returns the RMSNorm scale 1 / sqrt(mean(x^2) + eps) of all of x.
 __device__ __forceinline__ float residual_and_scale(float4 xin, const float4 (&xp)[NX], bool add_parts, float* xs,
@@ -160,6 +181,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     if (state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
+  const KcacheWarm kw = kcache_warm();
   const uint32_t s = blockIdx.x / NX;
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
   const uint32_t splits = max(n_runs, 1u);
@@ -583,6 +605,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       // done before the merge and o_proj: the run workgroups load pf region 1 (the rest of the
       // MLP block's gate|up rows) while those finish
       if (p.pf_run) fused_prefetch<1, 2>(p, x, s, splits);
+      kcache_release(kw);
       return;
     }
     if (!oproj) {
@@ -590,10 +613,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       // layer's gate|up rows of XCD x) into the XCD's L2 for the MLP launch (fewer than 16 runs
       // are fewer than 1024 positions, where prefetching pays at any cache element type)
       if (p.pf_idle && splits < 16) fused_prefetch<0, 1>(p, x, s - splits, 16 - splits);
+      kcache_release(kw);
       return;
     }
     load_wo();
     merge_oproj();
+    kcache_release(kw);
   } else {
     attention();
 #if QE_PF32
@@ -608,6 +633,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     merge_oproj();
     if (s == 0 && tid == 0)
       __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    kcache_release(kw);
   }
 }
 
@@ -627,6 +653,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
     if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
+  const KcacheWarm kw = kcache_warm();
   const uint32_t s = blockIdx.x / NX;
   __shared__ __align__(16) float xs[H];
   __shared__ float red4[4];
@@ -740,6 +767,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   // of them), so all of them have read the generation word
   if (s == 0 && tid == 0)
     __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  kcache_release(kw);
 }
 
 // x = res + part[0] + ... + part[7]
