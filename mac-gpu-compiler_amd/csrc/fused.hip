@@ -645,7 +645,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 // wait for a scalar load of the argument block.
 __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* res_in, const float* part_in,
                                                    const uint16_t* w_gu, const uint16_t* w_post, const uint16_t* w_down,
-                                                   FusedLayerParams p) {
+                                                   const uint16_t* qkv_next, FusedLayerParams p) {
   const uint32_t tid = threadIdx.x, lane = tid & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const uint32_t x = fused_xcd(p.err);
@@ -693,8 +693,8 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   // 64-byte half lines) into XCD x's L2, one word of half lines tid and tid + 256, through a
   // descriptor that holds no bytes for the last layer (its loads then read 0 without touching
   // memory; a branch here would make the waits after it wait for every load)
-  const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv_next ? p.qkv_next + size_t(qkv_row0(x, s)) * H : w_gu,
-                                            p.qkv_next ? 16 * H * 2 : 0);
+  const __amdgpu_buffer_rsrc_t rq = rsrc_of(qkv_next ? qkv_next + size_t(qkv_row0(x, s)) * H : w_gu,
+                                            qkv_next ? 16 * H * 2 : 0);
   uint32_t pfw[2];
 #pragma unroll
   for (int k = 0; k < 2; k++) pfw[k] = __builtin_amdgcn_raw_buffer_load_b32(rq, int((tid + 256 * k) * 64), 0, 0);
@@ -834,7 +834,7 @@ hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStr
 hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s) {
   if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
-                     p.w_post, p.w_down, p);
+                     p.w_post, p.w_down, p.qkv_next, p);
   return hipGetLastError();
 }
 
