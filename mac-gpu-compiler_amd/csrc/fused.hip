@@ -661,13 +661,10 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
 
   const uint32_t tag = *gen_word(sync, x) + 1;
 
-  const float4 xin = reinterpret_cast<const float4*>(res_in)[tid];
-  float4 xp[NX];
-#pragma unroll
-  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
-  __builtin_amdgcn_sched_barrier(0);  // the residual's loads first: loads complete in issue order
   // gate|up: rows 768 x + 24 s + 6 wave + r (pairs (gate_i, up_i) interleaved), lane l holds
-  // chunks l and l + 64
+  // chunks l and l + 64. These rows sit in the XCD's L2 (the attention block loaded them) and go
+  // first: loads complete in issue order, and they arrive while the residual and the partials come
+  // from beyond L2 (with the arguments preloaded, 2252 -> 2300 tok/s against residual first).
   const uint4* Wg = reinterpret_cast<const uint4*>(w_gu);
   const uint32_t row0 = __builtin_amdgcn_readfirstlane((2 * I / NX) * x + 24 * s + 6 * wave);
   uint4 wg[6][2];
@@ -676,6 +673,12 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
 #pragma unroll
     for (int k = 0; k < 2; k++) wg[r][k] = Wg[size_t(row0 + r) * (H / 8) + lane + 64 * k];
   }
+  __builtin_amdgcn_sched_barrier(0);
+  const float4 xin = reinterpret_cast<const float4*>(res_in)[tid];
+  float4 xp[NX];
+#pragma unroll
+  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
+  __builtin_amdgcn_sched_barrier(0);
   uint4 gp[2];
 #pragma unroll
   for (int k = 0; k < 2; k++) gp[k] = reinterpret_cast<const uint4*>(w_post)[lane + 64 * k];
