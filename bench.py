@@ -672,13 +672,27 @@ def main():
                               "us_per_step": round(mean_us * per_step, 2), "isolated_mean_us": round(iso, 3),
                               "bytes_per_launch": int(b),
                               "achieved_gbs": round(b / (mean_us * 1e-6) / 1e9, 1) if mean_us > 0 else None}
+        # two-launch layers: the same launches timed inside the whole step's graph from their
+        # workgroups' clock stamps. in_step_us is a launch's share of the step (its first
+        # workgroup's start to the next launch's; dispatch and drain included, as a kernel trace
+        # counts a dispatch), in_exec_us its first workgroup's start to its last one's exit.
+        share, window = stages.get("in_step:" + name), stages.get("in_exec:" + name)
+        if share:
+            ins = sum(share[0]) / len(share[0])
+            kernel_table[name]["in_step_us"] = round(ins, 3)
+            kernel_table[name]["in_step_gbs"] = round(b / (ins * 1e-6) / 1e9, 1) if ins > 0 else None
+        if window:
+            kernel_table[name]["in_exec_us"] = round(sum(window[0]) / len(window[0]), 3)
     pf = qe.prefetch_bytes(cfg, mean_pos, el) if qe.l2_prefetch_enabled() and mode == 0 else 0
     if "attention" in kernel_table:
         # the gate/up and down weights this launch also pulls into L2 (counted with those stages)
         kernel_table["attention"]["prefetch_bytes"] = int(pf)
     if kernel_table:
-        dom_name = max(kernel_table, key=lambda k: kernel_table[k]["us_per_step"])
-        dom = kernel_table[dom_name]
+        dom_name = max(kernel_table, key=lambda k: kernel_table[k].get("in_step_us", kernel_table[k]["mean_us"])
+                       * kernel_table[k]["launches_per_step"])
+        dom = dict(kernel_table[dom_name])
+        if "in_step_us" in dom:  # the launch's share of the step, as a kernel trace times each dispatch
+            dom["mean_us"], dom["achieved_gbs"] = dom["in_step_us"], dom["in_step_gbs"]
     else:
         dom_name, dom = None, {"achieved_gbs": None, "bytes_per_launch": None, "mean_us": None,
                                "launches_per_step": None}
@@ -721,6 +735,7 @@ def main():
             "bytes_per_launch": dom["bytes_per_launch"],
             "mean_position": mean_pos,
             "launch_us": dom["mean_us"],
+            "exec_us": dom.get("in_exec_us"),
             "launches_per_step": dom["launches_per_step"],
             "measured_ceiling_gbs": round(ceiling, 1),
             "measured_copy_gbs": round(copy_gbs, 1),

@@ -49,6 +49,7 @@ SOURCE_FLAGS = {"batch.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
                 # into scalar registers at wave launch (up to 14 dwords), so their first loads do
                 # not wait for a load of the argument block
                 "fused.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"],
+                "fused_timed.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"],
                 # kernels.hip: the same for k_matvec (the lm_head) and k_argmax
                 "kernels.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=14"]}
 

@@ -150,6 +150,12 @@ struct qe_model {
   // attention block reads into their XCD's L2 (QE_FUSED_PF_QKV=0: off)
   bool fused_pf_qkv = true;
   uint8_t* scratch = nullptr;
+  // qe_profile_step's in-step timing: while ts_buf is set, the i-th two-launch-layer launch that
+  // enqueue_step_fused makes stamps its workgroups' start and end clocks at ts_buf + i *
+  // kTsPerLaunch, and ts_stage[i] names its stage
+  uint64_t* ts_buf = nullptr;
+  const char** ts_stage = nullptr;
+  uint32_t n_ts = 0, ts_cap = 0;
   // pinned host staging
   float* h_logits = nullptr;
   uint32_t* h_small = nullptr;  // [0..3] state staging, [4] error word
@@ -540,6 +546,9 @@ namespace {
 // Enqueues one decode step on the model's stream. With `only` set, just the kernels of that
 // stage are enqueued (qe_profile_step times each stage this way); `launches` counts them.
 int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
+// timing-buffer words per launch: a start and an end stamp for each of the layer workgroups
+// (the prefetch workgroups beyond them stamp nothing)
+constexpr size_t kTsPerLaunch = 2 * size_t(qe::kFusedXcds) * qe::kFusedSlots;
 int enqueue_step_persist(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
 
 int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* launches = nullptr) {
@@ -653,6 +662,12 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     if (w && launches) ++*launches;
     return w;
   };
+  // qe_profile_step's stamps: the next launch's slot of the timing buffer, or none
+  auto ts_slot = [&](const char* stage) -> uint64_t* {
+    if (!m->ts_buf || m->n_ts >= m->ts_cap) return nullptr;
+    m->ts_stage[m->n_ts] = stage;
+    return m->ts_buf + size_t(m->n_ts++) * kTsPerLaunch;
+  };
   FusedLayerParams f{};
   f.qkv = m->fqkv; f.attn_part = reinterpret_cast<uint2*>(m->attn_part); f.h = m->fh;
   f.embed = m->embed; f.tokens = kv->tokens; f.vocab = V; f.state = kv->state;
@@ -700,7 +715,10 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       }
     }
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
-    if (want("attn_block")) HIP_TRY(qe::launch_fused_attn(f, l == 0, s));
+    if (want("attn_block")) {
+      f.ts = ts_slot("attn_block");
+      HIP_TRY(f.ts ? qe::launch_fused_attn_timed(f, l == 0, s) : qe::launch_fused_attn(f, l == 0, s));
+    }
     // MLP block: x = res1 + the o_proj partials; its extra workgroups load the next layer's q|k|v
     // rows and o_proj columns of each XCD
     f.res_in = m->res1; f.part_in = m->part_attn; f.res_out = m->res0; f.part_out = m->part_mlp;
@@ -718,7 +736,10 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       f.pf[3] = qe::FusedPrefetch{bytes(n.w_o), G * D * 2, G * D * 2, QD * 2, H};
       f.pf_max_pos = uint32_t(std::min(0.5 * double((QD + 2 * KD + QD) * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     }
-    if (want("mlp_block")) HIP_TRY(qe::launch_fused_mlp(f, s));
+    if (want("mlp_block")) {
+      f.ts = ts_slot("mlp_block");
+      HIP_TRY(f.ts ? qe::launch_fused_mlp_timed(f, s) : qe::launch_fused_mlp(f, s));
+    }
   }
   if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, s));
   MatvecParams p{};
@@ -1378,6 +1399,92 @@ int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, fl
   if (e1) (void)hipEventDestroy(e1);
   if (rc != QE_OK) return rc;
   if (he != hipSuccess) return fail(QE_ERR_HIP, "stage timing failed: %s", hipGetErrorString(he));
+  // Last, the two-launch layers' launches inside the whole step: a graph of the step whose layer
+  // launches are the clock-stamping compilation of the same kernels (FusedLayerParams::ts),
+  // replayed kReps times at pos .. pos + kReps - 1 (one attention shape, as for "step"). Per
+  // stage: "in_step:<stage>", a launch's share of the step, from its first workgroup's start to
+  // the next layer launch's first start (dispatch and drain included, as a kernel trace counts
+  // them; the step's last launch has no successor and is left out), and "in_exec:<stage>", its
+  // first workgroup's start to its last workgroup's exit.
+  uint32_t s0, r0, s1, r1;
+  step_shape(kv, pos, s0, r0);
+  step_shape(kv, std::min<uint64_t>(pos + kReps, kv->max_seq - 1), s1, r1);
+  if (model->fused == 1 && s0 == s1 && r0 == r1 && pos + kReps < kv->max_seq && kv->tok_cap >= uint32_t(kReps + 3)) {
+    const uint32_t cap = 2 * uint32_t(model->cfg.num_hidden_layers);
+    std::vector<const char*> ts_stage(cap, nullptr);
+    std::vector<uint64_t> host(size_t(cap) * kTsPerLaunch);
+    uint64_t* dts = nullptr;
+    hipGraph_t g = nullptr;
+    hipGraphExec_t ge = nullptr;
+    hipError_t me = hipMalloc(&dts, host.size() * 8);
+    int mrc = QE_OK;
+    if (me == hipSuccess) me = hipMemsetAsync(dts, 0, host.size() * 8, model->stream);
+    if (me == hipSuccess) mrc = set_state(model, kv, token, pos);
+    if (me == hipSuccess && mrc == QE_OK) {
+      model->ts_buf = dts;
+      model->ts_stage = ts_stage.data();
+      model->n_ts = 0;
+      model->ts_cap = cap;
+      me = hipStreamBeginCapture(model->stream, hipStreamCaptureModeThreadLocal);
+      if (me == hipSuccess) {
+        mrc = enqueue_step(model, kv);
+        const hipError_t ce = hipStreamEndCapture(model->stream, &g);
+        if (me == hipSuccess) me = ce;
+      }
+      model->ts_buf = nullptr;
+      model->ts_stage = nullptr;
+    }
+    const uint32_t nl = model->n_ts;
+    model->n_ts = 0;
+    double sum[2][2] = {{0.0, 0.0}, {0.0, 0.0}};  // [share, window][attn, mlp]
+    uint32_t cnt[2][2] = {{0, 0}, {0, 0}};
+    if (me == hipSuccess && mrc == QE_OK && nl > 0) me = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+    if (me == hipSuccess && mrc == QE_OK && nl > 0) {
+      me = hipGraphLaunch(ge, model->stream);  // warm-up replay
+      const uint32_t nwg = qe::kFusedXcds * qe::kFusedSlots;  // the stamping workgroups
+      for (int r = 0; r < kReps && me == hipSuccess; r++) {
+        me = hipGraphLaunch(ge, model->stream);
+        if (me == hipSuccess) me = hipMemcpyAsync(host.data(), dts, size_t(nl) * kTsPerLaunch * 8, hipMemcpyDeviceToHost, model->stream);
+        if (me == hipSuccess) me = hipStreamSynchronize(model->stream);
+        std::vector<uint64_t> first(nl, UINT64_MAX), last(nl, 0);
+        for (uint32_t i = 0; i < nl && me == hipSuccess; i++) {
+          const uint64_t* t = host.data() + size_t(i) * kTsPerLaunch;
+          for (uint32_t b = 0; b < nwg; b++) {
+            first[i] = std::min(first[i], t[2 * b]);
+            last[i] = std::max(last[i], t[2 * b + 1]);
+          }
+        }
+        for (uint32_t i = 0; i < nl && me == hipSuccess; i++) {
+          const int k = strcmp(ts_stage[i], "attn_block") == 0 ? 0 : 1;
+          if (i + 1 < nl && first[i + 1] > first[i]) {
+            sum[0][k] += double(first[i + 1] - first[i]) * 0.01;  // 100 MHz clock: 10 ns per tick
+            cnt[0][k]++;
+          }
+          if (last[i] > first[i]) {
+            sum[1][k] += double(last[i] - first[i]) * 0.01;
+            cnt[1][k]++;
+          }
+        }
+      }
+    }
+    static const char* const kInStep[2][2] = {{"in_step:attn_block", "in_step:mlp_block"},
+                                              {"in_exec:attn_block", "in_exec:mlp_block"}};
+    for (int w = 0; w < 2; w++)
+      for (int k = 0; k < 2 && me == hipSuccess && mrc == QE_OK; k++) {
+        if (cnt[w][k] && n < max_stages) {
+          us_out[n] = float(sum[w][k] / cnt[w][k]);
+          if (launches_out) launches_out[n] = cnt[w][k] / kReps;
+          if (names_out) names_out[n] = kInStep[w][k];
+          n++;
+        }
+      }
+    if (ge) (void)hipGraphExecDestroy(ge);
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamSynchronize(model->stream);
+    if (dts) (void)hipFree(dts);
+    if (mrc != QE_OK) return mrc;
+    if (me != hipSuccess) return fail(QE_ERR_HIP, "in-step timing failed: %s", hipGetErrorString(me));
+  }
   // a kernel error raised by any of the replays is reported like one of a step
   if ((rc = check_err(model))) return rc;
   // the stage replays ran on the activations the step left behind, so the K/V they wrote at pos

@@ -51,6 +51,13 @@
 #ifndef QE_PF32
 #define QE_PF32 1
 #endif
+// QE_FUSED_TIMED: this file compiled a second time (fused_timed.hip) with clock stamps in the
+// layer kernels and the two layer launchers named *_timed
+#ifdef QE_FUSED_TIMED
+#define QE_FUSED_LAUNCHER(name) name##_timed
+#else
+#define QE_FUSED_LAUNCHER(name) name
+#endif
 // attention blocks with at least this many runs merge them in two rounds (below)
 #ifndef QE_MERGE2_MIN_SM
 #define QE_MERGE2_MIN_SM 8
@@ -89,6 +96,32 @@ __device__ __forceinline__ KcacheWarm kcache_warm() {
 }
 __device__ __forceinline__ void kcache_release(const KcacheWarm& w) {
   asm volatile("s_waitcnt lgkmcnt(0)" ::"s"(w.d[0]), "s"(w.d[1]), "s"(w.d[2]), "s"(w.d[3]), "s"(w.d[4]), "s"(w.d[5]));
+}
+
+// Clock stamps, in the QE_FUSED_TIMED compilation of this file only: a layer workgroup reads the
+// 100 MHz real-time clock at its start (kept in registers, so nothing at the start waits for the
+// argument block) and at its exit writes both to FusedLayerParams::ts[2 b], ts[2 b + 1], b = its
+// workgroup index. The other compilation reads no clock and writes nothing.
+__device__ __forceinline__ uint64_t clock_start() {
+#ifdef QE_FUSED_TIMED
+  return __builtin_amdgcn_s_memrealtime();
+#else
+  return 0;
+#endif
+}
+
+// every exit of a layer kernel's workgroup: the scalar-cache warm loads are in; the clock stamps
+__device__ __forceinline__ void finish(const KcacheWarm& w, uint64_t* ts, uint64_t t_start) {
+  kcache_release(w);
+#ifdef QE_FUSED_TIMED
+  if (ts && threadIdx.x == 0) {
+    ts[2 * blockIdx.x] = t_start;
+    ts[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+  }
+#else
+  (void)ts;
+  (void)t_start;
+#endif
 }
 
 // x[4 tid .. 4 tid + 3] = xin + part[0] + ... + part[7] (a fixed order) into xs; workgroup 0
@@ -181,6 +214,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     if (state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
+  const uint64_t t_start = clock_start();
   const KcacheWarm kw = kcache_warm();
   const uint32_t s = blockIdx.x / NX;
   const int pg = tid >> 3, dc = tid & 7, dg = tid & 31, pp = tid >> 5;
@@ -605,7 +639,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       // done before the merge and o_proj: the run workgroups load pf region 1 (the rest of the
       // MLP block's gate|up rows) while those finish
       if (p.pf_run) fused_prefetch<1, 2>(p, x, s, splits);
-      kcache_release(kw);
+      finish(kw, p.ts, t_start);
       return;
     }
     if (!oproj) {
@@ -613,12 +647,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       // layer's gate|up rows of XCD x) into the XCD's L2 for the MLP launch (fewer than 16 runs
       // are fewer than 1024 positions, where prefetching pays at any cache element type)
       if (p.pf_idle && splits < 16) fused_prefetch<0, 1>(p, x, s - splits, 16 - splits);
-      kcache_release(kw);
+      finish(kw, p.ts, t_start);
       return;
     }
     load_wo();
     merge_oproj();
-    kcache_release(kw);
+    finish(kw, p.ts, t_start);
   } else {
     attention();
 #if QE_PF32
@@ -633,7 +667,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     merge_oproj();
     if (s == 0 && tid == 0)
       __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    kcache_release(kw);
+    finish(kw, p.ts, t_start);
   }
 }
 
@@ -653,6 +687,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
     if (p.state->pos < p.pf_max_pos) fused_prefetch(p, x, (blockIdx.x - NX * NS) / NX, p.pf_wgs);
     return;
   }
+  const uint64_t t_start = clock_start();
   const KcacheWarm kw = kcache_warm();
   const uint32_t s = blockIdx.x / NX;
   __shared__ __align__(16) float xs[H];
@@ -770,7 +805,7 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   // of them), so all of them have read the generation word
   if (s == 0 && tid == 0)
     __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  kcache_release(kw);
+  finish(kw, p.ts, t_start);
 }
 
 // x = res + part[0] + ... + part[7]
@@ -823,7 +858,7 @@ bool common_ok(const FusedLayerParams& p) {
 
 }  // namespace
 
-hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s) {
+hipError_t QE_FUSED_LAUNCHER(launch_fused_attn)(const FusedLayerParams& p, bool first_layer, hipStream_t s) {
   if (!common_ok(p) || !p.w_in || !p.w_qkv || !p.q_norm || !p.k_norm || !p.w_o || !p.qkv || !p.attn_part ||
       !p.k_cache || !p.v_cache || !p.rope_cur || p.max_seq == 0 || p.splits == 0 || p.splits > kFusedMaxRuns ||
       (p.splits > 16 && p.splits != kFusedMaxRuns) || (p.splits <= 16 && p.run != 64 && p.run != 32) ||
@@ -834,13 +869,14 @@ hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStr
   return p.kv_bf16 ? launch_attn_sm<false, true>(p, s) : launch_attn_sm<false, false>(p, s);
 }
 
-hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s) {
+hipError_t QE_FUSED_LAUNCHER(launch_fused_mlp)(const FusedLayerParams& p, hipStream_t s) {
   if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
                      p.w_post, p.w_down, p.qkv_next, p);
   return hipGetLastError();
 }
 
+#ifndef QE_FUSED_TIMED
 hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s) {
   if (!res || !part || !x) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_fused_reduce, dim3(1), dim3(256), 0, s, res, part, x);
@@ -859,5 +895,6 @@ hipError_t fused_placement_check(uint32_t* dev_ids, uint32_t* host_ids, bool* ok
   *ok = good;
   return e;
 }
+#endif
 
 }  // namespace qe

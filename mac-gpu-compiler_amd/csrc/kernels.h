@@ -219,6 +219,9 @@ struct FusedLayerParams {
   // MLP block: the next layer's q|k|v rows [QD + 2 KD][H] (null: none); workgroup (x, s) loads
   // the rows that slot s of the next attention block reads into XCD x's L2
   const uint16_t* qkv_next;
+  // clock stamps, read by the *_timed launchers only (null: none): layer workgroup b stores the
+  // 100 MHz real-time clock at its start to ts[2 b] and at its exit to ts[2 b + 1]
+  uint64_t* ts;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
@@ -226,6 +229,10 @@ struct FusedLayerParams {
 hipError_t launch_fused_attn(const FusedLayerParams& p, bool first_layer, hipStream_t s);
 // layer l's MLP block: residual + partials -> RMSNorm -> gate|up + silu -> down slice partial
 hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
+// the same two blocks compiled with the clock stamps of FusedLayerParams::ts (fused_timed.hip),
+// for timing the layer launches inside a whole step
+hipError_t launch_fused_attn_timed(const FusedLayerParams& p, bool first_layer, hipStream_t s);
+hipError_t launch_fused_mlp_timed(const FusedLayerParams& p, hipStream_t s);
 // x = res + sum of the 8 partials (the last layer's output, before the final norm)
 hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s);
 // ---- the decode step's layers in one persistent launch (persist.hip), same shape ----

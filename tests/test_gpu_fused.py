@@ -138,3 +138,30 @@ def test_fused_prefetch_switches_change_no_result(gpu, narrow_ckpt, monkeypatch,
     toks, lg = run()
     assert toks == want_toks
     np.testing.assert_array_equal(lg, want_lg)
+
+
+def test_fused_profile_step_times_layer_launches_in_step(gpu, narrow_ckpt):
+    """qe_profile_step times the two-launch layer's launches inside the whole step from the clock
+    stamps of their workgroups (the stamping compilation of the same kernels): a launch's share of
+    the step (to the next layer launch's start; the step's last layer launch has none) is at least
+    its own execution window, and the next forward still matches the oracle"""
+    m = load(narrow_ckpt, 1)
+    om = oracle.Model(narrow_ckpt)
+    L = NARROW.num_hidden_layers
+    prompt = qe.random_prompt(13, 41, NARROW.vocab_size)
+    c = qe.KVCache(m, 400)
+    m.prefill(prompt[:40], 0, c, want_logits=False)
+    stages = {name: (us, n) for name, us, n in m.profile_step(int(prompt[40]), 40, c)}
+    assert stages["in_step:attn_block"][1] == L and stages["in_step:mlp_block"][1] == L - 1
+    assert stages["in_exec:attn_block"][1] == L and stages["in_exec:mlp_block"][1] == L
+    for name in ("attn_block", "mlp_block"):
+        share, window = stages["in_step:" + name][0], stages["in_exec:" + name][0]
+        assert 0 < window <= share * 1.001, (name, window, share)
+        assert share < stages["step"][0] * stages["step"][1]
+    oc = om.new_cache()
+    for pos, tok in enumerate(prompt):
+        om.forward(int(tok), pos, oc)
+    ref = om.forward(3, 41, oc)
+    got = m.forward(3, 41, c)
+    assert int(np.argmax(got)) == int(np.argmax(ref))
+    assert float(np.max(np.abs(got - ref))) < 1e-3
