@@ -185,9 +185,16 @@ uint64_t qe_lookup_draft(const uint32_t* history, uint64_t n, uint32_t ngram, ui
  *      differences of consecutive prefixes (duration x launches) are the stages' costs inside the
  *      step (the argmax, the last launch, is timed alone only: its replays advance the step
  *      state). A cache of fewer than 9 positions skips the argmax stage (its replays advance the
- *      token ring). Afterwards the step is run once more, so the cache holds what qe_forward(token,
- *      pos) leaves; a kernel error raised by any replay is returned as QE_ERR_KERNEL. No reference
- *      counterpart: the reference timed kernels by removing them by hand (README.md:64-71). ---- */
+ *      token ring). With two launches per layer (qe_model_fused_layers() == 1) the stages are
+ *      attn_block, mlp_block, final_reduce, lm_head and argmax, their prefixes and "step" (the
+ *      whole step's graph); then "in_step:attn_block" and "in_step:mlp_block", each layer
+ *      launch's share of the whole step (its first workgroup's start to the next layer launch's
+ *      first start, from per-workgroup clock stamps of a compilation of the same kernels that
+ *      writes them; launches_out counts the launches with a successor), and "in_exec:attn_block",
+ *      "in_exec:mlp_block", first start to last workgroup exit. Afterwards the step is run once
+ *      more, so the cache holds what qe_forward(token, pos) leaves; a kernel error raised by any
+ *      replay is returned as QE_ERR_KERNEL. No reference counterpart: the reference timed kernels
+ *      by removing them by hand (README.md:64-71). ---- */
 int qe_profile_step(qe_model* model, uint32_t token, uint64_t pos, qe_kv* kv, float* us_out,
                     uint32_t* launches_out, const char** names_out, uint32_t max_stages, uint32_t* n_out);
 
