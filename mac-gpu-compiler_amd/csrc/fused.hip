@@ -283,13 +283,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   // them, the tile through descriptors over the run's first rows (none for a workgroup without
   // a run: its loads read 0 without touching memory): behind a branch, the wait counts of the
   // two paths would merge and every workgroup's q|k|v rows would wait for the tile.
+  // A 32-position tile is issued only once the residual is in (below): issued here it delays
+  // the run workgroups' residual by ~0.3 us (2321 vs 2305 tok/s at positions 130..257), while a
+  // 64-position tile issued there arrives too late (1740 vs 1767 tok/s over 4096 steps).
   const size_t head_base = size_t(x) * p.max_seq * D;
   KVTile<KV_BF16, NT> A;
-  __builtin_amdgcn_sched_barrier(0);
-  const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
-  const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
-  const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
-  {
+  auto load_first_tile = [&]() __attribute__((always_inline)) {
     constexpr uint32_t EL = KV_BF16 ? 2 : 4;
     const uint32_t r0 = s * run_len;
     const uint32_t rows = attn && r0 < p.max_seq ? min(p.max_seq - r0, T) : 0u;
@@ -298,7 +297,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(b), short(0), int(rows * D * EL), 0x00020000);
     };
     load_tile_buf<KV_BF16, NT>(A, run_rsrc(p.k_cache), run_rsrc(p.v_cache), 0, tid);
-  }
+  };
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
+  const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
+  const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  if constexpr (NT != 32) load_first_tile();
   // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
   const uint32_t rg = tid >> 4, t16 = tid & 15;
@@ -316,6 +320,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   // ---- input RMSNorm + this workgroup's 16 q|k|v rows (cpu_inference.rs:129-132) ----
   {
     const float rs = residual_and_scale(xin, xp, !FIRST, xs, p.res_out, p.eps, red4);
+    if constexpr (NT == 32) load_first_tile();
     const float4* xs4 = reinterpret_cast<const float4*>(xs);
     float acc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
