@@ -341,6 +341,19 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   if (SM > 16 && attn) load_wo();
 
   // ---- attention run s of KV head x (cpu_inference.rs:134-162) ----
+  // With 32 runs every slot runs attention and holds o_proj rows (no idle slot), and each loads
+  // the 24 gate|up rows of MLP slot s on this XCD (48 KB, one word of each 64-byte half line)
+  // into its L2 while its run computes. Loads complete in issue order, so the issue point is
+  // after the loads the run waits for and before the merge's polls, which would otherwise wait
+  // for this HBM round trip: a single-tile run issues it once its q|k|v pairs are in, a run of
+  // several tiles right after its second tile's loads (after the partial, where the merge's
+  // polls waited for it: 1765 -> 1786 tok/s over 4096 steps, 1556 -> 1598 over the last 512).
+  uint32_t gpf[3] = {0u, 0u, 0u};
+  auto load_gpf = [&]() __attribute__((always_inline)) {
+    const uint8_t* gb = reinterpret_cast<const uint8_t*>(p.w_gu + size_t((2 * I / NX) * x + 24 * s) * H);
+#pragma unroll
+    for (int k = 0; k < 3; k++) gpf[k] = *reinterpret_cast<const uint32_t*>(gb + (tid + 256 * k) * 64);
+  };
   auto attention = [&]() __attribute__((always_inline)) {
     // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v]; lane l holds dims l, l + 64
     const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, uint32_t(kFusedQkvPairs * 8));
@@ -352,6 +365,9 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       if (poll_done(qa.y == tag && qb.y == tag, spins, p.err)) break;
     }
     float a = __uint_as_float(qa.x), b = __uint_as_float(qb.x);
+#if QE_PF32
+    if constexpr (SM == 32 && !MULTI) load_gpf();  // (see gpf above)
+#endif
 
     const uint32_t pos = pos_step;
     const bool bad = pos >= p.max_seq;
@@ -477,6 +493,9 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       for (uint32_t tile = t0;; tile += 2 * T) {
         const bool more = tile + T < t1;
         if (more) load_tile<KV_BF16>(B, p.k_cache, p.v_cache, p.max_seq, head_base, tile + T, tid);
+#if QE_PF32
+        if (tile == t0) load_gpf();  // (see gpf above)
+#endif
         __builtin_amdgcn_sched_barrier(0);
         process(A, tile);
         if (!more) break;
@@ -507,9 +526,6 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       }
     }
   };
-
-  // words of the MLP block's gate|up rows that 32-run slots load while the runs finish (below)
-  uint32_t gpf[3] = {0u, 0u, 0u};
 
   // ---- merge of the runs, then o_proj ----
   // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
@@ -660,15 +676,6 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     finish(kw, p.ts, t_start);
   } else {
     attention();
-#if QE_PF32
-    // slot s's partial is out and the merge waits for the slowest run: load the 24 gate|up rows
-    // of MLP slot s on this XCD (48 KB, one word of each 64-byte half line) into its L2
-    {
-      const uint8_t* gb = reinterpret_cast<const uint8_t*>(p.w_gu + size_t((2 * I / NX) * x + 24 * s) * H);
-#pragma unroll
-      for (int k = 0; k < 3; k++) gpf[k] = *reinterpret_cast<const uint32_t*>(gb + (tid + 256 * k) * 64);
-    }
-#endif
     merge_oproj();
     if (s == 0 && tid == 0)
       __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
