@@ -149,6 +149,9 @@ struct qe_model {
   // each MLP block's workgroups load the next layer's q|k|v rows that their slot of the next
   // attention block reads into their XCD's L2 (QE_FUSED_PF_QKV=0: off)
   bool fused_pf_qkv = true;
+  // the attention block's o_proj workgroups load the MLP block's down columns of their XCD into
+  // its L2 while the runs work (QE_FUSED_PF_DOWN=0: off; up to 16 runs)
+  bool fused_pf_down = true;
   uint8_t* scratch = nullptr;
   // qe_profile_step's in-step timing: while ts_buf is set, the i-th two-launch-layer launch that
   // enqueue_step_fused makes stamps its workgroups' start and end clocks at ts_buf + i *
@@ -478,6 +481,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* v = getenv("QE_FUSED_PF_IDLE")) m->fused_pf_idle = strcmp(v, "0") != 0;
   if (const char* v = getenv("QE_FUSED_PF_RUN")) m->fused_pf_run = strcmp(v, "0") != 0;
   if (const char* v = getenv("QE_FUSED_PF_QKV")) m->fused_pf_qkv = strcmp(v, "0") != 0;
+  if (const char* v = getenv("QE_FUSED_PF_DOWN")) m->fused_pf_down = strcmp(v, "0") != 0;
   if (const char* v = getenv("QE_FUSED_RUN32")) m->fused_run32 = uint64_t(std::min(std::max(atoi(v), 0), 512)) / 64 * 64;
   // the layers' tensors sit at one stride in the arena (the persistent launch finds layer l's from
   // layer 0's)
@@ -714,6 +718,8 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
         f.pf_run = 1;
       }
     }
+    if (!f.pf_wgs && m->fused_pf_down && f.splits <= 16)
+      f.pf[2] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     if (want("attn_block")) {
       f.ts = ts_slot("attn_block");

@@ -672,6 +672,9 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       return;
     }
     load_wo();
+    // the MLP block's down columns of this XCD (pf region 2, when set) into its L2 while the
+    // runs work
+    fused_prefetch<2, 3>(p, x, s - 16, 16);
     merge_oproj();
     finish(kw, p.ts, t_start);
   } else {

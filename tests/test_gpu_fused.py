@@ -117,11 +117,11 @@ def test_fused_real_model_matches_fixture_tokens(gpu, real_ckpt, mode):
     assert worst < 1e-2, worst
 
 
-@pytest.mark.parametrize("env", ["QE_FUSED_PF_IDLE", "QE_FUSED_PF_RUN", "QE_FUSED_PF_QKV", "QE_FUSED_PF_ATTN",
-                                 "QE_FUSED_PF_MLP"])
+@pytest.mark.parametrize("env", ["QE_FUSED_PF_IDLE", "QE_FUSED_PF_RUN", "QE_FUSED_PF_QKV", "QE_FUSED_PF_DOWN",
+                                 "QE_FUSED_PF_ATTN", "QE_FUSED_PF_MLP"])
 def test_fused_prefetch_switches_change_no_result(gpu, narrow_ckpt, monkeypatch, env):
-    """the two-launch layer's L2 prefetches only load: turning the idle-slot, run-workgroup or
-    next-layer q|k|v prefetch off, or adding prefetch workgroups, gives the same tokens and
+    """the two-launch layer's L2 prefetches only load: turning the idle-slot, run-workgroup,
+    next-layer q|k|v or down-column prefetch off, or adding prefetch workgroups, gives the same tokens and
     bit-identical logits, at 4, 8 and 16 attention runs per KV head (positions 40..339)"""
     prompt = qe.random_prompt(9, 40, NARROW.vocab_size)
 
