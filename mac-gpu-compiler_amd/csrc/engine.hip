@@ -150,7 +150,7 @@ struct qe_model {
   // attention block reads into their XCD's L2 (QE_FUSED_PF_QKV=0: off)
   bool fused_pf_qkv = true;
   // the attention block's o_proj workgroups load the MLP block's down columns of their XCD into
-  // its L2 while the runs work (QE_FUSED_PF_DOWN=0: off; up to 16 runs)
+  // its L2 while the runs work (QE_FUSED_PF_DOWN=0: off)
   bool fused_pf_down = true;
   uint8_t* scratch = nullptr;
   // qe_profile_step's in-step timing: while ts_buf is set, the i-th two-launch-layer launch that
@@ -718,7 +718,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
         f.pf_run = 1;
       }
     }
-    if (!f.pf_wgs && m->fused_pf_down && f.splits <= 16)
+    if (!f.pf_wgs && m->fused_pf_down)
       f.pf[2] = qe::FusedPrefetch{bytes(w.w_down), I / NX * 2, I / NX * 2, I * 2, H};
     f.pf_max_pos = uint32_t(std::min(0.5 * double(3 * I * H * 2) / kv_pos_bytes, double(kv->max_seq)));
     if (want("attn_block")) {
