@@ -348,25 +348,28 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   // for this HBM round trip: a single-tile run issues it once its q|k|v pairs are in, a run of
   // several tiles right after its second tile's loads (after the partial, where the merge's
   // polls waited for it: 1765 -> 1786 tok/s over 4096 steps, 1556 -> 1598 over the last 512).
-  // With pf region 2 set, a single-tile run also loads the down columns of MLP slot s (rows
-  // 32 s .., 768 bytes each), through a descriptor that holds no bytes otherwise (positions
-  // 1154..1665: 1893 -> 1975 tok/s; the same in runs of several tiles: 1652 -> 1607 at 3202..3713).
+  // With pf region 2 set, a run also loads the down columns of MLP slot s (rows 32 s .., 768
+  // bytes each; load_gdn), through a descriptor that holds no bytes otherwise: a single-tile run
+  // with the gate|up rows (positions 1154..1665: 1893 -> 1975 tok/s), a run of several tiles once
+  // its first tile is computed (2178..2689: 1659 -> 1688; issued with the gate|up rows, after the
+  // second tile's loads, it cost 1652 -> 1607 at 3202..3713).
   uint32_t gpf[5] = {0u, 0u, 0u, 0u, 0u};
+  auto load_gdn = [&]() __attribute__((always_inline)) {
+    constexpr uint32_t DL = (I / NX) * 2 / 64;  // 64-byte lines of one down row's slice: 12
+    const bool dn = p.pf[2].base != nullptr;
+    const __amdgpu_buffer_rsrc_t rd = rsrc_of(p.w_down + size_t(32 * s) * I + (I / NX) * x,
+                                              dn ? 31 * I * 2 + DL * 64 : 0u);
+#pragma unroll
+    for (int k = 0; k < 2; k++) {
+      const uint32_t i = min(tid + 256 * k, 32 * DL - 1), row = i / DL;
+      gpf[3 + k] = __builtin_amdgcn_raw_buffer_load_b32(rd, int(row * I * 2 + (i - row * DL) * 64), 0, 0);
+    }
+  };
   auto load_gpf = [&]() __attribute__((always_inline)) {
     const uint8_t* gb = reinterpret_cast<const uint8_t*>(p.w_gu + size_t((2 * I / NX) * x + 24 * s) * H);
 #pragma unroll
     for (int k = 0; k < 3; k++) gpf[k] = *reinterpret_cast<const uint32_t*>(gb + (tid + 256 * k) * 64);
-    if constexpr (!MULTI) {
-      constexpr uint32_t DL = (I / NX) * 2 / 64;  // 64-byte lines of one down row's slice: 12
-      const bool dn = p.pf[2].base != nullptr;
-      const __amdgpu_buffer_rsrc_t rd = rsrc_of(p.w_down + size_t(32 * s) * I + (I / NX) * x,
-                                                dn ? 31 * I * 2 + DL * 64 : 0u);
-#pragma unroll
-      for (int k = 0; k < 2; k++) {
-        const uint32_t i = min(tid + 256 * k, 32 * DL - 1), row = i / DL;
-        gpf[3 + k] = __builtin_amdgcn_raw_buffer_load_b32(rd, int(row * I * 2 + (i - row * DL) * 64), 0, 0);
-      }
-    }
+    if constexpr (!MULTI) load_gdn();
   };
   auto attention = [&]() __attribute__((always_inline)) {
     // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v]; lane l holds dims l, l + 64
@@ -512,6 +515,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 #endif
         __builtin_amdgcn_sched_barrier(0);
         process(A, tile);
+        if (tile == t0) load_gdn();  // (see gpf above)
         if (!more) break;
         const bool more2 = tile + 2 * T < t1;
         if (more2) load_tile<KV_BF16>(A, p.k_cache, p.v_cache, p.max_seq, head_base, tile + 2 * T, tid);
@@ -598,8 +602,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
         if (poll_done(av1.y == tag, spins, p.err)) break;
       }
       att[tid] = __uint_as_float(av1.x);
-      if constexpr (MULTI) asm volatile("" ::"v"(gpf[0] ^ gpf[1] ^ gpf[2]));  // (in: the polls waited for every load)
-      else asm volatile("" ::"v"(gpf[0] ^ gpf[1] ^ gpf[2] ^ gpf[3] ^ gpf[4]));
+      asm volatile("" ::"v"(gpf[0] ^ gpf[1] ^ gpf[2] ^ gpf[3] ^ gpf[4]));  // (in: the polls waited for every load)
       __syncthreads();
     } else {
     // Wave 0 takes the (m, l) of every run (lane u: head u / SM, run u % SM) and leaves the
