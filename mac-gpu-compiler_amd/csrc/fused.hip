@@ -190,6 +190,42 @@ __device__ __forceinline__ void fused_prefetch(const FusedLayerParams& p, uint32
   asm volatile("" ::"v"(hsum));
 }
 
+// The same for one region T, with the line's row and segment advanced by constant steps from
+// load to load instead of divided out for every load (fewer instructions before the last load
+// issues). Lines past the region's end load the region's last line again.
+template <int T>
+__device__ __forceinline__ void prefetch_region(const FusedLayerParams& p, uint32_t x, uint32_t k, uint32_t n) {
+  constexpr uint32_t U = 8, SEG = 64;
+  const FusedPrefetch& r = p.pf[T];
+  if (!r.base || !r.rows) return;
+  const uint32_t per_row = ceil_div(r.row_bytes, SEG), span = per_row * r.rows, step = n * 256;
+  const uint32_t dq = step / per_row, dr = step - dq * per_row;
+  const uint32_t i0 = k * 256 + threadIdx.x;
+  uint32_t row = i0 / per_row, seg = i0 - row * per_row;
+  const uint8_t* base = r.base + size_t(x) * r.xcd_bytes;
+  const uint32_t last_row = r.rows - 1, last_off = r.row_bytes - 4;
+  uint32_t hsum = 0;
+  for (uint32_t j0 = 0; k * 256 + j0 * step < span; j0 += U) {
+    uint32_t v[U];
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) {
+      const bool in = row <= last_row;
+      const uint8_t* a = base + size_t(in ? row : last_row) * r.stride + (in ? min(seg * SEG, last_off) : last_off);
+      v[u] = *reinterpret_cast<const uint32_t*>(a);
+      seg += dr;
+      row += dq;
+      if (seg >= per_row) {
+        seg -= per_row;
+        row++;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (uint32_t u = 0; u < U; u++) hsum ^= v[u];
+  }
+  asm volatile("" ::"v"(hsum));
+}
+
 // ---------------------------------------------------------------------------------------------
 // attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type,
 // MULTI: runs of more than one 64-position tile (only with 32 runs), NT: positions per tile and
@@ -677,7 +713,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
         __hip_atomic_store(gen_word(sync, x), tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       // done before the merge and o_proj: the run workgroups load pf region 1 (the rest of the
       // MLP block's gate|up rows) while those finish
-      if (p.pf_run) fused_prefetch<1, 2>(p, x, s, splits);
+      if (p.pf_run) prefetch_region<1>(p, x, s, splits);
       finish(kw, p.ts, t_start);
       return;
     }
@@ -685,14 +721,14 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       // slots splits..15 are done once their q|k|v rows are out: they load the pf regions (this
       // layer's gate|up rows of XCD x) into the XCD's L2 for the MLP launch (fewer than 16 runs
       // are fewer than 1024 positions, where prefetching pays at any cache element type)
-      if (p.pf_idle && splits < 16) fused_prefetch<0, 1>(p, x, s - splits, 16 - splits);
+      if (p.pf_idle && splits < 16) prefetch_region<0>(p, x, s - splits, 16 - splits);
       finish(kw, p.ts, t_start);
       return;
     }
     load_wo();
     // the MLP block's down columns of this XCD (pf region 2, when set) into its L2 while the
     // runs work
-    fused_prefetch<2, 3>(p, x, s - 16, 16);
+    prefetch_region<2>(p, x, s - 16, 16);
     merge_oproj();
     finish(kw, p.ts, t_start);
   } else {
