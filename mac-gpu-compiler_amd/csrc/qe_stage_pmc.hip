@@ -319,6 +319,8 @@ int main(int argc, char** argv) {
                                       qe::kFusedSlots};
           f.pf_run = 1;
         }
+        // ... and its o_proj workgroups the down columns of their XCD
+        f.pf[2] = qe::FusedPrefetch{reinterpret_cast<const uint8_t*>(f.w_down), I / NX * 2, I / NX * 2, I * 2, H};
       }
       CK(qe::launch_fused_attn(f, false, s));
       f.pf_idle = 0;

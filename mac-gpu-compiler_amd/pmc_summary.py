@@ -116,8 +116,8 @@ def main():
         cfg = qe.QWEN3_0_6B
         if a.pf_idle and st == "attn_block":
             # with fewer than 16 runs (up to 1024 positions) the idle and run slots load all 24
-            # gate|up rows of each MLP workgroup
-            extra = 2 * cfg.intermediate_size * cfg.hidden_size * 2 if a.attn_pos < 1024 else 0
+            # gate|up rows of each MLP workgroup, and the o_proj slots the down columns
+            extra = 3 * cfg.intermediate_size * cfg.hidden_size * 2 if a.attn_pos < 1024 else 0
         if a.pf_idle and st == "mlp_block":
             # the MLP block loads the next layer's q|k|v rows
             qd = cfg.num_attention_heads * cfg.head_dim
@@ -171,8 +171,9 @@ def main():
         f"WRITE_SIZE x {fw:.4f}. Attention runs at position {a.attn_pos} ({a.attn_pos + 1} cached positions).",
         "Algorithmic bytes: weights + f32 input + f32 output per matvec; K/V history + q/k/v + output",
         "for attention (the figures `bench.py` divides by the launch time)." +
-        (" The attention block's idle and run workgroups also load the MLP block's gate|up rows into L2, and the"
-         " MLP block the next layer's q|k|v rows (prefetch bytes; the ratio is traffic over own + prefetch bytes)."
+        (" The attention block's idle and run workgroups also load the MLP block's gate|up rows into L2, its"
+         " o_proj workgroups the down columns, and the MLP block the next layer's q|k|v rows (prefetch bytes;"
+         " the ratio is traffic over own + prefetch bytes)."
          if a.pf_idle else "") +
         ("" if a.no_prefetch else " The attention launch also streams the layer's gate/up and down weights into"
          " L2 (prefetch bytes, counted with those stages); its ratio is traffic over own + prefetch bytes."),
