@@ -249,6 +249,11 @@ int qe_op_argmax(const float* logits, uint64_t rows, uint64_t n, uint32_t* token
 /* Streaming read of n floats (n % 4 == 0): the read_sum kernel of tests/read_bandwidth.rs:16-54,
  * writing one partial sum per block to partial[grid]. grid == 0 picks a default. */
 int qe_op_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream);
+/* The same sum with non-temporal loads (not allocated in the MALL), block b reading the contiguous
+ * quarter-float4 range [n/4 b / grid, n/4 (b + 1) / grid): on gfx950 this streaming form reads
+ * faster than the strided one, so the read ceiling is the better of the two. It replaces nothing
+ * in the reference, whose read_bandwidth.rs kernel has one form (tests/read_bandwidth.rs:16-54). */
+int qe_op_read_sum_nt(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1462,7 +1462,7 @@ __global__ __launch_bounds__(256) void k_lm_head_rows(MvRowsParams p) {
     const uint32_t row = min(row0 + uint32_t(r), p.rows - 1);  // past the end: re-read the last row
     const uint4* wr = W + size_t(row) * nch;
 #pragma unroll
-    for (int k = 0; k < CPL; k++) wv[r][k] = wr[min(uint32_t(lane) + 64u * k, nch - 1)];
+    for (int k = 0; k < CPL; k++) wv[r][k] = ld_stream(&wr[min(uint32_t(lane) + 64u * k, nch - 1)]);  // (as k_matvec)
   }
   const float4* x4 = reinterpret_cast<const float4*>(p.x);
   float4* xs4 = reinterpret_cast<float4*>(xs);

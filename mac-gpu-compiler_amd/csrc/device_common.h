@@ -80,6 +80,16 @@ __device__ __forceinline__ float dot8(uint4 u, float4 a, float4 b, float acc) {
   return acc;
 }
 
+// A 16-byte load with the non-temporal hint (`nt`): on gfx950 the line is not allocated in the
+// memory-side cache (MALL), which lets a stream that is read once per step run faster (a 1 GiB
+// stream: 6.8 vs 6.1 TB/s) and leaves the MALL's contents alone. Only for data no later launch
+// expects in a cache: an nt line does not stay in L2 either.
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 ld_stream(const uint4* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __host__ __device__ __forceinline__ uint32_t ceil_div(uint32_t a, uint32_t b) { return (a + b - 1) / b; }
 
 }  // namespace

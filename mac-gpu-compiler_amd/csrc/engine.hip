@@ -133,6 +133,11 @@ struct qe_model {
   uint64_t layer_stride = 0;  // bytes between consecutive layers' tensors in the arena
   uint2 *fqkv = nullptr, *fh = nullptr;  // (value, tag) pairs exchanged inside an XCD
   uint32_t* fsync = nullptr;
+  // a two-row verify pass through the two launches per layer: its step state {pos, 0, ..}, its
+  // two token ids and the RoPE rows of its two positions (res0 .. fh hold kFusedMaxRows rows)
+  StepState* vstate = nullptr;
+  uint32_t* vtokens = nullptr;
+  float* vrope = nullptr;
   uint32_t* place_word = nullptr;
   // extra workgroups per XCD of each attention block that load the layer's MLP weights into the
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
@@ -161,7 +166,7 @@ struct qe_model {
   uint32_t n_ts = 0, ts_cap = 0;
   // pinned host staging
   float* h_logits = nullptr;
-  uint32_t* h_small = nullptr;  // [0..3] state staging, [4] error word
+  uint32_t* h_small = nullptr;  // [0..3] state staging, [8] token, [12] error word, [16..21] verify staging
   uint64_t weight_bytes = 0;
   // decode attention launches also load the next weights into L2 (QE_L2_PREFETCH=0 turns it off)
   bool l2_prefetch = true;
@@ -181,6 +186,8 @@ struct qe_model {
   // ... and their lm_head is the decode step's matvec over all their rows, each row's logits
   // equal to a decode step's (QE_LM_HEAD_ROWS=0: the skinny GEMM; a 2-row pass 0.83 -> 0.80 ms)
   bool lm_head_rows = true;
+  // two-row verify passes through the two launches per layer (QE_VERIFY_FUSED=0: the batch path)
+  bool verify_fused = true;
   // qe_decode_lookup decodes plain blocks while its verify passes emit tokens more slowly than
   // plain steps (QE_LOOKUP_ADAPTIVE=0: always drafts)
   bool lookup_adaptive = true;
@@ -257,12 +264,25 @@ struct qe_kv {
     hipGraphExec_t exec;
   };
   std::vector<StepGraph> graphs;
+  // two-row verify passes (verify_fused): one graph per attention shape and batch logits buffer
+  struct VerifyGraph {
+    uint32_t splits, run;
+    const void* logits;
+    const void* cand;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+  };
+  std::vector<VerifyGraph> vgraphs;
   std::vector<hipEvent_t> events;
   uint64_t len = 0;
 
   ~qe_kv() {
     if (model && model->stream) (void)hipStreamSynchronize(model->stream);
     for (auto& g : graphs) {
+      if (g.exec) (void)hipGraphExecDestroy(g.exec);
+      if (g.graph) (void)hipGraphDestroy(g.graph);
+    }
+    for (auto& g : vgraphs) {
       if (g.exec) (void)hipGraphExecDestroy(g.exec);
       if (g.graph) (void)hipGraphDestroy(g.graph);
     }
@@ -318,6 +338,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* ra = getenv("QE_ROWS_SPLIT_ATTN")) m->rows_split_attn = strcmp(ra, "0") != 0;
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
+  if (const char* vf = getenv("QE_VERIFY_FUSED")) m->verify_fused = strcmp(vf, "0") != 0;
   if (const char* la = getenv("QE_LOOKUP_ADAPTIVE")) m->lookup_adaptive = strcmp(la, "0") != 0;
   if (const char* ps = getenv("QE_PREFILL_STREAMS"))
     m->prefill_streams = std::min(std::max(atoi(ps), 1), kMaxPrefillStreams);
@@ -442,13 +463,16 @@ int qe_model_load(const char* path, qe_model** out) {
   m->n_cand = qe::matvec_num_blocks(uint32_t(V), uint32_t(H), qe::kLogits);
   size_t so = 0;
   auto stake = [&](size_t bytes) { size_t o = so; so = align_up(so + bytes, 256); return o; };
-  const size_t s_x = stake(H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
+  constexpr size_t FR = qe::kFusedMaxRows;
+  const size_t s_x = stake(FR * H * 4), s_qkv = stake((QD + 2 * KD) * 4), s_att = stake(QD * 4), s_h = stake(I * 4),
                s_logits = stake(V * 4), s_cand = stake(size_t(m->n_cand) * sizeof(ArgCand)),
-               s_part = stake(size_t(c.num_key_value_heads) * qe::kAttnMaxWideSplits * G * qe::kPartStride * 4),
-               s_err = stake(4), s_res0 = stake(H * 4), s_res1 = stake(H * 4),
-               s_pa = stake(qe::kFusedXcds * H * 4), s_pm = stake(qe::kFusedXcds * H * 4),
+               s_part = stake(std::max(size_t(c.num_key_value_heads) * qe::kAttnMaxWideSplits * G * qe::kPartStride * 4,
+                                       FR * qe::kFusedPartPairs * 8)),
+               s_err = stake(4), s_res0 = stake(FR * H * 4), s_res1 = stake(FR * H * 4),
+               s_pa = stake(FR * qe::kFusedXcds * H * 4), s_pm = stake(FR * qe::kFusedXcds * H * 4),
                s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4),
-               s_fqkv = stake((qe::kFusedQkvPairs + qe::kFusedAttPairs) * 8), s_fh = stake(qe::kFusedHPairs * 8),
+               s_fqkv = stake(FR * qe::kFusedQkvRowPairs * 8), s_fh = stake(FR * qe::kFusedHPairs * 8),
+               s_vstate = stake(sizeof(StepState) + FR * 4), s_vrope = stake(FR * D * 4),
                s_pxa = stake(qe::kFusedXcds * H * 8), s_pxm = stake(qe::kFusedXcds * H * 8),
                s_ppa = stake(qe::kFusedXcds * H * 8), s_ppm = stake(qe::kFusedXcds * H * 8), s_pgen = stake(256);
   static_assert(qe::kFusedPartPairs * 8 <= size_t(qe::kFusedKv) * qe::kAttnMaxWideSplits * 2 * qe::kPartStride * 4,
@@ -471,6 +495,9 @@ int qe_model_load(const char* path, qe_model** out) {
   m->place_word = reinterpret_cast<uint32_t*>(m->scratch + s_place);
   m->fqkv = reinterpret_cast<uint2*>(m->scratch + s_fqkv);
   m->fh = reinterpret_cast<uint2*>(m->scratch + s_fh);
+  m->vstate = reinterpret_cast<StepState*>(m->scratch + s_vstate);
+  m->vtokens = reinterpret_cast<uint32_t*>(m->scratch + s_vstate + sizeof(StepState));
+  m->vrope = reinterpret_cast<float*>(m->scratch + s_vrope);
   m->pxa = reinterpret_cast<uint2*>(m->scratch + s_pxa);
   m->pxm = reinterpret_cast<uint2*>(m->scratch + s_pxm);
   m->ppa = reinterpret_cast<uint2*>(m->scratch + s_ppa);
@@ -514,7 +541,7 @@ int qe_model_load(const char* path, qe_model** out) {
     if (ok) m->fused = want_mode == 2 && strided && L <= 32 ? 2 : 1;
   }
   HIP_TRY(hipHostMalloc(&m->h_logits, V * 4, hipHostMallocDefault));
-  HIP_TRY(hipHostMalloc(&m->h_small, 64, hipHostMallocDefault));
+  HIP_TRY(hipHostMalloc(&m->h_small, 128, hipHostMallocDefault));
   *out = m.release();
   return QE_OK;
 }
@@ -549,7 +576,7 @@ namespace {
 // the last), with the stage name of the kernel that follows it.
 // Enqueues one decode step on the model's stream. With `only` set, just the kernels of that
 // stage are enqueued (qe_profile_step times each stage this way); `launches` counts them.
-int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches);
+int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches, uint32_t rows = 1);
 // timing-buffer words per launch: a start and an end stamp for each of the layer workgroups
 // (the prefetch workgroups beyond them stamp nothing)
 constexpr size_t kTsPerLaunch = 2 * size_t(qe::kFusedXcds) * qe::kFusedSlots;
@@ -652,7 +679,9 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
 // MLP block; the final reduction of the last layer's partials, the lm_head and the argmax.
 // `only` / `launches` as in enqueue_step, with the stages attn_block, mlp_block, final_reduce,
 // lm_head and argmax.
-int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches) {
+// rows = 2: the layers of a two-row verify pass (m->vstate, m->vtokens, m->vrope), ending with the
+// final residual rows in m->x; the caller runs the lm_head and the argmax over both rows.
+int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches, uint32_t rows) {
   const qe_config& c = m->cfg;
   const uint32_t V = uint32_t(c.vocab_size), D = uint32_t(c.head_dim);
   const size_t el = kv->dtype == QE_KV_BF16 ? 2 : 4;
@@ -673,10 +702,14 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
     return m->ts_buf + size_t(m->n_ts++) * kTsPerLaunch;
   };
   FusedLayerParams f{};
+  f.rows = rows;
   f.qkv = m->fqkv; f.attn_part = reinterpret_cast<uint2*>(m->attn_part); f.h = m->fh;
   f.embed = m->embed; f.tokens = kv->tokens; f.vocab = V; f.state = kv->state;
   f.kv_bf16 = kv->dtype == QE_KV_BF16; f.max_seq = uint32_t(kv->max_seq); f.rope_cur = kv->rope_cur;
   f.splits = kv->step_splits; f.run = kv->step_run;
+  if (rows > 1) {
+    f.state = m->vstate; f.tokens = m->vtokens; f.rope_cur = m->vrope;
+  }
   f.eps = c.rms_norm_eps; f.scale = 1.0f / sqrtf(float(D));
   f.sync = m->fsync; f.err = m->err;
   const uint32_t H = uint32_t(c.hidden_size), I = uint32_t(c.intermediate_size), NX = qe::kFusedXcds;
@@ -747,7 +780,8 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       HIP_TRY(f.ts ? qe::launch_fused_mlp_timed(f, s) : qe::launch_fused_mlp(f, s));
     }
   }
-  if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, s));
+  if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, rows, s));
+  if (rows > 1) return QE_OK;
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = uint32_t(c.hidden_size);
@@ -1600,10 +1634,91 @@ int check_verify_args(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t
   return QE_OK;
 }
 
+constexpr int kNotFused = -1;
+
+// A two-row verify pass (positions pos, pos + 1) through the two launches per layer, every weight
+// read once for both rows; the lm_head over both rows and the device argmax of each row follow.
+// kNotFused when the pass's attention needs more than 16 runs (the batch path takes it).
+// tokens: the greedy token of each row, or null; logits_out: host [R][V] logits, or null.
+int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_kv* kv, uint32_t* tokens,
+                 float* logits_out) {
+  uint32_t splits, run;
+  step_shape(kv, pos + R - 1, splits, run);  // the runs cover positions 0 .. pos + R - 1
+  if (R != qe::kFusedMaxRows || splits > 16) return kNotFused;
+  const qe_config& c = m->cfg;
+  const size_t D = c.head_dim, V = c.vocab_size;
+  HIP_TRY(hipStreamSynchronize(m->stream));  // the staging words are free
+  const StepState st{uint32_t(pos), 0u, uint32_t(kv->max_seq), R};
+  memcpy(m->h_small + 16, &st, sizeof(st));
+  std::copy(ids, ids + R, m->h_small + 20);
+  HIP_TRY(hipMemcpyAsync(m->vstate, m->h_small + 16, sizeof(st) + R * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipMemcpyAsync(m->vrope, kv->rope + pos * D, R * D * 4, hipMemcpyDeviceToDevice, m->stream));
+  // the pass: the layers, the lm_head over both rows, each row's argmax into pinned memory
+  uint32_t* host_tok = reinterpret_cast<uint32_t*>(m->h_logits);
+  auto enqueue = [&]() -> int {
+    const uint32_t ks = kv->step_splits, kr = kv->step_run;
+    kv->step_splits = splits;
+    kv->step_run = run;
+    int rc = enqueue_step_fused(m, kv, nullptr, nullptr, R);
+    kv->step_splits = ks;
+    kv->step_run = kr;
+    if (rc) return rc;
+    const qe::MvRowsParams r{m->lm_head, m->x, m->final_norm, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
+                             uint32_t(V), c.rms_norm_eps};
+    HIP_TRY(qe::launch_lm_head_rows(r, m->stream));
+    HIP_TRY(qe::launch_row_argmax(m->blogits, R, uint32_t(V), host_tok, m->bcand, m->stream));
+    return QE_OK;
+  };
+  int rc = QE_OK;
+  if (kv->eager) {
+    if ((rc = enqueue())) return rc;
+  } else {
+    // one graph per attention shape (the launches are ~60, so a pass replayed from the host
+    // would wait on its launch calls)
+    qe_kv::VerifyGraph* vg = nullptr;
+    for (auto& g : kv->vgraphs)
+      if (g.splits == splits && g.run == run && g.logits == m->blogits && g.cand == m->bcand) vg = &g;
+    if (!vg) {
+      HIP_TRY(hipStreamSynchronize(m->stream));
+      HIP_TRY(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+      rc = enqueue();
+      hipGraph_t g = nullptr;
+      const hipError_t e = hipStreamEndCapture(m->stream, &g);
+      if (rc != QE_OK) {
+        if (g) (void)hipGraphDestroy(g);
+        return rc;
+      }
+      if (e != hipSuccess) return fail(QE_ERR_HIP, "verify graph capture failed: %s", hipGetErrorString(e));
+      hipGraphExec_t ex = nullptr;
+      const hipError_t ie = hipGraphInstantiate(&ex, g, nullptr, nullptr, 0);
+      if (ie != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return fail(QE_ERR_HIP, "verify graph instantiation failed: %s", hipGetErrorString(ie));
+      }
+      kv->vgraphs.push_back({splits, run, m->blogits, m->bcand, g, ex});
+      vg = &kv->vgraphs.back();
+    }
+    HIP_TRY(hipGraphLaunch(vg->exec, m->stream));
+  }
+  if (logits_out)
+    HIP_TRY(hipMemcpyAsync(logits_out, m->blogits, size_t(R) * V * 4, hipMemcpyDeviceToHost, m->stream));
+  // the error word comes back with the results (one synchronization)
+  HIP_TRY(hipMemcpyAsync(m->h_small + 12, m->err, 4, hipMemcpyDeviceToHost, m->stream));
+  HIP_TRY(hipStreamSynchronize(m->stream));
+  if (m->h_small[12] && (rc = check_err(m))) return rc;
+  if (tokens) memcpy(tokens, host_tok, size_t(R) * 4);
+  kv->len = std::max<uint64_t>(kv->len, pos + R);
+  return QE_OK;
+}
+
 // verify pass with the argmax on the device: tokens[i] = greedy token of row i
 int verify_greedy(qe_model* model, const uint32_t* ids, uint32_t k, uint64_t start_pos, qe_kv* kv, uint32_t* tokens) {
   int rc = ensure_batch(model, k, k);
   if (rc) return rc;
+  if (k == qe::kFusedMaxRows && model->fused == 1 && model->verify_fused) {
+    rc = verify_fused(model, ids, k, start_pos, kv, tokens, nullptr);
+    if (rc != kNotFused) return rc;
+  }
   qe::TokenIds tv{};  // k <= kVerifyMaxTokens = kIdsByValue: the ids travel in the kernel argument
   std::copy(ids, ids + k, tv.id);
   if ((rc = enqueue_batch(model, kv, k, uint32_t(start_pos), nullptr, kAllLogits, &tv))) return rc;
@@ -1648,6 +1763,10 @@ int qe_verify(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t start_p
   if (int rc = check_verify_args(model, ids, k, start_pos, kv)) return rc;
   int rc = ensure_batch(model, uint32_t(k), uint32_t(k));
   if (rc) return rc;
+  if (k == qe::kFusedMaxRows && model->fused == 1 && model->verify_fused) {
+    rc = verify_fused(model, ids, uint32_t(k), start_pos, kv, nullptr, logits_out);
+    if (rc != kNotFused) return rc;
+  }
   qe::TokenIds tv{};
   std::copy(ids, ids + k, tv.id);
   if ((rc = enqueue_batch(model, kv, uint32_t(k), uint32_t(start_pos), nullptr, kAllLogits, &tv))) return rc;
@@ -1955,7 +2074,14 @@ int qe_op_argmax(const float* logits, uint64_t rows, uint64_t n, uint32_t* token
 int qe_op_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream) {
   if (!src || !partial) return fail(QE_ERR_ARG, "null argument");
   if (n % 4) return fail(QE_ERR_ARG, "n must be a multiple of 4");
-  HIP_TRY(qe::launch_read_sum(src, n, partial, grid ? grid : 2048, static_cast<hipStream_t>(stream)));
+  HIP_TRY(qe::launch_read_sum(src, n, partial, grid ? grid : 2048, false, static_cast<hipStream_t>(stream)));
+  return QE_OK;
+}
+
+int qe_op_read_sum_nt(const float* src, uint64_t n, float* partial, uint32_t grid, void* stream) {
+  if (!src || !partial) return fail(QE_ERR_ARG, "null argument");
+  if (n % 4) return fail(QE_ERR_ARG, "n must be a multiple of 4");
+  HIP_TRY(qe::launch_read_sum(src, n, partial, grid ? grid : 2048, true, static_cast<hipStream_t>(stream)));
   return QE_OK;
 }
 

@@ -69,6 +69,7 @@ namespace {
 constexpr uint32_t H = kFusedH, I = kFusedI, D = kHeadDim, NKV = kFusedKv, G = kFusedHeads / kFusedKv;
 constexpr uint32_t QD = kFusedHeads * D, KD = NKV * D;
 constexpr uint32_t NX = kFusedXcds, NS = kFusedSlots;
+constexpr uint32_t kQkvRowPairs = uint32_t(kFusedQkvRowPairs);  // p.qkv pairs per token row
 
 static_assert(NKV == NX, "one KV head per XCD");
 static_assert(G == 2 && H == 1024 && I == 3072, "the launch layouts below are written for these sizes");
@@ -126,21 +127,30 @@ __device__ __forceinline__ void finish(const KcacheWarm& w, uint64_t* ts, uint64
 
 // x[4 tid .. 4 tid + 3] = xin + part[0] + ... + part[7] (a fixed order) into xs; workgroup 0
 // also stores it to res_out. Returns the RMSNorm scale 1 / sqrt(mean(x^2) + eps) of all of x.
-__device__ __forceinline__ float residual_and_scale(float4 xin, const float4 (&xp)[NX], bool add_parts, float* xs,
-                                                    float* res_out, float eps, float* red4) {
+// R rows (a verify pass): row r from xin[r], xp[r] into xs + r H and res_out + r H, scale rs[r].
+template <int R>
+__device__ __forceinline__ void residual_and_scale(const float4 (&xin)[R], const float4 (&xp)[R][NX], bool add_parts,
+                                                   float* xs, float* res_out, float eps, float (*red4)[4],
+                                                   float (&rs)[R]) {
   const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float4 v = xin;
-  if (add_parts) {
 #pragma unroll
-    for (uint32_t g = 0; g < NX; g++) v = add4(v, xp[g]);
+  for (int r = 0; r < R; r++) {
+    float4 v = xin[r];
+    if (add_parts) {
+#pragma unroll
+      for (uint32_t g = 0; g < NX; g++) v = add4(v, xp[r][g]);
+    }
+    reinterpret_cast<float4*>(xs + r * H)[tid] = v;
+    if (blockIdx.x == 0) reinterpret_cast<float4*>(res_out + r * H)[tid] = v;
+    const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+    if (lane == 0) red4[r][wave] = ss;
   }
-  reinterpret_cast<float4*>(xs)[tid] = v;
-  if (blockIdx.x == 0) reinterpret_cast<float4*>(res_out)[tid] = v;
-  const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
-  if (lane == 0) red4[wave] = ss;
   __syncthreads();
-  const float tot = (red4[0] + red4[1]) + (red4[2] + red4[3]);
-  return 1.0f / sqrtf(tot / float(H) + eps);
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    const float tot = (red4[r][0] + red4[r][1]) + (red4[r][2] + red4[r][3]);
+    rs[r] = 1.0f / sqrtf(tot / float(H) + eps);
+  }
 }
 
 // first q|k|v row of slot s of KV head x: slots 0-15 take 16 rows each of q heads 2x, 2x+1,
@@ -230,16 +240,21 @@ __device__ __forceinline__ void prefetch_region(const FusedLayerParams& p, uint3
 // attention block of one layer. SM: merge slots (>= splits), KV_BF16: cache element type,
 // MULTI: runs of more than one 64-position tile (only with 32 runs), NT: positions per tile and
 // per single-tile run (64, or 32 for short contexts: half the K/V each run's CU takes in).
+// R: token rows (1: a decode step; 2: a verify pass over positions pos and pos + 1, whose rows
+// share every weight load; row r's buffers sit r row strides on, its q heads are q vectors
+// r G .. r G + G - 1 of the KV head, and it attends to positions 0 .. pos + r).
 // ---------------------------------------------------------------------------------------------
 // The arguments the first loads need come first, as plain pointers (preloaded into scalar
 // registers at wave launch, as in k_fused_mlp).
-template <bool FIRST, bool KV_BF16, int SM, bool MULTI, int NT>
+template <bool FIRST, bool KV_BF16, int SM, bool MULTI, int NT, int R>
 __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepState* state, const float* res_in,
                                                     const float* part_in, const uint16_t* w_qkv, const uint16_t* w_in,
                                                     uint32_t n_runs, uint32_t run_len, FusedLayerParams p) {
   static_assert(SM == 32 || !MULTI, "runs of several tiles come with 32 runs");
   static_assert(NT == 64 || (NT == 32 && !MULTI), "runs of several tiles use 64-position tiles");
+  static_assert(R == 1 || (R == 2 && SM <= 16), "verify rows: single-tile runs, up to 16");
   constexpr uint32_t T = NT, VP = NT / 8;  // positions per tile, per thread in the P.V layout
+  constexpr uint32_t QV = R * G;           // q vectors per KV head
   // o_proj: with up to 16 runs, slots 16..31 take 64 rows each (4 per 16-thread row group), so
   // the attention runs (slots 0..15) carry no o_proj weights; with 32 runs every slot takes 32
   constexpr uint32_t ORR = SM <= 16 ? 4 : 2;
@@ -259,16 +274,16 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   const bool oproj = SM <= 16 ? s >= 16 : true;
   const uint32_t orow0 = SM <= 16 ? 64 * (s - 16) : 32 * s;
 
-  __shared__ __align__(16) float xs[H];
-  __shared__ float red4[4];
-  __shared__ __align__(16) float qs[G][D];
-  __shared__ __align__(16) float knew[D];
-  __shared__ __align__(16) float vnew[D];
-  __shared__ float sc[G][T], pes[G][T];
-  __shared__ float Ms[G], Ls[G], Cs[G];
-  __shared__ __align__(16) float red[8][G][D];
-  __shared__ __align__(16) float att[G * D];
-  __shared__ float mw[G][SM], msum[G];  // merge weights of the runs and their sums per head
+  __shared__ __align__(16) float xs[R * H];
+  __shared__ float red4[R][4];
+  __shared__ __align__(16) float qs[QV][D];
+  __shared__ __align__(16) float knew[R][D];
+  __shared__ __align__(16) float vnew[R][D];
+  __shared__ float sc[QV][T], pes[QV][T];
+  __shared__ float Ms[QV], Ls[QV], Cs[QV];
+  __shared__ __align__(16) float red[8][QV][D];
+  __shared__ __align__(16) float att[R][G * D];
+  __shared__ float mw[QV][SM], msum[QV];  // merge weights of the runs and their sums per q vector
 
   const uint32_t tag = *gen_word(sync, x) + 1;
   // this step's position (set before the step's first launch), read now so that no load of it
@@ -282,22 +297,25 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 
   // ---- loads that depend on no other workgroup, issued before any use ----
   // the residual stream (from the previous launch) or the embedding row
-  float4 xin;
-  float4 xp[NX];
-  if constexpr (FIRST) {
-    uint32_t tok = p.tokens[state->tok_idx];
-    if (tok >= p.vocab) {
-      if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
-      tok = 0;
+  float4 xin[R];
+  float4 xp[R][NX];
+#pragma unroll
+  for (int r = 0; r < R; r++) {
+    if constexpr (FIRST) {
+      uint32_t tok = p.tokens[state->tok_idx + r];
+      if (tok >= p.vocab) {
+        if (blockIdx.x == 0 && tid == 0) atomicOr(p.err, kErrToken);
+        tok = 0;
+      }
+      const uint2 e = reinterpret_cast<const uint2*>(p.embed + size_t(tok) * H)[tid];
+      xin[r] = bf16x4(e.x, e.y);
+#pragma unroll
+      for (uint32_t g = 0; g < NX; g++) xp[r][g] = make_float4(0.f, 0.f, 0.f, 0.f);
+    } else {
+      xin[r] = reinterpret_cast<const float4*>(res_in + r * H)[tid];
+#pragma unroll
+      for (uint32_t g = 0; g < NX; g++) xp[r][g] = reinterpret_cast<const float4*>(part_in + (r * NX + g) * H)[tid];
     }
-    const uint2 e = reinterpret_cast<const uint2*>(p.embed + size_t(tok) * H)[tid];
-    xin = bf16x4(e.x, e.y);
-#pragma unroll
-    for (uint32_t g = 0; g < NX; g++) xp[g] = make_float4(0.f, 0.f, 0.f, 0.f);
-  } else {
-    xin = reinterpret_cast<const float4*>(res_in)[tid];
-#pragma unroll
-    for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
   }
   // q|k|v: row group = wave, 4 rows of 1024 columns, lane l holds chunks l and l + 64
   const uint4* Wq = reinterpret_cast<const uint4*>(w_qkv);
@@ -337,7 +355,10 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   __builtin_amdgcn_sched_barrier(0);
   const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
   const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
-  const float2 cs = reinterpret_cast<const float2*>(p.rope_cur)[lane];
+  // RoPE rows of positions pos .. pos + R - 1 (consecutive rows of D floats)
+  float2 cs[R];
+#pragma unroll
+  for (int r = 0; r < R; r++) cs[r] = reinterpret_cast<const float2*>(p.rope_cur + r * D)[lane];
   if constexpr (NT != 32) load_first_tile();
   // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
@@ -355,23 +376,32 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 
   // ---- input RMSNorm + this workgroup's 16 q|k|v rows (cpu_inference.rs:129-132) ----
   {
-    const float rs = residual_and_scale(xin, xp, !FIRST, xs, p.res_out, p.eps, red4);
+    float rs[R];
+    residual_and_scale<R>(xin, xp, !FIRST, xs, p.res_out, p.eps, red4, rs);
     if constexpr (NT == 32) load_first_tile();
-    const float4* xs4 = reinterpret_cast<const float4*>(xs);
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    float acc[R][4];
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const uint32_t c = lane + 64 * k;
-      float4 a = xs4[2 * c], b = xs4[2 * c + 1];
-      scale8(a, b, gin[k]);
+    for (int t = 0; t < R; t++) {
+      const float4* xs4 = reinterpret_cast<const float4*>(xs + t * H);
 #pragma unroll
-      for (int r = 0; r < 4; r++) acc[r] = dot8(wq[r][k], a, b, acc[r]);
+      for (int r = 0; r < 4; r++) acc[t][r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t c = lane + 64 * k;
+        float4 a = xs4[2 * c], b = xs4[2 * c + 1];
+        scale8(a, b, gin[k]);
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[t][r] = dot8(wq[r][k], a, b, acc[t][r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; r++) acc[t][r] = wave_sum(acc[t][r]) * rs[t];
     }
-#pragma unroll
-    for (int r = 0; r < 4; r++) acc[r] = wave_sum(acc[r]) * rs;
     if (lane == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; r++) p.qkv[qrow0 + r] = pair(acc[r], tag);
+      for (int t = 0; t < R; t++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) p.qkv[t * kQkvRowPairs + qrow0 + r] = pair(acc[t][r], tag);
+      }
     }
   }
   if (SM > 16 && attn) load_wo();
@@ -408,80 +438,100 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     if constexpr (!MULTI) load_gdn();
   };
   auto attention = [&]() __attribute__((always_inline)) {
-    // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v]; lane l holds dims l, l + 64
-    const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, uint32_t(kFusedQkvPairs * 8));
+    // raw rows: wave w takes row w of [q head 2x, q head 2x+1, k, v] of every token row; lane l
+    // holds dims l, l + 64
+    const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, uint32_t(R * kQkvRowPairs * 8));
     const uint32_t off = wave < G ? (x * G + wave) * D : wave == G ? QD + x * D : QD + KD + x * D;
-    uint2 qa, qb;
+    uint2 qa[R], qb[R];
     for (uint32_t spins = 0;;) {
-      qa = ld_pair(rq, off + lane);
-      qb = ld_pair(rq, off + lane + 64);
-      if (poll_done(qa.y == tag && qb.y == tag, spins, p.err)) break;
+      bool ok = true;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        qa[r] = ld_pair(rq, r * kQkvRowPairs + off + lane);
+        qb[r] = ld_pair(rq, r * kQkvRowPairs + off + lane + 64);
+        ok = ok && qa[r].y == tag && qb[r].y == tag;
+      }
+      if (poll_done(ok, spins, p.err)) break;
     }
-    float a = __uint_as_float(qa.x), b = __uint_as_float(qb.x);
 #if QE_PF32
     if constexpr (SM == 32 && !MULTI) load_gpf();  // (see gpf above)
 #endif
 
     const uint32_t pos = pos_step;
-    const bool bad = pos >= p.max_seq;
+    const bool bad = R == 1 ? pos >= p.max_seq : pos + R > p.max_seq;
     if (bad && x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrPos);
-    uint32_t n = bad ? 0u : pos + 1;
+    uint32_t n = bad ? 0u : pos + R;  // positions 0 .. pos + R - 1
     const uint32_t run = run_len;
     if (n > splits * run) {  // the host's runs would skip positions
       if (x == 0 && s == 0 && tid == 0) atomicOr(p.err, kErrShape);
       n = 0;
     }
     const uint32_t t0 = s * run, t1 = min(n, t0 + run);
-    const bool owns_new = n != 0 && pos >= t0 && pos < t0 + run;
+    const bool owns_new = n != 0 && pos >= t0 && pos < t0 + run;  // (row 0)
+    // row r sees positions up to pos + r (cpu_inference.rs:144-162 at each row's position)
+    uint32_t t1r[R];
+    t1r[0] = t1;
+#pragma unroll
+    for (int r = 1; r < R; r++) t1r[r] = min(n == 0 ? 0u : pos + r + 1, t0 + run);
+    if constexpr (R > 1) t1r[0] = min(n == 0 ? 0u : pos + 1, t0 + run);
 
-    // q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215)
-    if (wave <= G) {
-      const float ss = wave_sum(a * a + b * b);
-      const float scl = 1.0f / sqrtf(ss / float(D) + p.eps);
-      a = a * scl * bf16f(wave < G ? gq[0] : gk[0]);
-      b = b * scl * bf16f(wave < G ? gq[1] : gk[1]);
-      const float ar = a * cs.x - b * cs.y, br = b * cs.x + a * cs.y;
-      a = ar;
-      b = br;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      float a = __uint_as_float(qa[r].x), b = __uint_as_float(qb[r].x);
+      // q/k RMSNorm (cpu_inference.rs:189-194) + rotate-half RoPE (cpu_inference.rs:203-215)
+      if (wave <= G) {
+        const float ss = wave_sum(a * a + b * b);
+        const float scl = 1.0f / sqrtf(ss / float(D) + p.eps);
+        a = a * scl * bf16f(wave < G ? gq[0] : gk[0]);
+        b = b * scl * bf16f(wave < G ? gq[1] : gk[1]);
+        const float ar = a * cs[r].x - b * cs[r].y, br = b * cs[r].x + a * cs[r].y;
+        a = ar;
+        b = br;
+      }
+      if (KV_BF16 && wave >= G) {  // attend with the values later steps read back
+        a = bf16f(f32_to_bf16(a));
+        b = bf16f(f32_to_bf16(b));
+      }
+      float* dst = wave < G ? qs[r * G + wave] : (wave == G ? knew[r] : vnew[r]);
+      dst[lane] = a;
+      dst[lane + 64] = b;
     }
-    if (KV_BF16 && wave >= G) {  // attend with the values later steps read back
-      a = bf16f(f32_to_bf16(a));
-      b = bf16f(f32_to_bf16(b));
-    }
-    float* dst = wave < G ? qs[wave] : (wave == G ? knew : vnew);
-    dst[lane] = a;
-    dst[lane + 64] = b;
-    if (tid < G) {
+    if (tid < QV) {
       Ms[tid] = -INFINITY;
       Ls[tid] = 0.f;
     }
     __syncthreads();
-    if (owns_new) {  // append the new K/V row (cpu_inference.rs:140-141)
-      const size_t slot = head_base + size_t(pos) * D + (tid & (D - 1));
-      const float val = tid < D ? knew[tid] : vnew[tid - D];
-      void* cache = wave < 2 ? p.k_cache : p.v_cache;  // (threads tid < D: waves 0 and 1)
-      if (KV_BF16) static_cast<uint16_t*>(cache)[slot] = f32_to_bf16(val);
-      else static_cast<float*>(cache)[slot] = val;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      if (r == 0 ? owns_new : n != 0 && pos + r >= t0 && pos + r < t0 + run) {  // append new K/V row r (cpu_inference.rs:140-141)
+        const size_t slot = head_base + size_t(pos + r) * D + (tid & (D - 1));
+        const float val = tid < D ? knew[r][tid] : vnew[r][tid - D];
+        void* cache = wave < 2 ? p.k_cache : p.v_cache;  // (threads tid < D: waves 0 and 1)
+        if (KV_BF16) static_cast<uint16_t*>(cache)[slot] = f32_to_bf16(val);
+        else static_cast<float*>(cache)[slot] = val;
+      }
     }
 
-    float4 acc[G];
+    float4 acc[QV];
 #pragma unroll
-    for (uint32_t j = 0; j < G; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t j = 0; j < QV; j++) acc[j] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     auto process = [&](const KVTile<KV_BF16, NT>& X, uint32_t tile) __attribute__((always_inline)) {
-      // scores s_t = (q . k_t) * scale (cpu_inference.rs:144-152); the new position's k is knew
+      // scores s_t = (q . k_t) * scale (cpu_inference.rs:144-152); the new positions' k rows are
+      // knew (the cache rows this launch writes are not read back)
 #pragma unroll
       for (int u = 0; u < int(NT / 32); u++) {
         const uint32_t t = tile + uint32_t(pg + 32 * u);
         float4 k4[4];
         tile_k<KV_BF16>(X, u, k4);
-        const bool sub = owns_new && t == pos;
-        const float4* kn = reinterpret_cast<const float4*>(knew) + 4 * dc;
+        const uint32_t dn = t - pos;  // new row dn when dn < R
+        const bool sub = R == 1 ? owns_new && t == pos : n != 0 && dn < uint32_t(R);
+        const float4* kn = reinterpret_cast<const float4*>(knew[R == 1 ? 0 : min(dn, uint32_t(R - 1))]) + 4 * dc;
 #pragma unroll
         for (int i = 0; i < 4; i++) k4[i] = sel4(sub, kn[i], k4[i]);
-        float sv[G];
+        float sv[QV];
 #pragma unroll
-        for (uint32_t j = 0; j < G; j++) {
+        for (uint32_t j = 0; j < QV; j++) {
           const float4* qj = reinterpret_cast<const float4*>(qs[j]) + 4 * dc;
           float d = 0.f;
 #pragma unroll
@@ -493,12 +543,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
         }
         if (dc == 0) {
 #pragma unroll
-          for (uint32_t j = 0; j < G; j++) sc[j][pg + 32 * u] = t < t1 ? sv[j] * p.scale : -INFINITY;
+          for (uint32_t j = 0; j < QV; j++) sc[j][pg + 32 * u] = t < t1r[j / G] ? sv[j] * p.scale : -INFINITY;
         }
       }
       __syncthreads();
       // softmax (cpu_inference.rs:217-223) as an online update: running max, rescaled sum
-      if (wave < G) {
+      if (wave < QV) {
         const uint32_t j = wave;
         const float xv = lane < T ? sc[j][lane] : -INFINITY;
         const float m_old = Ms[j];
@@ -516,15 +566,22 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       __syncthreads();
       // out += p_t * v_t (cpu_inference.rs:153-160); positions past the run add 0
       float4 v4[VP];
-      const float4 vn = reinterpret_cast<const float4*>(vnew)[dg];
+      float4 vn[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) vn[r] = reinterpret_cast<const float4*>(vnew[r])[dg];
 #pragma unroll
       for (int i = 0; i < int(VP); i++) {
         const uint32_t t = tile + uint32_t(VP * pp + i);
-        v4[i] = sel4(owns_new && t == pos, vn, tile_v<KV_BF16>(X, i));
+        if constexpr (R == 1) {
+          v4[i] = sel4(owns_new && t == pos, vn[0], tile_v<KV_BF16>(X, i));
+        } else {
+          const uint32_t dn = t - pos;
+          v4[i] = sel4(n != 0 && dn < uint32_t(R), dn == 0 ? vn[0] : vn[1], tile_v<KV_BF16>(X, i));
+        }
         v4[i] = sel4(t < t1, v4[i], make_float4(0.f, 0.f, 0.f, 0.f));
       }
 #pragma unroll
-      for (uint32_t j = 0; j < G; j++) {
+      for (uint32_t j = 0; j < QV; j++) {
         const float c = Cs[j];
         float4 o = make_float4(acc[j].x * c, acc[j].y * c, acc[j].z * c, acc[j].w * c);
 #pragma unroll
@@ -565,11 +622,12 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 
     // the 8 position groups meet; m and l are the softmax state; the partial goes out as pairs
 #pragma unroll
-    for (uint32_t j = 0; j < G; j++) reinterpret_cast<float4*>(red[pp][j])[dg] = acc[j];
+    for (uint32_t j = 0; j < QV; j++) reinterpret_cast<float4*>(red[pp][j])[dg] = acc[j];
     __syncthreads();
-    uint2* part = p.attn_part + (size_t(x) * kFusedMaxRuns + s) * G * kPartStride;
-    {
-      const uint32_t j = tid / D, d = tid % D;  // 256 threads = G x D outputs
+    uint2* part = p.attn_part + (size_t(x) * kFusedMaxRuns + s) * QV * kPartStride;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t j = r * G + tid / D, d = tid % D;  // 256 threads = G x D outputs per row
       float v = 0.f;
 #pragma unroll
       for (int q = 0; q < 8; q++) v += red[q][j][d];
@@ -585,78 +643,113 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   // out = sum_s e_s acc_s / sum_s e_s l_s, e_s = exp(m_s - max m); empty runs (m = -inf) and
   // slots past the last run weigh 0.
   auto merge_oproj = [&]() __attribute__((always_inline)) {
-    const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * G * kPartStride,
-                                              uint32_t(kFusedMaxRuns * G * kPartStride * 8));
+    const __amdgpu_buffer_rsrc_t rp = rsrc_of(p.attn_part + size_t(x) * kFusedMaxRuns * QV * kPartStride,
+                                              uint32_t(kFusedMaxRuns * QV * kPartStride * 8));
     if constexpr (SM >= QE_MERGE2_MIN_SM) {
       // In two rounds. The OW slots with o_proj rows (all 32 with 32 runs, else slots 16..31)
-      // each merge VW = 256 / OW of the XCD's 256 values (head j1) over the runs: thread t takes
-      // run t / VW, value t % VW, wave 0 lanes 0..SM-1 the (m, l) of the runs; the merged values go
-      // out as pairs after the q|k|v pairs, and every o_proj slot then gathers the 256 (one per
-      // thread), instead of each polling SM pairs per thread of every run.
+      // each merge VW = 256 / OW of the XCD's 256 values (head j1) of every token row over the
+      // runs: thread t takes run t / VW, value t % VW, wave 0 lanes 0..SM-1 the (m, l) of the runs;
+      // the merged values go out as pairs after the q|k|v pairs, and every o_proj slot then
+      // gathers the 256 of each row (one per thread), instead of each polling SM pairs per thread
+      // of every run.
       constexpr uint32_t OW = SM <= 16 ? 16 : 32, VW = G * D / OW;
       const uint32_t o = SM <= 16 ? s - 16 : s;
       const uint32_t q = tid / VW, e = tid % VW, j1 = (VW * o) / D;
       const uint32_t d1 = (VW * o) % D + e;
       const bool live = wave == 0 && lane < SM && lane < splits;
       const bool mine = q < SM && q < splits;
-      uint4 ml = make_uint4(0u, 0u, 0u, 0u);
-      uint2 a1 = make_uint2(0u, 0u);
+      uint4 ml[R];
+      uint2 a1[R];
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        ml[r] = make_uint4(0u, 0u, 0u, 0u);
+        a1[r] = make_uint2(0u, 0u);
+      }
       for (uint32_t spins = 0;;) {
-        if (wave == 0) ml = ld_pair2(rp, (min(lane, splits - 1) * G + j1) * kPartStride);
-        a1 = ld_pair(rp, (min(q, splits - 1) * G + j1) * kPartStride + 4 + d1);
-        const bool ok = (!live || (ml.y == tag && ml.w == tag)) && (!mine || a1.y == tag);
+        bool ok = true;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const uint32_t jq = r * G + j1;
+          if (wave == 0) ml[r] = ld_pair2(rp, (min(lane, splits - 1) * QV + jq) * kPartStride);
+          a1[r] = ld_pair(rp, (min(q, splits - 1) * QV + jq) * kPartStride + 4 + d1);
+          ok = ok && (!live || (ml[r].y == tag && ml[r].w == tag)) && (!mine || a1[r].y == tag);
+        }
         if (poll_done(ok, spins, p.err)) break;
       }
       if (wave == 0) {
-        const float m = live ? __uint_as_float(ml.x) : -INFINITY;
-        float M = m;
 #pragma unroll
-        for (int w = 1; w < int(SM); w <<= 1) M = fmaxf(M, __shfl_xor(M, w));
-        const float wt = m != -INFINITY ? expf(m - M) : 0.f;
-        float L = wt * (live ? __uint_as_float(ml.z) : 0.f);
+        for (int r = 0; r < R; r++) {
+          const float m = live ? __uint_as_float(ml[r].x) : -INFINITY;
+          float M = m;
 #pragma unroll
-        for (int w = 1; w < int(SM); w <<= 1) L += __shfl_xor(L, w);
-        if (lane < SM) mw[0][lane] = wt;
-        if (lane == 0) msum[0] = L;
+          for (int w = 1; w < int(SM); w <<= 1) M = fmaxf(M, __shfl_xor(M, w));
+          const float wt = m != -INFINITY ? expf(m - M) : 0.f;
+          float L = wt * (live ? __uint_as_float(ml[r].z) : 0.f);
+#pragma unroll
+          for (int w = 1; w < int(SM); w <<= 1) L += __shfl_xor(L, w);
+          if (lane < SM) mw[r][lane] = wt;
+          if (lane == 0) msum[r] = L;
+        }
       }
       __syncthreads();
       // sum over the runs: the lanes of a wave with the same value index, then the 4 waves in LDS
-      float c = mine ? mw[0][q] * __uint_as_float(a1.x) : 0.f;
 #pragma unroll
-      for (uint32_t w = VW; w < 64; w <<= 1) c += __shfl_xor(c, w);
-      if (lane < VW) red[wave][0][lane] = c;
+      for (int r = 0; r < R; r++) {
+        float c = mine ? mw[r][q] * __uint_as_float(a1[r].x) : 0.f;
+#pragma unroll
+        for (uint32_t w = VW; w < 64; w <<= 1) c += __shfl_xor(c, w);
+        if (lane < VW) red[wave][r][lane] = c;
+      }
       __syncthreads();
       uint2* ax = p.qkv + kFusedQkvPairs + size_t(x) * (G * D);
       if (tid < VW) {
-        const float v = ((red[0][0][tid] + red[1][0][tid]) + (red[2][0][tid] + red[3][0][tid])) * (1.0f / msum[0]);
-        ax[VW * o + tid] = pair(v, tag);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          const float v = ((red[0][r][tid] + red[1][r][tid]) + (red[2][r][tid] + red[3][r][tid])) * (1.0f / msum[r]);
+          ax[r * kQkvRowPairs + VW * o + tid] = pair(v, tag);
+        }
       }
-      const __amdgpu_buffer_rsrc_t ra = rsrc_of(ax, G * D * 8);
-      uint2 av1;
+      const __amdgpu_buffer_rsrc_t ra = rsrc_of(ax, ((R - 1) * kQkvRowPairs + G * D) * 8);
+      uint2 av1[R];
       for (uint32_t spins = 0;;) {
-        av1 = ld_pair(ra, tid);
-        if (poll_done(av1.y == tag, spins, p.err)) break;
+        bool ok = true;
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+          av1[r] = ld_pair(ra, r * kQkvRowPairs + tid);
+          ok = ok && av1[r].y == tag;
+        }
+        if (poll_done(ok, spins, p.err)) break;
       }
-      att[tid] = __uint_as_float(av1.x);
+#pragma unroll
+      for (int r = 0; r < R; r++) att[r][tid] = __uint_as_float(av1[r].x);
       asm volatile("" ::"v"(gpf[0] ^ gpf[1] ^ gpf[2] ^ gpf[3] ^ gpf[4]));  // (in: the polls waited for every load)
       __syncthreads();
     } else {
-    // Wave 0 takes the (m, l) of every run (lane u: head u / SM, run u % SM) and leaves the
+    // Wave 0 takes the (m, l) of every run (lane u: q vector u / SM, run u % SM) and leaves the
     // weights e_s and the sums in LDS; then thread (head 2x + tid / 128, dim tid % 128) adds up its
-    // acc values. One poll round trip for both: wave 0's (m, l) pairs and every thread's acc values.
+    // acc values of every row. One poll round trip for both: wave 0's (m, l) pairs and every
+    // thread's acc values.
+    static_assert(QV * SM <= 64, "one (m, l) pair per lane of wave 0");
     const uint32_t j = tid >> 7, d = tid & 127;
-    const uint32_t jh = min(lane / SM, G - 1), u = lane % SM;
-    const bool live = wave == 0 && lane < G * SM && u < splits;
-    const uint32_t base = (min(u, splits - 1) * G + jh) * kPartStride;
+    const uint32_t jh = min(lane / SM, QV - 1), u = lane % SM;
+    const bool live = wave == 0 && lane < QV * SM && u < splits;
+    const uint32_t base = (min(u, splits - 1) * QV + jh) * kPartStride;
     uint4 ml = make_uint4(0u, 0u, 0u, 0u);  // pairs m, l (wave 0)
-    uint2 av[SM];
+    uint2 av[R][SM];
     for (uint32_t spins = 0;;) {
       if (wave == 0) ml = ld_pair2(rp, base);
 #pragma unroll
-      for (int q = 0; q < SM; q++) av[q] = ld_pair(rp, (min(uint32_t(q), splits - 1) * G + j) * kPartStride + 4 + d);
+      for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int q = 0; q < SM; q++)
+          av[r][q] = ld_pair(rp, (min(uint32_t(q), splits - 1) * QV + r * G + j) * kPartStride + 4 + d);
+      }
       bool ok = !live || (ml.y == tag && ml.w == tag);
 #pragma unroll
-      for (int q = 0; q < SM; q++) ok = ok && av[q].y == tag;
+      for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int q = 0; q < SM; q++) ok = ok && av[r][q].y == tag;
+      }
       if (poll_done(ok, spins, p.err)) break;
     }
     if (wave == 0) {
@@ -668,38 +761,46 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
       float L = e * (live ? __uint_as_float(ml.z) : 0.f);
 #pragma unroll
       for (int o = 1; o < SM; o <<= 1) L += __shfl_xor(L, o);
-      if (lane < G * SM) {
+      if (lane < QV * SM) {
         mw[jh][u] = e;
         if (u == 0) msum[jh] = L;
       }
     }
     __syncthreads();
-    {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+      const uint32_t jq = r * G + j;
       float Av = 0.f;
 #pragma unroll
-      for (int q = 0; q < SM; q++) Av += uint32_t(q) < splits ? mw[j][q] * __uint_as_float(av[q].x) : 0.f;
-      att[tid] = Av * (1.0f / msum[j]);
+      for (int q = 0; q < SM; q++) Av += uint32_t(q) < splits ? mw[jq][q] * __uint_as_float(av[r][q].x) : 0.f;
+      att[r][tid] = Av * (1.0f / msum[jq]);
     }
     __syncthreads();
     }
     // o_proj over this XCD's 256 columns (cpu_inference.rs:163-164): the partial of rows orow0..;
     // the next launch adds the 8 partials and the residual
-    const float4* at4 = reinterpret_cast<const float4*>(att);
-    float oa[ORR];
+    float oa[R][ORR];
 #pragma unroll
-    for (uint32_t r = 0; r < ORR; r++) oa[r] = 0.f;
+    for (int t = 0; t < R; t++) {
+      const float4* at4 = reinterpret_cast<const float4*>(att[t]);
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const uint32_t c = t16 + 16 * k;
-      const float4 a = at4[2 * c], b = at4[2 * c + 1];
+      for (uint32_t r = 0; r < ORR; r++) oa[t][r] = 0.f;
 #pragma unroll
-      for (uint32_t r = 0; r < ORR; r++) oa[r] = dot8(wo[r][k], a, b, oa[r]);
+      for (int k = 0; k < 2; k++) {
+        const uint32_t c = t16 + 16 * k;
+        const float4 a = at4[2 * c], b = at4[2 * c + 1];
+#pragma unroll
+        for (uint32_t r = 0; r < ORR; r++) oa[t][r] = dot8(wo[r][k], a, b, oa[t][r]);
+      }
+#pragma unroll
+      for (uint32_t r = 0; r < ORR; r++) oa[t][r] = sum16(oa[t][r]);
     }
-#pragma unroll
-    for (uint32_t r = 0; r < ORR; r++) oa[r] = sum16(oa[r]);
     if (t16 == 0) {
 #pragma unroll
-      for (uint32_t r = 0; r < ORR; r++) p.part_out[x * H + orow0 + ORR * rg + r] = oa[r];
+      for (int t = 0; t < R; t++) {
+#pragma unroll
+        for (uint32_t r = 0; r < ORR; r++) p.part_out[(t * NX + x) * H + orow0 + ORR * rg + r] = oa[t][r];
+      }
     }
   };
 
@@ -746,6 +847,7 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
 // The arguments the first loads need come first, as plain pointers: those are preloaded into
 // scalar registers at wave launch (the build's -amdgpu-kernarg-preload-count), so the loads do not
 // wait for a scalar load of the argument block.
+template <int R>
 __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* res_in, const float* part_in,
                                                    const uint16_t* w_gu, const uint16_t* w_post, const uint16_t* w_down,
                                                    const uint16_t* qkv_next, FusedLayerParams p) {
@@ -759,9 +861,9 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   const uint64_t t_start = clock_start();
   const KcacheWarm kw = kcache_warm();
   const uint32_t s = blockIdx.x / NX;
-  __shared__ __align__(16) float xs[H];
-  __shared__ float red4[4];
-  __shared__ __align__(16) float hs[I / NX];  // this XCD's h values
+  __shared__ __align__(16) float xs[R * H];
+  __shared__ float red4[R][4];
+  __shared__ __align__(16) float hs[R][I / NX];  // this XCD's h values of every token row
 
   const uint32_t tag = *gen_word(sync, x) + 1;
 
@@ -778,10 +880,14 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
     for (int k = 0; k < 2; k++) wg[r][k] = Wg[size_t(row0 + r) * (H / 8) + lane + 64 * k];
   }
   __builtin_amdgcn_sched_barrier(0);
-  const float4 xin = reinterpret_cast<const float4*>(res_in)[tid];
-  float4 xp[NX];
+  float4 xin[R];
+  float4 xp[R][NX];
 #pragma unroll
-  for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part_in + g * H)[tid];
+  for (int r = 0; r < R; r++) {
+    xin[r] = reinterpret_cast<const float4*>(res_in + r * H)[tid];
+#pragma unroll
+    for (uint32_t g = 0; g < NX; g++) xp[r][g] = reinterpret_cast<const float4*>(part_in + (r * NX + g) * H)[tid];
+  }
   __builtin_amdgcn_sched_barrier(0);
   uint4 gp[2];
 #pragma unroll
@@ -809,24 +915,33 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
 
   // post_attention_layernorm + gate|up + silu * up (cpu_inference.rs:167-170)
   {
-    const float rs = residual_and_scale(xin, xp, true, xs, p.res_out, p.eps, red4);
-    const float4* xs4 = reinterpret_cast<const float4*>(xs);
-    float acc[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    float rs[R];
+    residual_and_scale<R>(xin, xp, true, xs, p.res_out, p.eps, red4, rs);
+    float acc[R][6];
 #pragma unroll
-    for (int k = 0; k < 2; k++) {
-      const uint32_t c = lane + 64 * k;
-      float4 a = xs4[2 * c], b = xs4[2 * c + 1];
-      scale8(a, b, gp[k]);
+    for (int t = 0; t < R; t++) {
+      const float4* xs4 = reinterpret_cast<const float4*>(xs + t * H);
 #pragma unroll
-      for (int r = 0; r < 6; r++) acc[r] = dot8(wg[r][k], a, b, acc[r]);
+      for (int r = 0; r < 6; r++) acc[t][r] = 0.f;
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t c = lane + 64 * k;
+        float4 a = xs4[2 * c], b = xs4[2 * c + 1];
+        scale8(a, b, gp[k]);
+#pragma unroll
+        for (int r = 0; r < 6; r++) acc[t][r] = dot8(wg[r][k], a, b, acc[t][r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 6; r++) acc[t][r] = wave_sum(acc[t][r]) * rs[t];
     }
-#pragma unroll
-    for (int r = 0; r < 6; r++) acc[r] = wave_sum(acc[r]) * rs;
     if (lane == 0) {
 #pragma unroll
-      for (int i = 0; i < 3; i++) {
-        const float gt = acc[2 * i];
-        p.h[(row0 >> 1) + i] = pair(gt / (1.0f + expf(-gt)) * acc[2 * i + 1], tag);
+      for (int t = 0; t < R; t++) {
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+          const float gt = acc[t][2 * i];
+          p.h[t * I + (row0 >> 1) + i] = pair(gt / (1.0f + expf(-gt)) * acc[t][2 * i + 1], tag);
+        }
       }
     }
   }
@@ -834,41 +949,58 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   // down over this XCD's 384 columns (cpu_inference.rs:171-172): the partial of rows 32 s ..
   // Wave 0 alone polls the XCD's 384 h pairs (lane l: pairs 6 l .. 6 l + 5) and leaves the values
   // in LDS: a poll round is 3 KB of L2 reads per workgroup instead of every thread's 24 pairs.
-  const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, (I / NX) * 8);
+  const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, ((R - 1) * I + I / NX) * 8);
   if (wave == 0) {
-    uint4 hv[3];
+    uint4 hv[R][3];
     for (uint32_t spins = 0;;) {
-#pragma unroll
-      for (int k = 0; k < 3; k++) hv[k] = ld_pair2(rh, 6 * lane + 2 * k);
       bool ok = true;
 #pragma unroll
-      for (int k = 0; k < 3; k++) ok = ok && hv[k].y == tag && hv[k].w == tag;
+      for (int t = 0; t < R; t++) {
+#pragma unroll
+        for (int k = 0; k < 3; k++) hv[t][k] = ld_pair2(rh, t * I + 6 * lane + 2 * k);
+#pragma unroll
+        for (int k = 0; k < 3; k++) ok = ok && hv[t][k].y == tag && hv[t][k].w == tag;
+      }
       if (poll_done(ok, spins, p.err)) break;
     }
 #pragma unroll
-    for (int k = 0; k < 3; k++) {
-      hs[6 * lane + 2 * k] = __uint_as_float(hv[k].x);
-      hs[6 * lane + 2 * k + 1] = __uint_as_float(hv[k].z);
+    for (int t = 0; t < R; t++) {
+#pragma unroll
+      for (int k = 0; k < 3; k++) {
+        hs[t][6 * lane + 2 * k] = __uint_as_float(hv[t][k].x);
+        hs[t][6 * lane + 2 * k + 1] = __uint_as_float(hv[t][k].z);
+      }
     }
   }
   __syncthreads();
-  const float4* hs4 = reinterpret_cast<const float4*>(hs);
-  float da[2] = {0.f, 0.f};
+  float da[R][2];
 #pragma unroll
-  for (int k = 0; k < 3; k++) {  // chunk c = t16 + 16 k: h values 8 c .. 8 c + 7
-    const uint32_t c = t16 + 16 * k;
-    const float4 ha = hs4[2 * c], hb = hs4[2 * c + 1];
+  for (int t = 0; t < R; t++) {
+    const float4* hs4 = reinterpret_cast<const float4*>(hs[t]);
+    da[t][0] = 0.f;
+    da[t][1] = 0.f;
 #pragma unroll
-    for (int r = 0; r < 2; r++) da[r] = dot8(wd[r][k], ha, hb, da[r]);
+    for (int k = 0; k < 3; k++) {  // chunk c = t16 + 16 k: h values 8 c .. 8 c + 7
+      const uint32_t c = t16 + 16 * k;
+      const float4 ha = hs4[2 * c], hb = hs4[2 * c + 1];
+#pragma unroll
+      for (int r = 0; r < 2; r++) da[t][r] = dot8(wd[r][k], ha, hb, da[t][r]);
+    }
   }
   // keeps the prefetch loads: they were issued after down's weights, which are in by now (a wait
   // for them after this wave's next store would also wait for that store)
   asm volatile("" ::"v"(pfw[0] ^ pfw[1]));
 #pragma unroll
-  for (int r = 0; r < 2; r++) da[r] = sum16(da[r]);
+  for (int t = 0; t < R; t++) {
+#pragma unroll
+    for (int r = 0; r < 2; r++) da[t][r] = sum16(da[t][r]);
+  }
   if (t16 == 0) {
 #pragma unroll
-    for (int r = 0; r < 2; r++) p.part_out[x * H + 32 * s + 2 * rg + r] = da[r];
+    for (int t = 0; t < R; t++) {
+#pragma unroll
+      for (int r = 0; r < 2; r++) p.part_out[(t * NX + x) * H + 32 * s + 2 * rg + r] = da[t][r];
+    }
   }
   // every workgroup of the XCD has published its h values with this tag (the down rows need all
   // of them), so all of them have read the generation word
@@ -877,10 +1009,13 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   finish(kw, p.ts, t_start);
 }
 
-// x = res + part[0] + ... + part[7]
+// x = res + part[0] + ... + part[7], workgroup r for token row r
 __global__ __launch_bounds__(256) void k_fused_reduce(const float* __restrict__ res, const float* __restrict__ part,
                                                       float* __restrict__ out) {
-  const uint32_t tid = threadIdx.x;
+  const uint32_t tid = threadIdx.x, r = blockIdx.x;
+  res += r * H;
+  part += r * NX * H;
+  out += r * H;
   float4 v = reinterpret_cast<const float4*>(res)[tid];
   float4 xp[NX];
 #pragma unroll
@@ -895,26 +1030,30 @@ __global__ __launch_bounds__(256) void k_place_check(uint32_t* ids) {
   if (threadIdx.x == 0) ids[blockIdx.x] = xcc_id();
 }
 
-template <bool FIRST, bool KV_BF16>
+template <bool FIRST, bool KV_BF16, int SM, bool MULTI, int NT, int R>
+void launch_attn_v(const FusedLayerParams& p, hipStream_t s) {
+  hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, SM, MULTI, NT, R>), dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s,
+                     p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in, p.splits, p.run, p);
+}
+
+template <bool FIRST, bool KV_BF16, int R>
 hipError_t launch_attn_sm(const FusedLayerParams& p, hipStream_t s) {
-  const dim3 grid(NX * (NS + p.pf_wgs)), block(256);
   if (p.run == 32) {  // runs of one 32-position tile
-    if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-    else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-    else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 32>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-  } else if (p.splits <= 4) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 4, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-  else if (p.splits <= 8) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 8, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-  else if (p.splits <= 16) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 16, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-  else if (p.run == 64) hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, false, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
-  else hipLaunchKernelGGL((k_fused_attn<FIRST, KV_BF16, 32, true, 64>), grid, block, 0, s, p.sync, p.state, p.res_in, p.part_in, p.w_qkv, p.w_in,
-                                     p.splits, p.run, p);
+    if (p.splits <= 4) launch_attn_v<FIRST, KV_BF16, 4, false, 32, R>(p, s);
+    else if (p.splits <= 8) launch_attn_v<FIRST, KV_BF16, 8, false, 32, R>(p, s);
+    else launch_attn_v<FIRST, KV_BF16, 16, false, 32, R>(p, s);
+  } else if (p.splits <= 4) {
+    launch_attn_v<FIRST, KV_BF16, 4, false, 64, R>(p, s);
+  } else if (p.splits <= 8) {
+    launch_attn_v<FIRST, KV_BF16, 8, false, 64, R>(p, s);
+  } else if (p.splits <= 16) {
+    launch_attn_v<FIRST, KV_BF16, 16, false, 64, R>(p, s);
+  } else if constexpr (R == 1) {
+    if (p.run == 64) launch_attn_v<FIRST, KV_BF16, 32, false, 64, 1>(p, s);
+    else launch_attn_v<FIRST, KV_BF16, 32, true, 64, 1>(p, s);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
@@ -934,21 +1073,33 @@ hipError_t QE_FUSED_LAUNCHER(launch_fused_attn)(const FusedLayerParams& p, bool 
       (p.splits > 16 && (p.run == 0 || p.run % 64)))
     return hipErrorInvalidValue;
   if (first_layer ? (!p.embed || !p.tokens || p.vocab == 0) : (!p.res_in || !p.part_in)) return hipErrorInvalidValue;
-  if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true>(p, s) : launch_attn_sm<true, false>(p, s);
-  return p.kv_bf16 ? launch_attn_sm<false, true>(p, s) : launch_attn_sm<false, false>(p, s);
+  if (p.rows == 2) {  // verify rows: single-tile runs only
+    if (p.splits > 16) return hipErrorInvalidValue;
+    if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true, 2>(p, s) : launch_attn_sm<true, false, 2>(p, s);
+    return p.kv_bf16 ? launch_attn_sm<false, true, 2>(p, s) : launch_attn_sm<false, false, 2>(p, s);
+  }
+  if (p.rows != 1) return hipErrorInvalidValue;
+  if (first_layer) return p.kv_bf16 ? launch_attn_sm<true, true, 1>(p, s) : launch_attn_sm<true, false, 1>(p, s);
+  return p.kv_bf16 ? launch_attn_sm<false, true, 1>(p, s) : launch_attn_sm<false, false, 1>(p, s);
 }
 
 hipError_t QE_FUSED_LAUNCHER(launch_fused_mlp)(const FusedLayerParams& p, hipStream_t s) {
   if (!common_ok(p) || !p.res_in || !p.part_in || !p.w_post || !p.w_gu || !p.w_down || !p.h) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_fused_mlp, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
-                     p.w_post, p.w_down, p.qkv_next, p);
+  if (p.rows == 1)
+    hipLaunchKernelGGL(k_fused_mlp<1>, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
+                       p.w_post, p.w_down, p.qkv_next, p);
+  else if (p.rows == 2)
+    hipLaunchKernelGGL(k_fused_mlp<2>, dim3(NX * (NS + p.pf_wgs)), dim3(256), 0, s, p.sync, p.res_in, p.part_in, p.w_gu,
+                       p.w_post, p.w_down, p.qkv_next, p);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 #ifndef QE_FUSED_TIMED
-hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s) {
-  if (!res || !part || !x) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_fused_reduce, dim3(1), dim3(256), 0, s, res, part, x);
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, hipStream_t s) {
+  if (!res || !part || !x || rows == 0 || rows > kFusedMaxRows) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_fused_reduce, dim3(rows), dim3(256), 0, s, res, part, x);
   return hipGetLastError();
 }
 

@@ -142,7 +142,8 @@ hipError_t launch_attention_rows(const AttnParams& p, uint32_t splits, float* ou
 hipError_t launch_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, StepState* st,
                          uint32_t* tokens, uint32_t* host_tokens, uint32_t* err, const float* rope,
                          float* rope_cur, uint32_t half, hipStream_t s);
-hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, hipStream_t s);
+// nt: the non-temporal form, one contiguous range of the buffer per workgroup
+hipError_t launch_read_sum(const float* src, uint64_t n, float* partial, uint32_t grid, bool nt, hipStream_t s);
 
 // ---- fused decode layer (fused.hip): two launches per layer for the Qwen3-0.6B shape ----
 // One KV head per XCD: the 256 workgroups of a launch are 8 XCDs x 32 slots (workgroup i runs
@@ -164,6 +165,10 @@ constexpr size_t kFusedQkvPairs = size_t(kFusedHeads + 2 * kFusedKv) * kHeadDim;
 constexpr size_t kFusedAttPairs = size_t(kFusedHeads) * kHeadDim;
 constexpr size_t kFusedPartPairs = size_t(kFusedKv) * kFusedMaxRuns * (kFusedHeads / kFusedKv) * kPartStride;
 constexpr size_t kFusedHPairs = kFusedI;
+// token rows of a fused launch: 1 (decode step) or 2 (verify pass); every exchange buffer, the
+// residual and the partials hold kFusedMaxRows rows, row r at r times the one-row size
+constexpr uint32_t kFusedMaxRows = 2;
+constexpr size_t kFusedQkvRowPairs = kFusedQkvPairs + kFusedAttPairs;
 
 // A region of weights that extra workgroups of a launch load into the L2 of each XCD for a later
 // launch: on XCD x the rows [0, rows) of row_bytes bytes at base + x * xcd_bytes + r * stride.
@@ -222,6 +227,9 @@ struct FusedLayerParams {
   // clock stamps, read by the *_timed launchers only (null: none): layer workgroup b stores the
   // 100 MHz real-time clock at its start to ts[2 b] and at its exit to ts[2 b + 1]
   uint64_t* ts;
+  // token rows (1 or kFusedMaxRows) at positions state->pos .. + rows - 1: tokens[state->tok_idx + r]
+  // in layer 0, RoPE row r at rope_cur + r D (rows > 1: up to 16 single-tile runs)
+  uint32_t rows;
 };
 
 // layer l's attention block: [embedding | residual + partials] -> RMSNorm -> q|k|v ->
@@ -234,7 +242,7 @@ hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
 hipError_t launch_fused_attn_timed(const FusedLayerParams& p, bool first_layer, hipStream_t s);
 hipError_t launch_fused_mlp_timed(const FusedLayerParams& p, hipStream_t s);
 // x = res + sum of the 8 partials (the last layer's output, before the final norm)
-hipError_t launch_fused_reduce(const float* res, const float* part, float* x, hipStream_t s);
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, hipStream_t s);
 // ---- the decode step's layers in one persistent launch (persist.hip), same shape ----
 struct PersistParams {
   // layer 0's tensors; layer l's are layer_stride bytes further on

@@ -296,6 +296,7 @@ int main(int argc, char** argv) {
     CK(hipMemsetAsync(fsync, 0, qe::kFusedSyncWords * 4, s));
     CK(hipStreamSynchronize(s));
     qe::FusedLayerParams f{};
+    f.rows = 1;
     f.w_in = gains; f.q_norm = gains; f.k_norm = gains; f.w_post = gains;
     f.qkv = fqkv; f.attn_part = fpart; f.h = fh;
     f.tokens = tokens; f.vocab = V; f.state = st;
@@ -333,7 +334,7 @@ int main(int argc, char** argv) {
       CK(hipStreamSynchronize(s));
     }
     for (int it = 0; it < 2; it++) {
-      CK(qe::launch_fused_reduce(res0, part_mlp, x, s));
+      CK(qe::launch_fused_reduce(res0, part_mlp, x, 1, s));
       qe::MatvecParams p{};
       p.eps = 1e-6f; p.w = LM; p.x = x; p.nw = gains; p.rows = V; p.cols = H; p.out = logits; p.cand = cand;
       CK(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));

@@ -212,6 +212,7 @@ def lib() -> ctypes.CDLL:
         "qe_op_attention_work_bytes": (u64, [u64, u64, u64]),
         "qe_op_attention": (i32, [vp, vp, vp, vp, u64, u64, u64, u64, u32, vp, vp]),
         "qe_op_read_sum": (i32, [vp, u64, vp, u32, vp]),
+        "qe_op_read_sum_nt": (i32, [vp, u64, vp, u32, vp]),
         "qe_op_argmax": (i32, [vp, u64, u64, vp, vp]),
     }
     for name, (res, args) in sig.items():
@@ -482,3 +483,7 @@ def op_argmax(logits, tokens, stream=None) -> None:
 
 def op_read_sum(src, partial, grid: int = 0, stream=None) -> None:
     _check(lib().qe_op_read_sum(_ptr(src), src.numel(), _ptr(partial), grid, _stream_ptr(stream)))
+
+
+def op_read_sum_nt(src, partial, grid: int = 0, stream=None) -> None:
+    _check(lib().qe_op_read_sum_nt(_ptr(src), src.numel(), _ptr(partial), grid, _stream_ptr(stream)))

@@ -144,4 +144,5 @@ extern "C" {
                                   stream: *mut c_void) -> c_int;
     pub fn qe_op_argmax(logits: *const f32, rows: u64, n: u64, tokens_out: *mut u32, stream: *mut c_void) -> c_int;
     pub fn qe_op_read_sum(src: *const f32, n: u64, partial: *mut f32, grid: u32, stream: *mut c_void) -> c_int;
+    pub fn qe_op_read_sum_nt(src: *const f32, n: u64, partial: *mut f32, grid: u32, stream: *mut c_void) -> c_int;
 }

@@ -133,3 +133,15 @@ def test_read_sum(gpu):
     qe.op_read_sum(src, part, 2048)
     torch.cuda.synchronize()
     assert float(part.double().sum()) == float(n)
+
+
+@pytest.mark.parametrize("n,grid", [(1 << 24, 2048), ((1 << 20) + 12, 777), (4, 3)])
+def test_read_sum_nt(gpu, n, grid):
+    # every float read exactly once over ranges that do not split evenly (workgroups with 0 or 1
+    # float4s included); the values keep each partial sum exact in f32
+    import torch
+    src = (torch.arange(n, device="cuda") % 7).float()
+    part = torch.full((grid,), float("nan"), device="cuda")
+    qe.op_read_sum_nt(src, part, grid)
+    torch.cuda.synchronize()
+    assert float(part.double().sum()) == float(src.double().sum())
