@@ -188,6 +188,8 @@ struct qe_model {
   bool lm_head_rows = true;
   // two-row verify passes through the two launches per layer (QE_VERIFY_FUSED=0: the batch path)
   bool verify_fused = true;
+  // the decode step's final reduce applies the final norm (QE_LM_PRENORM=0: the lm_head does)
+  bool lm_prenorm = true;
   // qe_decode_lookup decodes plain blocks while its verify passes emit tokens more slowly than
   // plain steps (QE_LOOKUP_ADAPTIVE=0: always drafts)
   bool lookup_adaptive = true;
@@ -339,6 +341,7 @@ int qe_model_load(const char* path, qe_model** out) {
   if (const char* mm = getenv("QE_MV_MERGE")) m->mv_merge = strcmp(mm, "0") != 0;
   if (const char* lh = getenv("QE_LM_HEAD_ROWS")) m->lm_head_rows = strcmp(lh, "0") != 0;
   if (const char* vf = getenv("QE_VERIFY_FUSED")) m->verify_fused = strcmp(vf, "0") != 0;
+  if (const char* pn = getenv("QE_LM_PRENORM")) m->lm_prenorm = strcmp(pn, "0") != 0;
   if (const char* la = getenv("QE_LOOKUP_ADAPTIVE")) m->lookup_adaptive = strcmp(la, "0") != 0;
   if (const char* ps = getenv("QE_PREFILL_STREAMS"))
     m->prefill_streams = std::min(std::max(atoi(ps), 1), kMaxPrefillStreams);
@@ -780,13 +783,17 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       HIP_TRY(f.ts ? qe::launch_fused_mlp_timed(f, s) : qe::launch_fused_mlp(f, s));
     }
   }
-  if (want("final_reduce")) HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, rows, s));
+  // one row: the reduce also applies the final norm, and the lm_head copies x as it is
+  const bool prenorm = rows == 1 && m->lm_prenorm;
+  if (want("final_reduce"))
+    HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, rows, prenorm ? m->final_norm : nullptr,
+                                    c.rms_norm_eps, s));
   if (rows > 1) return QE_OK;
   MatvecParams p{};
   p.eps = c.rms_norm_eps;
   p.w = m->lm_head; p.x = m->x; p.nw = m->final_norm; p.rows = V; p.cols = uint32_t(c.hidden_size);
   p.out = m->logits; p.cand = m->cand;
-  if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
+  if (want("lm_head")) HIP_TRY(qe::launch_matvec(p, prenorm ? qe::kCopy : qe::kNorm, qe::kLogits, s));
   if (want("argmax")) {
     HIP_TRY(qe::launch_argmax(m->cand, m->n_cand, m->logits, kv->state, kv->tokens, kv->host_tokens, m->err,
                               kv->rope, kv->rope_cur, D / 2, s));

@@ -1009,9 +1009,13 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   finish(kw, p.ts, t_start);
 }
 
-// x = res + part[0] + ... + part[7], workgroup r for token row r
+// x = res + part[0] + ... + part[7], workgroup r for token row r. With a gain (one row: the decode
+// step), out = the final RMSNorm of x instead, (x s) gain with s = 1 / sqrt(mean(x^2) + eps), the
+// lm_head's prologue summed in its order (cpu_inference.rs:175-176), so that no lm_head workgroup
+// repeats it.
 __global__ __launch_bounds__(256) void k_fused_reduce(const float* __restrict__ res, const float* __restrict__ part,
-                                                      float* __restrict__ out) {
+                                                      float* __restrict__ out, const uint16_t* __restrict__ gain,
+                                                      float eps) {
   const uint32_t tid = threadIdx.x, r = blockIdx.x;
   res += r * H;
   part += r * NX * H;
@@ -1022,6 +1026,19 @@ __global__ __launch_bounds__(256) void k_fused_reduce(const float* __restrict__ 
   for (uint32_t g = 0; g < NX; g++) xp[g] = reinterpret_cast<const float4*>(part + g * H)[tid];
 #pragma unroll
   for (uint32_t g = 0; g < NX; g++) v = add4(v, xp[g]);
+  if (gain) {
+    __shared__ float red[4];
+    const float ss = wave_sum(v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    const float tot = (red[0] + red[1]) + (red[2] + red[3]);
+    const float sc = 1.0f / sqrtf(tot / float(H) + eps);
+    const uint2 gw = reinterpret_cast<const uint2*>(gain)[tid];
+    v.x = v.x * sc * __uint_as_float(gw.x << 16);
+    v.y = v.y * sc * __uint_as_float(gw.x & 0xFFFF0000u);
+    v.z = v.z * sc * __uint_as_float(gw.y << 16);
+    v.w = v.w * sc * __uint_as_float(gw.y & 0xFFFF0000u);
+  }
   reinterpret_cast<float4*>(out)[tid] = v;
 }
 
@@ -1097,9 +1114,10 @@ hipError_t QE_FUSED_LAUNCHER(launch_fused_mlp)(const FusedLayerParams& p, hipStr
 }
 
 #ifndef QE_FUSED_TIMED
-hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, hipStream_t s) {
-  if (!res || !part || !x || rows == 0 || rows > kFusedMaxRows) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_fused_reduce, dim3(rows), dim3(256), 0, s, res, part, x);
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, const uint16_t* gain,
+                               float eps, hipStream_t s) {
+  if (!res || !part || !x || rows == 0 || rows > kFusedMaxRows || (gain && rows != 1)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_fused_reduce, dim3(rows), dim3(256), 0, s, res, part, x, gain, eps);
   return hipGetLastError();
 }
 

@@ -242,7 +242,9 @@ hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
 hipError_t launch_fused_attn_timed(const FusedLayerParams& p, bool first_layer, hipStream_t s);
 hipError_t launch_fused_mlp_timed(const FusedLayerParams& p, hipStream_t s);
 // x = res + sum of the 8 partials (the last layer's output, before the final norm)
-hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, hipStream_t s);
+// gain (rows = 1 only): x = the final RMSNorm of the sum, with that gain and eps
+hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, const uint16_t* gain,
+                               float eps, hipStream_t s);
 // ---- the decode step's layers in one persistent launch (persist.hip), same shape ----
 struct PersistParams {
   // layer 0's tensors; layer l's are layer_stride bytes further on

@@ -563,6 +563,7 @@ hipError_t launch_matvec(const MatvecParams& p, int prologue, int epilogue, hipS
   if (prologue == kNorm && epilogue == kStore) return launch_mv_cpl<kNorm, kStore>(p, s);
   if (prologue == kNorm && epilogue == kSiluPair) return launch_mv_cpl<kNorm, kSiluPair>(p, s);
   if (prologue == kNorm && epilogue == kLogits) return launch_mv_cpl<kNorm, kLogits>(p, s);
+  if (prologue == kCopy && epilogue == kLogits) return launch_mv_cpl<kCopy, kLogits>(p, s);
   return hipErrorInvalidValue;
 }
 

@@ -334,7 +334,7 @@ int main(int argc, char** argv) {
       CK(hipStreamSynchronize(s));
     }
     for (int it = 0; it < 2; it++) {
-      CK(qe::launch_fused_reduce(res0, part_mlp, x, 1, s));
+      CK(qe::launch_fused_reduce(res0, part_mlp, x, 1, nullptr, 0.f, s));
       qe::MatvecParams p{};
       p.eps = 1e-6f; p.w = LM; p.x = x; p.nw = gains; p.rows = V; p.cols = H; p.out = logits; p.cand = cand;
       CK(qe::launch_matvec(p, qe::kNorm, qe::kLogits, s));
