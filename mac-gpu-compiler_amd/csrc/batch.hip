@@ -1467,6 +1467,8 @@ __global__ __launch_bounds__(256) void k_lm_head_rows(MvRowsParams p) {
   const float4* x4 = reinterpret_cast<const float4*>(p.x);
   float4* xs4 = reinterpret_cast<float4*>(xs);
   const uint32_t c4 = p.cols / 4;
+  // no gain: the rows come normalized (the fused verify pass's final reduce applied the norm)
+  const bool norm = p.gain != nullptr;
 #pragma unroll
   for (int v = 0; v < NV; v++) {
     float ss = 0.f;
@@ -1475,17 +1477,21 @@ __global__ __launch_bounds__(256) void k_lm_head_rows(MvRowsParams p) {
       xs4[v * c4 + i] = a;
       ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
     }
-    ss = wave_sum(ss);
-    if (lane == 0) red[v][wave] = ss;
+    if (norm) {
+      ss = wave_sum(ss);
+      if (lane == 0) red[v][wave] = ss;
+    }
   }
   __syncthreads();
+  if (norm) {
 #pragma unroll
-  for (int v = 0; v < NV; v++) {
-    const float tot = (red[v][0] + red[v][1]) + (red[v][2] + red[v][3]);
-    const float sc = 1.0f / sqrtf(tot / float(p.cols) + p.eps);
-    for (uint32_t i = tid; i < p.cols; i += 256) xs[v * p.cols + i] = xs[v * p.cols + i] * sc * bf16f(p.gain[i]);
+    for (int v = 0; v < NV; v++) {
+      const float tot = (red[v][0] + red[v][1]) + (red[v][2] + red[v][3]);
+      const float sc = 1.0f / sqrtf(tot / float(p.cols) + p.eps);
+      for (uint32_t i = tid; i < p.cols; i += 256) xs[v * p.cols + i] = xs[v * p.cols + i] * sc * bf16f(p.gain[i]);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   float acc[NV][R];
 #pragma unroll
   for (int v = 0; v < NV; v++)
@@ -1600,7 +1606,7 @@ hipError_t launch_mv_rows_merge(const MvRowsParams& p, hipStream_t st) {
 }
 
 hipError_t launch_lm_head_rows(const MvRowsParams& p, hipStream_t st) {
-  if (!p.w || !p.x || !p.gain || !p.out || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||
+  if (!p.w || !p.x || !p.out || p.M == 0 || p.M > kMvRowsMaxM || p.rows == 0 || p.cols == 0 ||
       p.cols % 8 || p.ldo < p.rows)
     return hipErrorInvalidValue;
   if (p.cols / 8 > 128) return hipErrorNotSupported;  // the decode lm_head's shape: 2 chunks per lane

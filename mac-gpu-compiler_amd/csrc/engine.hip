@@ -133,11 +133,10 @@ struct qe_model {
   uint64_t layer_stride = 0;  // bytes between consecutive layers' tensors in the arena
   uint2 *fqkv = nullptr, *fh = nullptr;  // (value, tag) pairs exchanged inside an XCD
   uint32_t* fsync = nullptr;
-  // a two-row verify pass through the two launches per layer: its step state {pos, 0, ..}, its
-  // two token ids and the RoPE rows of its two positions (res0 .. fh hold kFusedMaxRows rows)
+  // a two-row verify pass through the two launches per layer: its step state {pos, 0, ..} and its
+  // two token ids (res0 .. fh hold kFusedMaxRows rows)
   StepState* vstate = nullptr;
   uint32_t* vtokens = nullptr;
-  float* vrope = nullptr;
   uint32_t* place_word = nullptr;
   // extra workgroups per XCD of each attention block that load the layer's MLP weights into the
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
@@ -475,7 +474,7 @@ int qe_model_load(const char* path, qe_model** out) {
                s_pa = stake(FR * qe::kFusedXcds * H * 4), s_pm = stake(FR * qe::kFusedXcds * H * 4),
                s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4),
                s_fqkv = stake(FR * qe::kFusedQkvRowPairs * 8), s_fh = stake(FR * qe::kFusedHPairs * 8),
-               s_vstate = stake(sizeof(StepState) + FR * 4), s_vrope = stake(FR * D * 4),
+               s_vstate = stake(sizeof(StepState) + FR * 4),
                s_pxa = stake(qe::kFusedXcds * H * 8), s_pxm = stake(qe::kFusedXcds * H * 8),
                s_ppa = stake(qe::kFusedXcds * H * 8), s_ppm = stake(qe::kFusedXcds * H * 8), s_pgen = stake(256);
   static_assert(qe::kFusedPartPairs * 8 <= size_t(qe::kFusedKv) * qe::kAttnMaxWideSplits * 2 * qe::kPartStride * 4,
@@ -500,7 +499,6 @@ int qe_model_load(const char* path, qe_model** out) {
   m->fh = reinterpret_cast<uint2*>(m->scratch + s_fh);
   m->vstate = reinterpret_cast<StepState*>(m->scratch + s_vstate);
   m->vtokens = reinterpret_cast<uint32_t*>(m->scratch + s_vstate + sizeof(StepState));
-  m->vrope = reinterpret_cast<float*>(m->scratch + s_vrope);
   m->pxa = reinterpret_cast<uint2*>(m->scratch + s_pxa);
   m->pxm = reinterpret_cast<uint2*>(m->scratch + s_pxm);
   m->ppa = reinterpret_cast<uint2*>(m->scratch + s_ppa);
@@ -682,7 +680,7 @@ int enqueue_step(qe_model* m, qe_kv* kv, const char* only = nullptr, uint32_t* l
 // MLP block; the final reduction of the last layer's partials, the lm_head and the argmax.
 // `only` / `launches` as in enqueue_step, with the stages attn_block, mlp_block, final_reduce,
 // lm_head and argmax.
-// rows = 2: the layers of a two-row verify pass (m->vstate, m->vtokens, m->vrope), ending with the
+// rows = 2: the layers of a two-row verify pass (m->vstate, m->vtokens; RoPE rows from the table), ending with the
 // final residual rows in m->x; the caller runs the lm_head and the argmax over both rows.
 int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launches, uint32_t rows) {
   const qe_config& c = m->cfg;
@@ -711,7 +709,7 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
   f.kv_bf16 = kv->dtype == QE_KV_BF16; f.max_seq = uint32_t(kv->max_seq); f.rope_cur = kv->rope_cur;
   f.splits = kv->step_splits; f.run = kv->step_run;
   if (rows > 1) {
-    f.state = m->vstate; f.tokens = m->vtokens; f.rope_cur = m->vrope;
+    f.state = m->vstate; f.tokens = m->vtokens; f.rope_cur = kv->rope;
   }
   f.eps = c.rms_norm_eps; f.scale = 1.0f / sqrtf(float(D));
   f.sync = m->fsync; f.err = m->err;
@@ -783,8 +781,9 @@ int enqueue_step_fused(qe_model* m, qe_kv* kv, const char* only, uint32_t* launc
       HIP_TRY(f.ts ? qe::launch_fused_mlp_timed(f, s) : qe::launch_fused_mlp(f, s));
     }
   }
-  // one row: the reduce also applies the final norm, and the lm_head copies x as it is
-  const bool prenorm = rows == 1 && m->lm_prenorm;
+  // the reduce also applies the final norm, and the lm_head copies x as it is (a verify pass's
+  // lm_head over its rows always)
+  const bool prenorm = rows > 1 || m->lm_prenorm;
   if (want("final_reduce"))
     HIP_TRY(qe::launch_fused_reduce(m->res0, m->part_mlp, m->x, rows, prenorm ? m->final_norm : nullptr,
                                     c.rms_norm_eps, s));
@@ -1653,13 +1652,12 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
   step_shape(kv, pos + R - 1, splits, run);  // the runs cover positions 0 .. pos + R - 1
   if (R != qe::kFusedMaxRows || splits > 16) return kNotFused;
   const qe_config& c = m->cfg;
-  const size_t D = c.head_dim, V = c.vocab_size;
+  const size_t V = c.vocab_size;
   HIP_TRY(hipStreamSynchronize(m->stream));  // the staging words are free
   const StepState st{uint32_t(pos), 0u, uint32_t(kv->max_seq), R};
   memcpy(m->h_small + 16, &st, sizeof(st));
   std::copy(ids, ids + R, m->h_small + 20);
   HIP_TRY(hipMemcpyAsync(m->vstate, m->h_small + 16, sizeof(st) + R * 4, hipMemcpyHostToDevice, m->stream));
-  HIP_TRY(hipMemcpyAsync(m->vrope, kv->rope + pos * D, R * D * 4, hipMemcpyDeviceToDevice, m->stream));
   // the pass: the layers, the lm_head over both rows, each row's argmax into pinned memory
   uint32_t* host_tok = reinterpret_cast<uint32_t*>(m->h_logits);
   auto enqueue = [&]() -> int {
@@ -1670,7 +1668,8 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
     kv->step_splits = ks;
     kv->step_run = kr;
     if (rc) return rc;
-    const qe::MvRowsParams r{m->lm_head, m->x, m->final_norm, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
+    // (x comes normalized from the final reduce)
+    const qe::MvRowsParams r{m->lm_head, m->x, nullptr, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
                              uint32_t(V), c.rms_norm_eps};
     HIP_TRY(qe::launch_lm_head_rows(r, m->stream));
     HIP_TRY(qe::launch_row_argmax(m->blogits, R, uint32_t(V), host_tok, m->bcand, m->stream));

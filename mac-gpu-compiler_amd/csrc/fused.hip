@@ -355,10 +355,10 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
   __builtin_amdgcn_sched_barrier(0);
   const uint16_t gq[2] = {p.q_norm[lane], p.q_norm[lane + 64]};
   const uint16_t gk[2] = {p.k_norm[lane], p.k_norm[lane + 64]};
-  // RoPE rows of positions pos .. pos + R - 1 (consecutive rows of D floats)
+  // RoPE row of the step's position (one row: rope_cur, no wait for pos); a verify pass's rows
+  // read theirs from the table at pos + r once the attention starts (pos is in by then)
   float2 cs[R];
-#pragma unroll
-  for (int r = 0; r < R; r++) cs[r] = reinterpret_cast<const float2*>(p.rope_cur + r * D)[lane];
+  if constexpr (R == 1) cs[0] = reinterpret_cast<const float2*>(p.rope_cur)[lane];
   if constexpr (NT != 32) load_first_tile();
   // o_proj rows orow0 + ORR rg + r over columns [256 x, 256 x + 256): 16 threads per row, chunks
   // t16 and t16 + 16 of the slice
@@ -442,6 +442,11 @@ __global__ __launch_bounds__(256) void k_fused_attn(uint32_t* sync, const StepSt
     // holds dims l, l + 64
     const __amdgpu_buffer_rsrc_t rq = rsrc_of(p.qkv, uint32_t(R * kQkvRowPairs * 8));
     const uint32_t off = wave < G ? (x * G + wave) * D : wave == G ? QD + x * D : QD + KD + x * D;
+    if constexpr (R > 1) {
+#pragma unroll
+      for (int r = 0; r < R; r++)
+        cs[r] = reinterpret_cast<const float2*>(p.rope_cur + size_t(min(pos_step + r, p.max_seq - 1)) * D)[lane];
+    }
     uint2 qa[R], qb[R];
     for (uint32_t spins = 0;;) {
       bool ok = true;
@@ -950,26 +955,21 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   // Wave 0 alone polls the XCD's 384 h pairs (lane l: pairs 6 l .. 6 l + 5) and leaves the values
   // in LDS: a poll round is 3 KB of L2 reads per workgroup instead of every thread's 24 pairs.
   const __amdgpu_buffer_rsrc_t rh = rsrc_of(p.h + (I / NX) * x, ((R - 1) * I + I / NX) * 8);
-  if (wave == 0) {
-    uint4 hv[R][3];
+  if (wave < uint32_t(R)) {  // wave t: token row t
+    const uint32_t t = wave;
+    uint4 hv[3];
     for (uint32_t spins = 0;;) {
+#pragma unroll
+      for (int k = 0; k < 3; k++) hv[k] = ld_pair2(rh, t * I + 6 * lane + 2 * k);
       bool ok = true;
 #pragma unroll
-      for (int t = 0; t < R; t++) {
-#pragma unroll
-        for (int k = 0; k < 3; k++) hv[t][k] = ld_pair2(rh, t * I + 6 * lane + 2 * k);
-#pragma unroll
-        for (int k = 0; k < 3; k++) ok = ok && hv[t][k].y == tag && hv[t][k].w == tag;
-      }
+      for (int k = 0; k < 3; k++) ok = ok && hv[k].y == tag && hv[k].w == tag;
       if (poll_done(ok, spins, p.err)) break;
     }
 #pragma unroll
-    for (int t = 0; t < R; t++) {
-#pragma unroll
-      for (int k = 0; k < 3; k++) {
-        hs[t][6 * lane + 2 * k] = __uint_as_float(hv[t][k].x);
-        hs[t][6 * lane + 2 * k + 1] = __uint_as_float(hv[t][k].z);
-      }
+    for (int k = 0; k < 3; k++) {
+      hs[t][6 * lane + 2 * k] = __uint_as_float(hv[k].x);
+      hs[t][6 * lane + 2 * k + 1] = __uint_as_float(hv[k].z);
     }
   }
   __syncthreads();
@@ -1009,8 +1009,8 @@ __global__ __launch_bounds__(256) void k_fused_mlp(uint32_t* sync, const float* 
   finish(kw, p.ts, t_start);
 }
 
-// x = res + part[0] + ... + part[7], workgroup r for token row r. With a gain (one row: the decode
-// step), out = the final RMSNorm of x instead, (x s) gain with s = 1 / sqrt(mean(x^2) + eps), the
+// x = res + part[0] + ... + part[7], workgroup r for token row r. With a gain, out = the final
+// RMSNorm of x instead, (x s) gain with s = 1 / sqrt(mean(x^2) + eps), the
 // lm_head's prologue summed in its order (cpu_inference.rs:175-176), so that no lm_head workgroup
 // repeats it.
 __global__ __launch_bounds__(256) void k_fused_reduce(const float* __restrict__ res, const float* __restrict__ part,
@@ -1116,7 +1116,7 @@ hipError_t QE_FUSED_LAUNCHER(launch_fused_mlp)(const FusedLayerParams& p, hipStr
 #ifndef QE_FUSED_TIMED
 hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, const uint16_t* gain,
                                float eps, hipStream_t s) {
-  if (!res || !part || !x || rows == 0 || rows > kFusedMaxRows || (gain && rows != 1)) return hipErrorInvalidValue;
+  if (!res || !part || !x || rows == 0 || rows > kFusedMaxRows) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_fused_reduce, dim3(rows), dim3(256), 0, s, res, part, x, gain, eps);
   return hipGetLastError();
 }

@@ -228,7 +228,8 @@ struct FusedLayerParams {
   // 100 MHz real-time clock at its start to ts[2 b] and at its exit to ts[2 b + 1]
   uint64_t* ts;
   // token rows (1 or kFusedMaxRows) at positions state->pos .. + rows - 1: tokens[state->tok_idx + r]
-  // in layer 0, RoPE row r at rope_cur + r D (rows > 1: up to 16 single-tile runs)
+  // in layer 0; rows > 1 (up to 16 single-tile runs): rope_cur is the RoPE table [max_seq][D]
+  // and row r takes row pos + r
   uint32_t rows;
 };
 
@@ -242,7 +243,7 @@ hipError_t launch_fused_mlp(const FusedLayerParams& p, hipStream_t s);
 hipError_t launch_fused_attn_timed(const FusedLayerParams& p, bool first_layer, hipStream_t s);
 hipError_t launch_fused_mlp_timed(const FusedLayerParams& p, hipStream_t s);
 // x = res + sum of the 8 partials (the last layer's output, before the final norm)
-// gain (rows = 1 only): x = the final RMSNorm of the sum, with that gain and eps
+// gain: x = the final RMSNorm of each row's sum, with that gain and eps
 hipError_t launch_fused_reduce(const float* res, const float* part, float* x, uint32_t rows, const uint16_t* gain,
                                float eps, hipStream_t s);
 // ---- the decode step's layers in one persistent launch (persist.hip), same shape ----
