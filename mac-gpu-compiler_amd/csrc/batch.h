@@ -137,10 +137,11 @@ hipError_t launch_attn_causal(const BatchAttnParams& p, uint32_t runs, hipStream
 // under 512 workgroups, and at most one per 128 keys
 uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t n_kv);
 // tokens[r] = greedy token of row r of logits [rows][V] (the decode step's argmax rule);
-// cand: rows * kArgParts candidates of scratch (device memory); rows <= 65535
+// cand: rows * kArgParts candidates of scratch (device memory); rows <= 65535; err_in / err_out
+// (optional): the device error word, copied to err_out once the tokens are written
 constexpr uint32_t kArgParts = 64;
 hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, ArgCand* cand,
-                             hipStream_t st);
+                             hipStream_t st, const uint32_t* err_in = nullptr, uint32_t* err_out = nullptr);
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,
                              hipStream_t st);
 // The ids of a short pass (M <= kIdsByValue) as a kernel argument: no host-to-device copy.

@@ -1159,9 +1159,12 @@ __global__ __launch_bounds__(256) void k_row_argmax_part(const float* __restrict
   }
 }
 
+// err_in / err_out (optional): workgroup 0 also copies the error word to err_out, so a host that
+// waits for tokens (and err_out) in pinned memory learns of a failed pass without synchronizing
 __global__ __launch_bounds__(64) void k_row_argmax_final(const ArgCand* __restrict__ cand,
                                                          const float* __restrict__ logits, uint32_t V,
-                                                         uint32_t* __restrict__ tokens) {
+                                                         uint32_t* __restrict__ tokens, const uint32_t* err_in,
+                                                         uint32_t* err_out) {
   static_assert(kArgParts == 64, "one candidate per lane");
   const uint32_t row = blockIdx.x, lane = threadIdx.x;
   const ArgCand c = cand[size_t(row) * kArgParts + lane];
@@ -1174,6 +1177,7 @@ __global__ __launch_bounds__(64) void k_row_argmax_final(const ArgCand* __restri
     if (cand_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
   }
   if (lane == 0) tokens[row] = (nan0 || bi == 0xFFFFFFFFu) ? 0u : bi;
+  if (err_out && row == 0 && lane == 0) __atomic_store_n(err_out, *err_in, __ATOMIC_RELAXED);
 }
 
 // x[m] = bf16 embedding row of ids[m] (cpu_inference.rs:109-111)
@@ -1834,11 +1838,11 @@ uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t
 }
 
 hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, ArgCand* cand,
-                             hipStream_t st) {
+                             hipStream_t st, const uint32_t* err_in, uint32_t* err_out) {
   if (!rows || !V || !cand || rows > 65535) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_row_argmax_part, dim3(kArgParts, rows), dim3(256), 0, st, logits, V, ceil_div(V, kArgParts),
                      cand);
-  hipLaunchKernelGGL(k_row_argmax_final, dim3(rows), dim3(64), 0, st, cand, logits, V, tokens);
+  hipLaunchKernelGGL(k_row_argmax_final, dim3(rows), dim3(64), 0, st, cand, logits, V, tokens, err_in, err_out);
   return hipGetLastError();
 }
 

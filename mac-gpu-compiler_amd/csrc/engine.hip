@@ -137,6 +137,7 @@ struct qe_model {
   // two token ids (res0 .. fh hold kFusedMaxRows rows)
   StepState* vstate = nullptr;
   uint32_t* vtokens = nullptr;
+  hipEvent_t vstage_ev = nullptr;  // recorded after the copy of the pass's staging words
   uint32_t* place_word = nullptr;
   // extra workgroups per XCD of each attention block that load the layer's MLP weights into the
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
@@ -230,6 +231,7 @@ struct qe_model {
     }
     for (hipEvent_t e : kv_ev0) (void)hipEventDestroy(e);
     if (start_ev) (void)hipEventDestroy(start_ev);
+    if (vstage_ev) (void)hipEventDestroy(vstage_ev);
     if (ids_dev) (void)hipFree(ids_dev);
     if (h_logits) (void)hipHostFree(h_logits);
     if (h_small) (void)hipHostFree(h_small);
@@ -1641,6 +1643,7 @@ int check_verify_args(qe_model* model, const uint32_t* ids, uint64_t k, uint64_t
 }
 
 constexpr int kNotFused = -1;
+constexpr uint32_t kTokPending = 0xFFFFFFFFu;  // a pinned token slot not yet written
 
 // A two-row verify pass (positions pos, pos + 1) through the two launches per layer, every weight
 // read once for both rows; the lm_head over both rows and the device argmax of each row follow.
@@ -1653,11 +1656,14 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
   if (R != qe::kFusedMaxRows || splits > 16) return kNotFused;
   const qe_config& c = m->cfg;
   const size_t V = c.vocab_size;
-  HIP_TRY(hipStreamSynchronize(m->stream));  // the staging words are free
+  // the staging words are free once the previous pass's copy of them is done
+  if (!m->vstage_ev) HIP_TRY(hipEventCreateWithFlags(&m->vstage_ev, hipEventDisableTiming));
+  else HIP_TRY(hipEventSynchronize(m->vstage_ev));
   const StepState st{uint32_t(pos), 0u, uint32_t(kv->max_seq), R};
   memcpy(m->h_small + 16, &st, sizeof(st));
   std::copy(ids, ids + R, m->h_small + 20);
   HIP_TRY(hipMemcpyAsync(m->vstate, m->h_small + 16, sizeof(st) + R * 4, hipMemcpyHostToDevice, m->stream));
+  HIP_TRY(hipEventRecord(m->vstage_ev, m->stream));
   // the pass: the layers, the lm_head over both rows, each row's argmax into pinned memory
   uint32_t* host_tok = reinterpret_cast<uint32_t*>(m->h_logits);
   auto enqueue = [&]() -> int {
@@ -1672,9 +1678,12 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
     const qe::MvRowsParams r{m->lm_head, m->x, nullptr, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
                              uint32_t(V), c.rms_norm_eps};
     HIP_TRY(qe::launch_lm_head_rows(r, m->stream));
-    HIP_TRY(qe::launch_row_argmax(m->blogits, R, uint32_t(V), host_tok, m->bcand, m->stream));
+    HIP_TRY(qe::launch_row_argmax(m->blogits, R, uint32_t(V), host_tok, m->bcand, m->stream, m->err, host_tok + R));
     return QE_OK;
   };
+  // the host waits for the tokens and the error word in pinned memory (every slot pending first)
+  // instead of synchronizing the stream, whose wake-up costs more than a spin on these words
+  for (uint32_t r = 0; r <= R; r++) __atomic_store_n(&host_tok[r], kTokPending, __ATOMIC_RELAXED);
   int rc = QE_OK;
   if (kv->eager) {
     if ((rc = enqueue())) return rc;
@@ -1706,12 +1715,26 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
     }
     HIP_TRY(hipGraphLaunch(vg->exec, m->stream));
   }
-  if (logits_out)
+  if (logits_out) {
     HIP_TRY(hipMemcpyAsync(logits_out, m->blogits, size_t(R) * V * 4, hipMemcpyDeviceToHost, m->stream));
-  // the error word comes back with the results (one synchronization)
-  HIP_TRY(hipMemcpyAsync(m->h_small + 12, m->err, 4, hipMemcpyDeviceToHost, m->stream));
-  HIP_TRY(hipStreamSynchronize(m->stream));
-  if (m->h_small[12] && (rc = check_err(m))) return rc;
+    HIP_TRY(hipStreamSynchronize(m->stream));
+  } else {
+    // spin until every slot is written; a stream that has failed or finished without writing them
+    // ends the wait (checked every 4096 spins)
+    for (uint32_t spins = 1;; spins++) {
+      bool done = true;
+      for (uint32_t r = 0; r <= R; r++) done = done && __atomic_load_n(&host_tok[r], __ATOMIC_ACQUIRE) != kTokPending;
+      if (done) break;
+      if (spins % 4096 == 0 && hipStreamQuery(m->stream) != hipErrorNotReady) {
+        HIP_TRY(hipStreamSynchronize(m->stream));
+        for (uint32_t r = 0; r <= R; r++)
+          if (__atomic_load_n(&host_tok[r], __ATOMIC_ACQUIRE) == kTokPending)
+            return fail(QE_ERR_KERNEL, "verify pass ended without its tokens");
+        break;
+      }
+    }
+  }
+  if (__atomic_load_n(&host_tok[R], __ATOMIC_ACQUIRE) && (rc = check_err(m))) return rc;
   if (tokens) memcpy(tokens, host_tok, size_t(R) * 4);
   kv->len = std::max<uint64_t>(kv->len, pos + R);
   return QE_OK;
