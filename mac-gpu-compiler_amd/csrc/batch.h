@@ -58,6 +58,9 @@ struct MvRowsParams {
   // row j of KV head g is token j / tok_heads, q head g tok_heads + j % tok_heads)
   const float* attn_part = nullptr;
   uint32_t attn_splits = 0, tok_heads = 0;
+  // launch_lm_head_rows only (null: none): each workgroup's greedy candidate of each token row,
+  // cand[v * workgroups + workgroup] (the decode step's kLogits rule)
+  ArgCand* cand = nullptr;
 };
 
 // Weights of the next GEMM that a short launch loads into the L2 of the XCDs that will read them
@@ -140,6 +143,12 @@ uint32_t attn_causal_runs(uint32_t M, uint32_t start, uint32_t n_heads, uint32_t
 // cand: rows * kArgParts candidates of scratch (device memory); rows <= 65535; err_in / err_out
 // (optional): the device error word, copied to err_out once the tokens are written
 constexpr uint32_t kArgParts = 64;
+// tokens[r] = the greedy token of row r from its n_cand candidates cand[r n_cand ..] (written by
+// launch_lm_head_rows) and the first logit of the row (logits [rows][V]); err as launch_row_argmax
+hipError_t launch_cand_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, uint32_t rows, uint32_t V,
+                              uint32_t* tokens, hipStream_t st, const uint32_t* err_in, uint32_t* err_out);
+// workgroups of launch_lm_head_rows for `rows` logit rows (its candidates per token row)
+uint32_t lm_head_rows_workgroups(uint32_t rows);
 hipError_t launch_row_argmax(const float* logits, uint32_t rows, uint32_t V, uint32_t* tokens, ArgCand* cand,
                              hipStream_t st, const uint32_t* err_in = nullptr, uint32_t* err_out = nullptr);
 hipError_t launch_embed_rows(const uint16_t* table, const uint32_t* ids, uint32_t M, uint32_t H, float* x,

@@ -1526,6 +1526,68 @@ __global__ __launch_bounds__(256) void k_lm_head_rows(MvRowsParams p) {
         if (row < p.rows) p.out[size_t(v) * p.ldo + row] = acc[v][r];
       }
   }
+  if (p.cand) {  // each token row's best (value, row) of this workgroup, NaN never (k_matvec kLogits)
+    __shared__ ArgCand cb[NV][4];
+#pragma unroll
+    for (int v = 0; v < NV; v++) {
+      float bv = -INFINITY;
+      uint32_t bi = 0xFFFFFFFFu;
+#pragma unroll
+      for (int r = 0; r < R; r++) {
+        const uint32_t row = row0 + uint32_t(r);
+        if (row < p.rows && !isnan(acc[v][r]) && cand_better(acc[v][r], row, bv, bi)) {
+          bv = acc[v][r];
+          bi = row;
+        }
+      }
+      if (lane == 0) cb[v][wave] = ArgCand{bv, bi};
+    }
+    __syncthreads();
+    if (tid < NV) {
+      ArgCand b = cb[tid][0];
+      for (int w = 1; w < 4; w++)
+        if (cand_better(cb[tid][w].v, cb[tid][w].i, b.v, b.i)) b = cb[tid][w];
+      p.cand[size_t(tid) * gridDim.x + blockIdx.x] = b;
+    }
+  }
+}
+
+// tokens[row] from the row's candidates: the first maximum, NaN never wins, a NaN first logit or
+// no candidate above -inf gives 0 (main.rs:37-42; k_argmax's reduction, one workgroup per row)
+__global__ __launch_bounds__(1024) void k_cand_argmax(const ArgCand* __restrict__ cand, uint32_t n_cand,
+                                                      const float* __restrict__ logits, uint32_t V,
+                                                      uint32_t* __restrict__ tokens, const uint32_t* err_in,
+                                                      uint32_t* err_out) {
+  __shared__ float sv[16];
+  __shared__ uint32_t si[16];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const uint32_t row = blockIdx.x;
+  cand += size_t(row) * n_cand;
+  float bv = -INFINITY;
+  uint32_t bi = 0xFFFFFFFFu;
+  constexpr int U = 16;
+  for (uint32_t base = 0; base < n_cand; base += 1024u * U) {
+    ArgCand c[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) c[u] = cand[min(base + uint32_t(tid) + 1024u * u, n_cand - 1)];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < U; u++)
+      if (cand_better(c[u].v, c[u].i, bv, bi)) { bv = c[u].v; bi = c[u].i; }
+  }
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const uint32_t oi = __shfl_xor(bi, o);
+    if (cand_better(ov, oi, bv, bi)) { bv = ov; bi = oi; }
+  }
+  if (lane == 0) { sv[wave] = bv; si[wave] = bi; }
+  __syncthreads();
+  if (tid == 0) {
+    for (int w = 1; w < 16; w++)
+      if (cand_better(sv[w], si[w], bv, bi)) { bv = sv[w]; bi = si[w]; }
+    tokens[row] = (isnan(logits[size_t(row) * V]) || bi == 0xFFFFFFFFu) ? 0u : bi;
+    if (err_out && row == 0) __atomic_store_n(err_out, *err_in, __ATOMIC_RELAXED);
+  }
 }
 
 template <int TPR, int CPT, int RR, int NV, bool NORM, int EPI>
@@ -1607,6 +1669,15 @@ hipError_t launch_mv_rows_merge(const MvRowsParams& p, hipStream_t st) {
     case 3: return launch_mv_merge_nv<3>(p, st);
     default: return launch_mv_merge_nv<4>(p, st);
   }
+}
+
+uint32_t lm_head_rows_workgroups(uint32_t rows) { return ceil_div(rows, 4u * 4u); }
+
+hipError_t launch_cand_argmax(const ArgCand* cand, uint32_t n_cand, const float* logits, uint32_t rows, uint32_t V,
+                              uint32_t* tokens, hipStream_t st, const uint32_t* err_in, uint32_t* err_out) {
+  if (!cand || !logits || !tokens || n_cand == 0 || rows == 0 || V == 0 || rows > 65535) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_cand_argmax, dim3(rows), dim3(1024), 0, st, cand, n_cand, logits, V, tokens, err_in, err_out);
+  return hipGetLastError();
 }
 
 hipError_t launch_lm_head_rows(const MvRowsParams& p, hipStream_t st) {

@@ -138,6 +138,7 @@ struct qe_model {
   StepState* vstate = nullptr;
   uint32_t* vtokens = nullptr;
   hipEvent_t vstage_ev = nullptr;  // recorded after the copy of the pass's staging words
+  ArgCand* vcand = nullptr;        // the pass's lm_head candidates, kFusedMaxRows x lm_head workgroups
   uint32_t* place_word = nullptr;
   // extra workgroups per XCD of each attention block that load the layer's MLP weights into the
   // L2 of their XCD (QE_FUSED_PF_ATTN), and of each MLP block that load the next layer's q|k|v
@@ -477,6 +478,7 @@ int qe_model_load(const char* path, qe_model** out) {
                s_sync = stake(qe::kFusedSyncWords * 4), s_place = stake(qe::kFusedXcds * qe::kFusedSlots * 4),
                s_fqkv = stake(FR * qe::kFusedQkvRowPairs * 8), s_fh = stake(FR * qe::kFusedHPairs * 8),
                s_vstate = stake(sizeof(StepState) + FR * 4),
+               s_vcand = stake(FR * qe::lm_head_rows_workgroups(uint32_t(V)) * sizeof(ArgCand)),
                s_pxa = stake(qe::kFusedXcds * H * 8), s_pxm = stake(qe::kFusedXcds * H * 8),
                s_ppa = stake(qe::kFusedXcds * H * 8), s_ppm = stake(qe::kFusedXcds * H * 8), s_pgen = stake(256);
   static_assert(qe::kFusedPartPairs * 8 <= size_t(qe::kFusedKv) * qe::kAttnMaxWideSplits * 2 * qe::kPartStride * 4,
@@ -501,6 +503,7 @@ int qe_model_load(const char* path, qe_model** out) {
   m->fh = reinterpret_cast<uint2*>(m->scratch + s_fh);
   m->vstate = reinterpret_cast<StepState*>(m->scratch + s_vstate);
   m->vtokens = reinterpret_cast<uint32_t*>(m->scratch + s_vstate + sizeof(StepState));
+  m->vcand = reinterpret_cast<ArgCand*>(m->scratch + s_vcand);
   m->pxa = reinterpret_cast<uint2*>(m->scratch + s_pxa);
   m->pxm = reinterpret_cast<uint2*>(m->scratch + s_pxm);
   m->ppa = reinterpret_cast<uint2*>(m->scratch + s_ppa);
@@ -1674,11 +1677,14 @@ int verify_fused(qe_model* m, const uint32_t* ids, uint32_t R, uint64_t pos, qe_
     kv->step_splits = ks;
     kv->step_run = kr;
     if (rc) return rc;
-    // (x comes normalized from the final reduce)
-    const qe::MvRowsParams r{m->lm_head, m->x, nullptr, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
-                             uint32_t(V), c.rms_norm_eps};
+    // (x comes normalized from the final reduce); each workgroup's candidates, then one
+    // reduction per row
+    qe::MvRowsParams r{m->lm_head, m->x, nullptr, m->blogits, R, uint32_t(V), uint32_t(c.hidden_size),
+                       uint32_t(V), c.rms_norm_eps};
+    r.cand = m->vcand;
     HIP_TRY(qe::launch_lm_head_rows(r, m->stream));
-    HIP_TRY(qe::launch_row_argmax(m->blogits, R, uint32_t(V), host_tok, m->bcand, m->stream, m->err, host_tok + R));
+    HIP_TRY(qe::launch_cand_argmax(m->vcand, qe::lm_head_rows_workgroups(uint32_t(V)), m->blogits, R, uint32_t(V),
+                                   host_tok, m->stream, m->err, host_tok + R));
     return QE_OK;
   };
   // the host waits for the tokens and the error word in pinned memory (every slot pending first)
