@@ -450,8 +450,9 @@ def other_configs(torch, qe, model, cfg, ceiling: float, args) -> dict:
     """Short runs of the other workloads, so that one default `bench.py` run also measures them
     (outside the timed decode): the isolated matvec and attention sweeps (100 launches per shape
     instead of 1000), the 4096-step decode with an f32 cache (one untimed decode that captures its
-    step graphs, then one timed), its tokens against the oracle's committed run, and the
-    2048-token chunked prefill with the k = 4 verify."""
+    step graphs, then one timed), its tokens against the oracle's committed run, the
+    2048-token chunked prefill with the k = 4 verify, and prompt-lookup decode (plain against
+    k_max = 1, and one draft at the emulated text acceptance rates)."""
     import numpy as np
     out = {}
     t0 = time.time()
@@ -496,6 +497,13 @@ def other_configs(torch, qe, model, cfg, ceiling: float, args) -> dict:
         "parity_vs_oracle_fixture": {"compared": n, "first_divergence": next((i for i in range(n) if got[i] != ref[i]), None)}
         if ref else None}
     del cache
+    # prompt-lookup decode (f3): plain vs k_max = 1 (two-row verify passes), and the emulated
+    # text acceptance rates with one draft, the emitted tokens checked against plain decode
+    lk = lookup_bench(qe, model, cfg, args)
+    out["lookup"] = {"plain_tok_s": lk["plain_tok_s"],
+                     "k1": {k: lk["k1"][k] for k in ("tok_s", "speedup", "same_tokens", "tokens_per_pass")},
+                     "emulated_text_acceptance_k1": {k: {"speedup": v["speedup"], "ms_per_pass": v["ms_per_pass"]}
+                                                     for k, v in lk["emulated_text_acceptance"].items() if "_k1" in k}}
     out["seconds"] = round(time.time() - t0, 1)
     return out
 
